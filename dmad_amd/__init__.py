@@ -1,0 +1,12 @@
+"""dmad_amd: MI355X (gfx950) flash-attention JVP path of DMAD / rCM.
+
+Public surface (mirrors the reference module train/wan/rcm/utils/flash_attention_jvp_triton.py
+and the attention helpers of train/wan/rcm/utils/jvp_helper.py):
+
+* ``_attention`` / ``attention``    -- autograd op (q, k, v, tq, tk, tv, sm_scale, magi_mask) -> (o, to)
+* ``torch_attention_op_withT``      -- BSHD (x, x_dot) pairs in, (o, o_dot.detach()) out
+* ``torch_attention_op``            -- plain BSHD attention on the same kernels
+* ``plain_attention``               -- plain BHSD attention with backward
+"""
+from .jvp_attention import _attention, attention, plain_attention, set_reference_backward  # noqa: F401
+from .jvp_helper import torch_attention_op, torch_attention_op_withT  # noqa: F401

@@ -1,0 +1,115 @@
+"""ctypes binding of ``libdmad_attn.so`` (C ABI declared in ``include/dmad_attn.h``).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime torch
+already loaded (both name it ``libamdhip64.so.7``); streams and device
+pointers then mean the same thing on both sides. There is no fallback: if the
+library is missing, every GPU entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the HIP runtime the library must share)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdmad_attn.so")
+
+DMAD_OK = 0
+DMAD_ERR_INVALID = 1
+DMAD_ERR_UNSUPPORTED = 2
+DMAD_ERR_WORKSPACE = 3
+DMAD_ERR_HIP = 4
+
+DMAD_BF16 = 0
+DMAD_F16 = 1
+
+DMAD_FWD_PLAIN = 0
+DMAD_FWD_JVP = 1
+DMAD_FWD_JVP_KV_TANGENT_ZERO = 2
+
+# Every function the header declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I64P = ctypes.POINTER(ctypes.c_int64)
+_FP = ctypes.POINTER(ctypes.c_float)
+_SZ = ctypes.c_size_t
+_SZP = ctypes.POINTER(ctypes.c_size_t)
+_INT = ctypes.c_int
+_F = ctypes.c_float
+
+SIGNATURES = {
+    "dmad_abi_version": (_INT, []),
+    "dmad_last_error": (ctypes.c_char_p, []),
+    "dmad_attn_fwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _SZP]),
+    "dmad_attn_jvp_fwd": (_INT, [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _I64,
+                                 _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
+                                 _P, _P, _I64P, _P, _P, _F, _P, _SZ, _P]),
+    "dmad_attn_fwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
+                             _I64P, _I64P, _I64P, _P, _I64P, _P, _F, _P, _SZ, _P]),
+    "dmad_attn_bwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _SZP]),
+    "dmad_attn_jvp_bwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64,
+                                 _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
+                                 _P, _P, _I64P, _P, _P, _P, _P, _I64P,
+                                 _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
+                                 _F, _P, _SZ, _P]),
+}
+
+
+class DmadError(RuntimeError):
+    """A non-zero status from the C ABI."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[dmad status {code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built: the gfx950 HIP kernels are required "
+                "(build with `python -m dmad_amd.build`)"
+            )
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != DMAD_OK:
+        msg = lib().dmad_last_error().decode(errors="replace")
+        if code == DMAD_ERR_INVALID:
+            raise ValueError(f"[dmad status {code}] {msg}")
+        if code == DMAD_ERR_UNSUPPORTED:
+            raise NotImplementedError(f"[dmad status {code}] {msg}")
+        raise DmadError(code, msg)
+
+
+def strides4(t: torch.Tensor):
+    return (ctypes.c_int64 * 4)(*t.stride())
+
+
+def ptr(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def stream_ptr(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return DMAD_BF16
+    if dtype == torch.float16:
+        return DMAD_F16
+    raise NotImplementedError(
+        f"dtype {dtype} is not supported by the gfx950 kernels (bfloat16 or float16 operands)"
+    )

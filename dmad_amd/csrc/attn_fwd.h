@@ -1,0 +1,340 @@
+// Forward attention kernels for gfx950: plain (O, LSE) and forward+JVP
+// (O, tangent output, LSE, mu) in a single online-softmax pass.
+//
+// Semantics follow the reference Triton kernel `_attn_fwd`
+// (train/wan/rcm/utils/flash_attention_jvp_triton.py:107-232):
+//   S  = s * Q K^T                     (log2 domain: qk = S * log2(e))
+//   P~ = exp2(qk - m)                  running max m per query row
+//   Sd = s * (Qd K^T + Q Kd^T)         tangent scores (natural domain)
+//   H~ = P~ * Sd,  r = rowsum(H~)
+//   O~ += bf16(P~) V,  C~ += bf16(P~) Vd + bf16(H~) V     (fp32 accumulators)
+//   O = O~/l,  Od = C~/l - (r/l) O,  LSE = (m + log2 l) ln 2,  mu = r/l
+// The reference keeps A~ = P~ Vd and B~ = H~ V apart and adds them in its
+// epilogue (:216-223); they receive identical rescales, so one accumulator
+// C~ = A~ + B~ holds the same sum.
+//
+// Work decomposition (one workgroup = 4 waves = 128 query rows of one head):
+//   * wave w owns query rows [32w, 32w+32); its Q and Qd slices stay in
+//     registers as the B operand of S^T = K Q^T (lane l <-> query l%32);
+//   * K, Kd tiles [BN keys][D] and V^T, Vd^T tiles [D][BN keys] are streamed
+//     through a double-buffered LDS ring by buffer->LDS DMA (16 B per lane);
+//   * the C layout of S^T (lane <-> query, 16 key values per lane) feeds the
+//     B operand of O^T = V^T P^T directly, because the K rows of every 32-key
+//     block are read in perm32 order (rows 8..15 of a lane's values then map
+//     to 8 consecutive keys);
+//   * O~^T and C~^T accumulate in registers with lane <-> query, so the
+//     per-row rescale is a per-lane scalar multiply.
+// V and Vd are read from a pre-transposed copy ([BH][DVP][LKP], zero padded),
+// produced by transpose_pad_kernel; that costs one extra HBM pass over V and
+// Vd, far below the O(L^2) work of the pass itself.
+#pragma once
+#include "common.h"
+
+namespace dmad {
+
+enum FwdMode : int { kFwdPlain = 0, kFwdJvp = 1, kFwdJvpQOnly = 2 };
+
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* tq;
+  const void* tk;
+  const void* vt;   // V^T  [B*H][DVP][LKP]
+  const void* tvt;  // Vd^T [B*H][DVP][LKP]
+  void* o;
+  void* to;
+  float* lse;  // [B*H][Lq]
+  float* mu;   // [B*H][Lq]
+  int64_t q_sb, q_sh, q_sl;  // element strides, shared by Q and Qd
+  int64_t k_sb, k_sh, k_sl;  // shared by K and Kd
+  int64_t o_sb, o_sh, o_sl;  // shared by O and Od
+  int B, H, Lq, Lk, LKP;
+  float scale;       // softmax scale s
+  float scale_log2;  // s * log2(e)
+};
+
+template <int DQK, int DV, int MODE>
+struct FwdCfg {
+  static constexpr int NW = 4;
+  static constexpr int BM = 32 * NW;
+  static constexpr int DVP = DV < 32 ? 32 : DV;
+  static constexpr int BN = (DQK > 128 || DVP > 128) ? 32 : 64;
+  static constexpr int NB = BN / 32;  // 32-key blocks per tile
+  static constexpr int KS = DQK / 16;  // 16-wide k slices of Q K^T
+  static constexpr int DB = DVP / 32;  // 32-row blocks of O^T
+  static constexpr int CK = DQK / 8;   // 16-byte chunks per K row
+  static constexpr int CV = BN / 8;    // 16-byte chunks per V^T row
+  static constexpr bool JVP = MODE != kFwdPlain;
+  static constexpr bool KVT = MODE == kFwdJvp;
+  static constexpr int K_BYTES = BN * DQK * 2;
+  static constexpr int V_BYTES = DVP * BN * 2;
+  static constexpr int OFF_K = 0;
+  static constexpr int OFF_V = K_BYTES;
+  static constexpr int OFF_KT = K_BYTES + V_BYTES;
+  static constexpr int OFF_VT = 2 * K_BYTES + V_BYTES;
+  static constexpr int STAGE = (KVT ? 2 : 1) * (K_BYTES + V_BYTES);
+  static constexpr int NKI = BN * CK / 64;   // wave-wide 1 KiB loads per K tile
+  static constexpr int NVI = DVP * CV / 64;  // ... per V^T tile
+  static constexpr int KPW = (NKI + NW - 1) / NW;
+  static constexpr int VPW = (NVI + NW - 1) / NW;
+  static constexpr int LKP_ALIGN = 64;  // V^T rows are padded to this many keys
+};
+
+template <typename T, int DQK, int DV, int MODE>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(FwdParams p) {
+  using C = FwdCfg<DQK, DV, MODE>;
+  constexpr int BN = C::BN, NB = C::NB, KS = C::KS, DB = C::DB, CK = C::CK, CV = C::CV;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  const char* qbase = (const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2;
+  const char* kbase = (const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2;
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + DQK) * 2);
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + DQK) * 2);
+  const uint32_t vt_bytes = (uint32_t)((int64_t)C::DVP * p.LKP * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, q_bytes);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.vt + (int64_t)bh * vt_bytes, vt_bytes);
+  __amdgpu_buffer_rsrc_t rtq = rq, rtk = rk, rtv = rv;
+  if constexpr (C::JVP) rtq = make_rsrc((const char*)p.tq + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  if constexpr (C::KVT) {
+    rtk = make_rsrc((const char*)p.tk + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+    rtv = make_rsrc((const char*)p.tvt + (int64_t)bh * vt_bytes, vt_bytes);
+  }
+
+  // ---- Q (and Qd) slices in registers: B operand of S^T = K Q^T
+  const int qrow = qt * C::BM + wave * 32 + col;
+  const uint32_t qoff = (uint32_t)((int64_t)qrow * p.q_sl * 2) + half * 16;
+  i32x4_t qr[KS], tqr[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qr[s] = buf_load16(rq, qoff + s * 32);
+    if constexpr (C::JVP) tqr[s] = buf_load16(rtq, qoff + s * 32);
+  }
+
+  // ---- per-lane DMA offsets (tile independent)
+  uint32_t koff[C::KPW], voff[C::VPW];
+#pragma unroll
+  for (int j = 0; j < C::KPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CK, phys = pch % CK;
+    const int logical = phys ^ swz<CK>(perm32(row & 31) & 15);
+    koff[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < C::VPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int d = pch / CV, phys = pch % CV;
+    const int logical = phys ^ swz<CV>(d & 15);
+    voff[j] = (uint32_t)(d * p.LKP * 2) + logical * 16;
+  }
+  const uint32_t k_tile_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
+
+  auto issue_tile = [&](int kt, int stage) {
+    char* st = smem + stage * C::STAGE;
+    const uint32_t ks = (uint32_t)kt * k_tile_step;
+    const uint32_t vs = (uint32_t)kt * BN * 2;
+#pragma unroll
+    for (int j = 0; j < C::KPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NKI) {
+        buf_load16_lds(rk, st + C::OFF_K + i * 1024, koff[j], ks);
+        if constexpr (C::KVT) buf_load16_lds(rtk, st + C::OFF_KT + i * 1024, koff[j], ks);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::VPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NVI) {
+        buf_load16_lds(rv, st + C::OFF_V + i * 1024, voff[j], vs);
+        if constexpr (C::KVT) buf_load16_lds(rtv, st + C::OFF_VT + i * 1024, voff[j], vs);
+      }
+    }
+  };
+
+  // ---- LDS read offsets (tile independent)
+  const int kswz = swz<CK>(col & 15), vswz = swz<CV>(col & 15);
+  const int krow_off = perm32(col) * CK * 16;
+  const int vrow_off = col * CV * 16;
+
+  f32x16_t oacc[DB], cacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      oacc[d][v] = 0.f;
+      cacc[d][v] = 0.f;
+    }
+  }
+  float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
+
+  const int ntiles = (p.Lk + BN - 1) / BN;
+  issue_tile(0, 0);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < ntiles) issue_tile(kt + 1, (kt + 1) & 1);
+    const char* st = smem + (kt & 1) * C::STAGE;
+
+    // ---- S^T and Sd^T for BN keys x 32 queries
+    f32x16_t sacc[NB], tacc[NB];
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        sacc[kb][v] = 0.f;
+        tacc[kb][v] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) {
+        const int off = kb * 32 * CK * 16 + krow_off + (((2 * s + half) ^ kswz) << 4);
+        const i32x4_t ak = *(const i32x4_t*)(st + C::OFF_K + off);
+        sacc[kb] = mfma32(ak, qr[s], sacc[kb], T());
+        if constexpr (C::JVP) tacc[kb] = mfma32(ak, tqr[s], tacc[kb], T());
+        if constexpr (C::KVT) {
+          const i32x4_t akt = *(const i32x4_t*)(st + C::OFF_KT + off);
+          tacc[kb] = mfma32(akt, qr[s], tacc[kb], T());
+        }
+      }
+    }
+
+    // ---- tail keys -> -inf
+    if ((kt + 1) * BN > p.Lk) {
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int j = v >> 2;
+          const int key = kt * BN + kb * 32 + ((j >> 1) << 4) + (half << 3) + ((j & 1) << 2) + (v & 3);
+          if (key >= p.Lk) sacc[kb][v] = -__builtin_inff();
+        }
+      }
+    }
+
+    // ---- online softmax (log2 domain); both halves of the wave share m
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[kb][v]);
+    }
+    mx = fmaxf(mx, other_half(mx));
+    const float m_new = fmaxf(m_i, mx * p.scale_log2);
+    const float alpha = fast_exp2(m_i - m_new);
+    const float neg_m = -m_new;
+    float ls = 0.f, rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float pv = fast_exp2(fmaf(sacc[kb][v], p.scale_log2, neg_m));
+        sacc[kb][v] = pv;
+        ls += pv;
+        if constexpr (C::JVP) {
+          const float hv = pv * (tacc[kb][v] * p.scale);
+          tacc[kb][v] = hv;
+          rs += hv;
+        }
+      }
+    }
+    l_i = l_i * alpha + ls;
+    m_i = m_new;
+    if constexpr (C::JVP) r_i = r_i * alpha + rs;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        oacc[d][v] *= alpha;
+        if constexpr (C::JVP) cacc[d][v] *= alpha;
+      }
+    }
+
+    // ---- O~^T += V^T P^T ; C~^T += Vd^T P^T + V^T H^T
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        i32x4_t pb, hb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pb[e] = (int)Elem<T>::pack2(sacc[kb][8 * t + 2 * e], sacc[kb][8 * t + 2 * e + 1]);
+          if constexpr (C::JVP) hb[e] = (int)Elem<T>::pack2(tacc[kb][8 * t + 2 * e], tacc[kb][8 * t + 2 * e + 1]);
+        }
+        const int vch = ((kb * 4 + 2 * t + half) ^ vswz) << 4;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+          const int off = d * 32 * CV * 16 + vrow_off + vch;
+          const i32x4_t av = *(const i32x4_t*)(st + C::OFF_V + off);
+          oacc[d] = mfma32(av, pb, oacc[d], T());
+          if constexpr (C::KVT) {
+            const i32x4_t avt = *(const i32x4_t*)(st + C::OFF_VT + off);
+            cacc[d] = mfma32(avt, pb, cacc[d], T());
+          }
+          if constexpr (C::JVP) cacc[d] = mfma32(av, hb, cacc[d], T());
+        }
+      }
+    }
+  }
+
+  // ---- epilogue
+  const float l = l_i + other_half(l_i);
+  const float inv_l = 1.0f / l;
+  float mu = 0.f;
+  if constexpr (C::JVP) mu = (r_i + other_half(r_i)) * inv_l;
+
+  const int64_t obase = b * p.o_sb + h * p.o_sh;
+  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + DV) * 2);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
+  __amdgpu_buffer_rsrc_t rto = ro;
+  if constexpr (C::JVP) rto = make_rsrc((char*)p.to + obase * 2, o_bytes);
+  const uint32_t orow = (uint32_t)((int64_t)qrow * p.o_sl * 2);
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int dc = d * 32 + 8 * j + 4 * half;
+      if (DV >= 32 || dc < DV) {
+        float ov[4], tv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          ov[r] = oacc[d][4 * j + r] * inv_l;
+          if constexpr (C::JVP) tv[r] = cacc[d][4 * j + r] * inv_l - mu * ov[r];
+        }
+        const uint32_t off = orow + dc * 2;
+        u32x2_t w = {Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])};
+        buf_store8(ro, w, off);
+        if constexpr (C::JVP) {
+          u32x2_t wt = {Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])};
+          buf_store8(rto, wt, off);
+        }
+      }
+    }
+  }
+  if (half == 0 && qrow < p.Lq) {
+    const int64_t si = (int64_t)bh * p.Lq + qrow;
+    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    if constexpr (C::JVP) p.mu[si] = mu;
+  }
+}
+
+// Transpose X [B,H,L,D] (element strides sb, sh, sl; unit stride in D) ->
+// Y [B*H][DP][LP] contiguous, zero where l >= L or d >= D.
+struct TransposeParams {
+  const void* x;
+  void* y;
+  int64_t sb, sh, sl;
+  int H, L, D, LP, DP;
+};
+
+}  // namespace dmad

@@ -1,0 +1,133 @@
+// Shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Everything here is written for one target: wave64, MFMA 32x32x16 on bf16/fp16
+// operands with fp32 accumulation, buffer resources with hardware range checks,
+// and direct buffer->LDS loads of 16 bytes per lane.
+//
+// MFMA 32x32x16 register layouts (checked on the device with a lane probe):
+//   A (M x K = 32 x 16): lane l holds row l%32, k = 8*(l/32) + e, e = 0..7
+//   B (K x N = 16 x 32): lane l holds col l%32, k = 8*(l/32) + e
+//   C (M x N = 32 x 32): lane l holds col l%32, rows 8*(v/4) + 4*(l/32) + v%4, v = 0..15
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dmad {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kWave = 64;
+constexpr unsigned kRsrcWord3 = 0x00020000u;  // raw buffer, gfx9 family
+
+// ---------------------------------------------------------------- buffers
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+// 16-byte load; bytes at or beyond the range of the resource read as zero.
+__device__ __forceinline__ i32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+}
+
+// 16 bytes per lane straight into LDS: lane i lands at lds_base + 16*i.
+__device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff,
+                                               uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_base, 16, (int)voff, (int)soff, 0, 0);
+}
+
+__device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, u32x2_t v, uint32_t voff) {
+  i32x2_t w = {(int)v[0], (int)v[1]};
+  __builtin_amdgcn_raw_buffer_store_b64(w, r, (int)voff, 0, 0);
+}
+
+// vmcnt(0): wait for this wave's outstanding vector-memory operations
+// (including buffer->LDS transfers). expcnt and lgkmcnt are left unconstrained.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ---------------------------------------------------------------- element types
+template <typename T> struct Elem;
+template <> struct Elem<__bf16> {
+  using vec8 = bf16x8_t;
+  // two floats -> two bf16 (round to nearest even), packed low|high
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    bf16x2_t r;
+    r[0] = (__bf16)a;
+    r[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, r);
+  }
+  __device__ __forceinline__ static float to_f32(uint16_t bits) {
+    return __uint_as_float(((uint32_t)bits) << 16);
+  }
+};
+template <> struct Elem<_Float16> {
+  using vec8 = f16x8_t;
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    f16x2_t r;
+    r[0] = (_Float16)a;
+    r[1] = (_Float16)b;
+    return __builtin_bit_cast(uint32_t, r);
+  }
+  __device__ __forceinline__ static float to_f32(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+  }
+};
+
+__device__ __forceinline__ f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c, __bf16) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c, _Float16) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- lane helpers
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// Value held by lane l^32 (the other half of the wave), via v_permlane32_swap.
+__device__ __forceinline__ float other_half(float x) {
+  uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// Row permutation inside a 32-row MFMA block: swap bits 2 and 3.
+// Feeding A-operand row i from source row perm32(i) makes the C-layout values
+// (v = 8..15 or 0..7 of one lane) cover 8 consecutive source rows, so the C
+// tile can be reused directly as the k-operand of the next MFMA.
+__device__ __forceinline__ int perm32(int i) {
+  return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+
+// XOR swizzle of the 16-byte chunk index for an LDS tile whose rows hold C
+// chunks; x is the row index modulo 16 (after any row permutation). Chosen so
+// that 16 lanes reading rows x = 0..15 at one logical chunk hit 16 distinct
+// 16-byte slots of a 256-byte bank window (and 8 lanes hit 8 distinct slots
+// of a 128-byte window).
+template <int C>
+__device__ __forceinline__ int swz(int x) {
+  if constexpr (C >= 16) return x & 15;
+  else if constexpr (C == 8) return ((x >> 1) & 7) ^ ((x & 1) << 2);
+  else return (x >> 1) & (C - 1);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup -> work-item remap so that each XCD (blocks are dealt to the 8
+// XCDs round-robin by block id) processes a contiguous range of work items:
+// neighbouring query tiles of one head then run on one XCD and share its L2.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int per = total >> 3, rem = total & 7;
+  return (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+}  // namespace dmad

@@ -1,0 +1,48 @@
+// Instantiates the forward kernels for one (element type, Dqk) pair:
+// compiled once per pair with -DDMAD_T=<0 bf16 | 1 f16> -DDMAD_D=<Dqk>.
+#include "launch.h"
+
+#ifndef DMAD_T
+#error "DMAD_T must be defined"
+#endif
+#ifndef DMAD_D
+#error "DMAD_D must be defined"
+#endif
+
+namespace dmad {
+
+#if DMAD_T == 0
+using Elt = __bf16;
+#else
+using Elt = _Float16;
+#endif
+
+template <typename T, int DQK, int DV, int MODE>
+static hipError_t fwd_launch(const FwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_fwd_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, int DQK, int DV>
+static FwdLaunchFn fwd_mode(int mode) {
+  switch (mode) {
+    case kFwdPlain: return &fwd_launch<T, DQK, DV, kFwdPlain>;
+    case kFwdJvp: return &fwd_launch<T, DQK, DV, kFwdJvp>;
+    case kFwdJvpQOnly: return &fwd_launch<T, DQK, DV, kFwdJvpQOnly>;
+    default: return nullptr;
+  }
+}
+
+template <>
+FwdLaunchFn fwd_select<Elt, DMAD_D>(int dv, int mode) {
+  switch (dv) {
+    case 16: return fwd_mode<Elt, DMAD_D, 16>(mode);
+    case 32: return fwd_mode<Elt, DMAD_D, 32>(mode);
+    case 64: return fwd_mode<Elt, DMAD_D, 64>(mode);
+    case 128: return fwd_mode<Elt, DMAD_D, 128>(mode);
+    case 256: return fwd_mode<Elt, DMAD_D, 256>(mode);
+    default: return nullptr;
+  }
+}
+
+}  // namespace dmad

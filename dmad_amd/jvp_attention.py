@@ -1,0 +1,261 @@
+"""Flash-attention JVP op for gfx950: drop-in for the reference ``_attention``.
+
+Reference: ``train/wan/rcm/utils/flash_attention_jvp_triton.py:450-582``.
+``_attention.apply(q, k, v, tq, tk, tv, sm_scale=None, magi_mask=None)`` returns
+``(o, to)``: the attention output and its directional derivative along the
+tangents ``(tq, tk, tv)``. Tensors are logical ``[B, H, L, D]`` with any
+strides (the Wan callers pass ``[B, L, H, D]`` storage viewed as BHSD).
+
+Device work is three hand-written HIP kernels reached through the C ABI of
+``libdmad_attn.so`` (``include/dmad_attn.h``); this module only checks
+arguments, allocates outputs with the torch caching allocator and launches on
+torch's current stream. There is no CPU or PyTorch fallback.
+
+Differences from the reference, all additive:
+  * ``tk``/``tv`` may be ``None`` (tangents of K and V known to be zero, as in
+    Wan cross-attention): the forward then skips the two GEMMs they feed.
+  * backward: when the cotangent of ``to`` is given, the gradients include its
+    contribution and, if the tangents require grad, gradients for them
+    (the reference discards that cotangent, :535, and returns None for the
+    tangents, :579). Without it the gradients are the reference's dO-only
+    ones. ``set_reference_backward(True)`` restores the reference behaviour
+    exactly in both cases.
+  * ``magi_mask`` (block-sparse masks, :504-531) raises NotImplementedError.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+_REFERENCE_BACKWARD = False
+
+
+def set_reference_backward(flag: bool) -> None:
+    """Ignore the cotangent of the tangent output in backward, as the reference does."""
+    global _REFERENCE_BACKWARD
+    _REFERENCE_BACKWARD = bool(flag)
+
+
+_HEAD_DIMS = {16, 32, 64, 128, 256}
+
+
+def _kernel_ready(t: torch.Tensor) -> bool:
+    """Unit inner stride, 16-byte aligned rows (what the kernels load from)."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        return False
+    return all(s % 8 == 0 for s in t.stride()[:-1])
+
+
+def _prep(*ts):
+    """Copy operands whose layout the kernels cannot read; tangents stay
+    stride-identical to their primals because both go through the same rule."""
+    return tuple(None if t is None else (t if _kernel_ready(t) else t.contiguous()) for t in ts)
+
+
+def _pair(x, tx):
+    """(primal, tangent) in a layout the kernels read, with equal strides."""
+    if tx is None:
+        return (x if _kernel_ready(x) else x.contiguous()), None
+    if x.stride() == tx.stride() and _kernel_ready(x) and _kernel_ready(tx):
+        return x, tx
+    return x.contiguous(), tx.contiguous()
+
+
+def _check_device(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "dmad_amd attention runs on the GPU only (HIP kernels); got a tensor on " + str(t.device)
+            )
+
+
+def jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale, need_mu=True):
+    """Launch the forward(+JVP) kernel; returns (o, to, lse, mu).
+
+    ``tq is None`` selects the plain forward (to and mu are None).
+    """
+    B, H, Lq, Dqk = q.shape
+    Lk, Dv = v.shape[-2], v.shape[-1]
+    _check_device(q, k, v, tq, tk, tv)
+    code = nat.dtype_code(q.dtype)
+    if tq is None:
+        mode = nat.DMAD_FWD_PLAIN
+    elif tk is None and tv is None:
+        mode = nat.DMAD_FWD_JVP_KV_TANGENT_ZERO
+    else:
+        if tk is None:
+            tk = torch.zeros_like(k)
+        if tv is None:
+            tv = torch.zeros_like(v)
+        mode = nat.DMAD_FWD_JVP
+    q, tq = _pair(q, tq)
+    k, tk = _pair(k, tk)
+    v, tv = _pair(v, tv)
+    dev = q.device
+    o = torch.empty((B, H, Lq, Dv), device=dev, dtype=q.dtype)
+    to = torch.empty_like(o) if tq is not None else None
+    lse = torch.empty((B, H, Lq), device=dev, dtype=torch.float32)
+    mu = torch.empty_like(lse) if tq is not None else None
+    lib = nat.lib()
+    ws_bytes = nat.ctypes.c_size_t(0)
+    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dv, nat.ctypes.byref(ws_bytes)))
+    ws = torch.empty(max(int(ws_bytes.value), 1), device=dev, dtype=torch.uint8)
+    nat.check(
+        lib.dmad_attn_jvp_fwd(
+            code, mode, B, H, Lq, Lk, Dqk, Dv,
+            nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(tq), nat.ptr(tk), nat.ptr(tv),
+            nat.strides4(q), nat.strides4(k), nat.strides4(v),
+            nat.ptr(o), nat.ptr(to), nat.strides4(o), nat.ptr(lse), nat.ptr(mu),
+            float(sm_scale), nat.ptr(ws), ws.numel(), nat.stream_ptr(dev),
+        )
+    )
+    return o, to, lse, mu
+
+
+def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_scale, want_tangent_grads):
+    """Launch the backward kernels; returns (dq, dk, dv, dtq, dtk, dtv)."""
+    B, H, Lq, D = q.shape
+    Lk = k.shape[-2]
+    _check_device(q, k, v, o, dout)
+    code = nat.dtype_code(q.dtype)
+    full = dto is not None
+    if full:
+        if tk is None:
+            tk = torch.zeros_like(k)
+        if tv is None:
+            tv = torch.zeros_like(v)
+        q, tq = _pair(q, tq)
+        k, tk = _pair(k, tk)
+        v, tv = _pair(v, tv)
+        o, to = _pair(o, to)
+        dout = torch.zeros_like(o) if dout is None else dout
+        dout, dto = _pair(dout, dto)
+    else:
+        q, k, v, o, dout = _prep(q, k, v, o, dout)
+        tq = tk = tv = to = None
+    dq = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    dk = torch.empty(k.shape, device=q.device, dtype=q.dtype)
+    dv = torch.empty(v.shape, device=q.device, dtype=q.dtype)
+    tgrads = full and want_tangent_grads
+    dtq = torch.empty_like(dq) if tgrads else None
+    dtk = torch.empty_like(dk) if tgrads else None
+    dtv = torch.empty_like(dv) if tgrads else None
+    lib = nat.lib()
+    ws_bytes = nat.ctypes.c_size_t(0)
+    nat.check(lib.dmad_attn_bwd_workspace_bytes(int(full), B, H, Lq, Lk, D, nat.ctypes.byref(ws_bytes)))
+    ws = torch.empty(max(int(ws_bytes.value), 1), device=q.device, dtype=torch.uint8)
+    nat.check(
+        lib.dmad_attn_jvp_bwd(
+            code, B, H, Lq, Lk, D,
+            nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(tq), nat.ptr(tk), nat.ptr(tv),
+            nat.strides4(q), nat.strides4(k), nat.strides4(v),
+            nat.ptr(o), nat.ptr(to), nat.strides4(o), nat.ptr(lse), nat.ptr(mu),
+            nat.ptr(dout), nat.ptr(dto), nat.strides4(dout),
+            nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dtq), nat.ptr(dtk), nat.ptr(dtv),
+            nat.strides4(dq), nat.strides4(dk), nat.strides4(dv),
+            float(sm_scale), nat.ptr(ws), ws.numel(), nat.stream_ptr(q.device),
+        )
+    )
+    return dq, dk, dv, dtq, dtk, dtv
+
+
+class _attention(torch.autograd.Function):
+    """
+    Arguments:
+        q, tq: (batch_size, nheads, seqlen_q, d_qk)
+        k, tk: (batch_size, nheads, seqlen_kv, d_qk)
+        v, tv: (batch_size, nheads, seqlen_kv, d_v)
+    Returns:
+        o, to: (batch_size, nheads, seqlen_q, d_v)
+
+    Backward is only supported when d_qk=d_v.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, tq, tk, tv, sm_scale=None, magi_mask=None):
+        # argument contract of flash_attention_jvp_triton.py:464-476
+        is_grad = any(x is not None and x.requires_grad for x in (q, k, v))
+        assert q.shape[:-2] == k.shape[:-2] and k.shape[:-2] == v.shape[:-2]
+        assert k.shape[-2] == v.shape[-2] and q.shape[-1] == k.shape[-1]
+        HEAD_DIM_QK, HEAD_DIM_V = q.shape[-1], v.shape[-1]
+        assert HEAD_DIM_QK in _HEAD_DIMS
+        assert HEAD_DIM_V in _HEAD_DIMS
+        assert tq.shape == q.shape
+        assert tk is None or tk.shape == k.shape
+        assert tv is None or tv.shape == v.shape
+        assert tq.stride() == q.stride()
+        assert tk is None or tk.stride() == k.stride()
+        assert tv is None or tv.stride() == v.stride()
+        if q.dim() != 4:
+            raise ValueError("expected 4-d [B, H, L, D] tensors")
+        if sm_scale is None:
+            sm_scale = HEAD_DIM_QK ** (-0.5)
+        if magi_mask is not None:
+            if is_grad:
+                raise RuntimeError("Backward with MagiMask is not supported.")
+            raise NotImplementedError("block-sparse (MagiMask) JVP attention is not implemented by dmad_amd")
+        tangent_grad = any(x is not None and x.requires_grad for x in (tq, tk, tv))
+        o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale)
+        if is_grad or tangent_grad:
+            ctx.save_for_backward(q, k, v, tq, tk, tv, o, to, lse, mu)
+            ctx.sm_scale = sm_scale
+            ctx.tangent_grad = tangent_grad
+        return o, to
+
+    @staticmethod
+    def backward(ctx, dout, dto):
+        q, k, v, tq, tk, tv, o, to, lse, mu = ctx.saved_tensors
+        assert q.shape[-1] == k.shape[-1] and k.shape[-1] == v.shape[-1], (
+            "Backward not supported with different headdim."
+        )
+        if _REFERENCE_BACKWARD:
+            dto = None
+        if dout is None and dto is None:
+            return (None,) * 8
+        if dout is None:
+            dout = torch.zeros_like(o)
+        dq, dk, dv, dtq, dtk, dtv = jvp_attention_backward(
+            q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, ctx.sm_scale, ctx.tangent_grad
+        )
+        if dtk is not None and tk is None:
+            dtk = None
+        if dtv is not None and tv is None:
+            dtv = None
+        return dq, dk, dv, dtq, dtk, dtv, None, None
+
+
+attention = _attention.apply
+
+
+class _plain_attention(torch.autograd.Function):
+    """Plain attention O = softmax(s Q K^T) V on the gfx950 forward kernel, with
+    the dO-only backward kernel (the same arithmetic the reference delegates to
+    flash-attn, flash_attention_jvp_triton.py:540-578)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, sm_scale=None):
+        assert q.shape[:-2] == k.shape[:-2] and k.shape[:-2] == v.shape[:-2]
+        assert k.shape[-2] == v.shape[-2] and q.shape[-1] == k.shape[-1]
+        assert q.shape[-1] in _HEAD_DIMS and v.shape[-1] in _HEAD_DIMS
+        if sm_scale is None:
+            sm_scale = q.shape[-1] ** (-0.5)
+        o, _, lse, _ = jvp_attention_forward(q, k, v, None, None, None, sm_scale)
+        if any(x.requires_grad for x in (q, k, v)):
+            ctx.save_for_backward(q, k, v, o, lse)
+            ctx.sm_scale = sm_scale
+        return o
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, o, lse = ctx.saved_tensors
+        assert q.shape[-1] == v.shape[-1], "Backward not supported with different headdim."
+        dq, dk, dv, _, _, _ = jvp_attention_backward(
+            q, k, v, None, None, None, o, None, lse, None, dout, None, ctx.sm_scale, False
+        )
+        return dq, dk, dv, None
+
+
+def plain_attention(q, k, v, sm_scale=None):
+    """softmax(sm_scale * q k^T) v for [B, H, L, D] tensors (gfx950 kernels)."""
+    return _plain_attention.apply(q, k, v, sm_scale)

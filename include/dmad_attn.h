@@ -1,0 +1,110 @@
+/*
+ * dmad_attn.h -- C ABI of the MI355X (gfx950) flash-attention JVP library.
+ *
+ * The library replaces the device side of the reference op
+ *   _attention.apply(q, k, v, tq, tk, tv, sm_scale=None, magi_mask=None) -> (o, to)
+ * (train/wan/rcm/utils/flash_attention_jvp_triton.py:450-582) and of the
+ * plain attention it is paired with. All buffers are owned by the caller;
+ * the library allocates nothing and keeps no state between calls. Every
+ * call enqueues work on `stream` (a hipStream_t) and returns without a host
+ * synchronisation.
+ *
+ * Tensor convention: logical shape [B, H, L, D] (BHSD) with arbitrary element
+ * strides given as int64_t[4] = {stride_b, stride_h, stride_l, stride_d}.
+ * stride_d must be 1. Tangent tensors share the strides of their primal
+ * (the reference asserts the same, :473-474). lse and mu are dense
+ * [B, H, Lq] float32.
+ *
+ * Every function returns DMAD_OK (0) or a non-zero status; dmad_last_error()
+ * then describes the failure (thread-local, valid until the next call).
+ */
+#ifndef DMAD_ATTN_H
+#define DMAD_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dmad_status {
+  DMAD_OK = 0,
+  DMAD_ERR_INVALID = 1,     /* bad pointer, shape, stride or argument */
+  DMAD_ERR_UNSUPPORTED = 2, /* head dim / dtype / size outside what the kernels handle */
+  DMAD_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  DMAD_ERR_HIP = 4          /* the HIP runtime reported an error at launch */
+};
+
+enum dmad_dtype { DMAD_BF16 = 0, DMAD_F16 = 1 };
+
+enum dmad_fwd_mode {
+  DMAD_FWD_PLAIN = 0,           /* O and LSE only */
+  DMAD_FWD_JVP = 1,             /* O, tangent output, LSE, mu */
+  DMAD_FWD_JVP_KV_TANGENT_ZERO = 2 /* as DMAD_FWD_JVP with tk = tv = 0 (tk, tv unused) */
+};
+
+/* Version of this ABI; bumped when a signature changes. */
+int dmad_abi_version(void);
+
+/* Description of the last failure on this thread ("" if none). */
+const char* dmad_last_error(void);
+
+/* Bytes of workspace dmad_attn_jvp_fwd / dmad_attn_fwd need for these sizes. */
+int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dv, size_t* bytes);
+
+/*
+ * Forward (+JVP): replaces the `_attn_fwd` launch of _attention.forward
+ * (flash_attention_jvp_triton.py:463-499, kernel :107-232).
+ *   o, to : [B,H,Lq,Dv] outputs in the input dtype (to unused in DMAD_FWD_PLAIN)
+ *   lse   : natural-log logsumexp of the scaled scores, [B,H,Lq] float32
+ *   mu    : r/l = rowsum(P * Sdot), [B,H,Lq] float32 (JVP modes; needed by the
+ *           full backward)
+ * Dqk, Dv in {16, 32, 64, 128, 256} (as asserted at :471-472); sm_scale > 0.
+ */
+int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
+                      const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4], void* o,
+                      void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
+ * Plain forward (O and LSE), the attention used by the non-JVP Wan forward
+ * (train/wan/rcm/utils/jvp_helper.py:305-308 and rcm/utils/attention.py:120-167).
+ */
+int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv, const void* q,
+                  const void* k, const void* v, const int64_t q_strides[4], const int64_t k_strides[4],
+                  const int64_t v_strides[4], void* o, const int64_t o_strides[4], float* lse, float sm_scale,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace dmad_attn_jvp_bwd needs. full != 0 selects the full
+ * derivative (cotangent of the tangent output included). */
+int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes);
+
+/*
+ * Backward: replaces _attention.backward (flash_attention_jvp_triton.py:534-579),
+ * whose arithmetic the reference delegates to flash-attn's _flash_attn_backward
+ * (:540-555) and _flash_attn_varlen_backward (:556-578).
+ *   dto == NULL : dO-only gradients dq, dk, dv, exactly what the reference
+ *                 computes (its cotangent of `to` is discarded, :535).
+ *   dto != NULL : full derivative of (o, to) w.r.t. (q, k, v), and, when dtq,
+ *                 dtk, dtv are non-NULL, w.r.t. the tangents (tq, tk, tv).
+ * Requires Dqk == Dv == D (as asserted at :537). o, to, lse, mu are the
+ * outputs of dmad_attn_jvp_fwd for the same inputs. Gradients have the
+ * strides given in dq_strides (shared by dq, dtq), dk_strides (dk, dtk) and
+ * dv_strides (dv, dtv); do/dto share do_strides.
+ */
+int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
+                      const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                      const void* o, const void* to, const int64_t o_strides[4], const float* lse, const float* mu,
+                      const void* dout, const void* dto, const int64_t do_strides[4], void* dq, void* dk, void* dv,
+                      void* dtq, void* dtk, void* dtv, const int64_t dq_strides[4], const int64_t dk_strides[4],
+                      const int64_t dv_strides[4], float sm_scale, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DMAD_ATTN_H */

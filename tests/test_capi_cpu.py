@@ -1,0 +1,97 @@
+"""The C-ABI library loads, exports every symbol include/dmad_attn.h declares,
+and rejects bad arguments before touching the GPU (no kernel launch here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dmad_attn.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dmad_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def nat():
+    from dmad_amd import _native
+
+    return _native
+
+
+def test_header_and_binding_agree(nat):
+    assert _declared() == sorted(nat.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(nat):
+    lib = nat.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.dmad_abi_version() == 1
+
+
+def _strides(*v):
+    return (ctypes.c_int64 * 4)(*v)
+
+
+def _fwd(nat, **over):
+    args = dict(dtype=0, mode=1, B=1, H=2, Lq=64, Lk=64, Dqk=64, Dv=64, q=256, k=256, v=256, tq=256, tk=256,
+                tv=256, qs=_strides(8192, 4096, 64, 1), ks=_strides(8192, 4096, 64, 1),
+                vs=_strides(8192, 4096, 64, 1), o=256, to=256, os=_strides(8192, 4096, 64, 1), lse=256, mu=256,
+                scale=0.125, ws=256, wsb=1 << 30, stream=0)
+    args.update(over)
+    a = args
+    return nat.lib().dmad_attn_jvp_fwd(
+        a["dtype"], a["mode"], a["B"], a["H"], a["Lq"], a["Lk"], a["Dqk"], a["Dv"],
+        ctypes.c_void_p(a["q"]), ctypes.c_void_p(a["k"]), ctypes.c_void_p(a["v"]), ctypes.c_void_p(a["tq"]),
+        ctypes.c_void_p(a["tk"]), ctypes.c_void_p(a["tv"]), a["qs"], a["ks"], a["vs"],
+        ctypes.c_void_p(a["o"]), ctypes.c_void_p(a["to"]), a["os"], ctypes.c_void_p(a["lse"]),
+        ctypes.c_void_p(a["mu"]), a["scale"], ctypes.c_void_p(a["ws"]), a["wsb"], ctypes.c_void_p(a["stream"]))
+
+
+@pytest.mark.parametrize(
+    "over,code,needle",
+    [
+        (dict(Dqk=48), 2, "head dims"),
+        (dict(Dv=512), 2, "head dims"),
+        (dict(dtype=7), 2, "dtype"),
+        (dict(mode=9), 1, "mode"),
+        (dict(scale=0.0), 2, "sm_scale"),
+        (dict(Lk=0), 1, "Lk"),
+        (dict(q=0), 1, "q: null"),
+        (dict(tk=0), 1, "tk: null"),
+        (dict(qs=_strides(8192, 4096, 64, 2)), 1, "stride of the head dim"),
+        (dict(ks=_strides(8192, 4096, 60, 1)), 1, "multiples of 8"),
+        (dict(v=258), 1, "aligned"),
+        (dict(mu=0), 1, "mu"),
+        (dict(wsb=16), 3, "workspace"),
+        (dict(ws=0), 3, "workspace"),
+        (dict(Lq=1 << 22, qs=_strides(0, 0, 4096, 1)), 2, "2 GiB"),
+    ],
+)
+def test_fwd_rejects_bad_arguments(nat, over, code, needle):
+    assert _fwd(nat, **over) == code
+    assert needle in nat.lib().dmad_last_error().decode()
+
+
+def test_fwd_empty_problem_is_a_no_op(nat):
+    assert _fwd(nat, Lq=0) == 0
+    assert _fwd(nat, B=0) == 0
+
+
+def test_kv_tangent_zero_mode_does_not_need_kv_tangents(nat):
+    # mode 2 never reads tk/tv: null is accepted up to the workspace check
+    assert _fwd(nat, mode=2, tk=0, tv=0, wsb=16) == 3
+
+
+def test_workspace_query(nat):
+    n = ctypes.c_size_t(0)
+    assert nat.lib().dmad_attn_fwd_workspace_bytes(1, 1, 40, 32760, 128, ctypes.byref(n)) == 0
+    assert n.value == 2 * 40 * 128 * 32768 * 2
+    assert nat.lib().dmad_attn_fwd_workspace_bytes(0, 1, 40, 32760, 128, ctypes.byref(n)) == 0
+    assert n.value == 40 * 128 * 32768 * 2
+    assert nat.lib().dmad_attn_fwd_workspace_bytes(0, 1, 1, 10, 16, ctypes.byref(n)) == 0
+    assert n.value == 32 * 64 * 2  # Dv < 32 pads to 32 rows, keys pad to 64
