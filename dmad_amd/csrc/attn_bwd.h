@@ -1,0 +1,470 @@
+// Backward attention kernels for gfx950.
+//
+// The reference backward (_attention.backward,
+// train/wan/rcm/utils/flash_attention_jvp_triton.py:534-579) hands dO, O and
+// LSE to flash-attn's FA2 backward and discards the cotangent of the tangent
+// output. Its arithmetic, restated from the mathematics:
+//   P  = exp(s Q K^T - LSE),  D = rowsum(dO * O)
+//   dP = dO V^T,  dS = P * (dP - D)
+//   dQ = s dS K,  dK = s dS^T Q,  dV = P^T dO                         (mode A)
+// The full derivative of (O, Od) (mode B), with Sd = s(Qd K^T + Q Kd^T),
+// mu = rowsum(P*Sd), rho = rowsum(dOd*O), D' = rowsum(dO*O) + rowsum(dOd*Od) - mu*rho:
+//   dPd = dOd V^T
+//   dP  = dO V^T + dOd Vd^T + dPd*(Sd - mu) - Sd*rho
+//   dS  = P*(dP - D'),  dSd = P*(dPd - rho),  Pd = P*(Sd - mu)
+//   dQ = s(dS K + dSd Kd),  dK = s(dS^T Q + dSd^T Qd),  dV = P^T dO + Pd^T dOd
+// and the tangent gradients dQd = s dSd K, dKd = s dSd^T Q, dVd = P^T dOd
+// are mode A with (dO, D) replaced by (dOd, rho).
+//
+// Work decomposition (one workgroup = 4 waves = 128 keys of one head):
+//   * lane l of wave w owns key 32w + l%32; its K, V (and Kd, Vd) rows stay in
+//     registers as the B operand of S = Q K^T and dP = dO V^T, so the C tiles
+//     have lane <-> key and 16 query values per lane;
+//   * query tiles stream through a double-buffered LDS ring by buffer->LDS
+//     DMA: Q, dO rows (A operands of the score GEMMs, read in perm32 row order),
+//     Q^T, dO^T (A operands of dK^T += Q^T dS, dV^T += dO^T P) and the per-row
+//     statistics (log2-domain LSE, D or D', mu, rho) prepared by bwd_prep;
+//   * P and dS leave the score C tiles already in B-operand layout (perm32),
+//     so dK^T and dV^T accumulate in registers with no data movement;
+//   * dS is written to LDS as [query][key] and each wave then forms one 32-row
+//     slice of dQ^T = K^T dS^T over all 128 keys of the workgroup, added to a
+//     float32 dQ buffer with global atomics (one add per element per
+//     workgroup); a final pass scales and casts it.
+#pragma once
+#include "common.h"
+
+namespace dmad {
+
+enum BwdMode : int { kBwdDoutOnly = 0, kBwdFull = 1 };
+
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* tq;
+  const void* tk;
+  const void* tv;
+  const void* dout;  // dO rows  (mode A with tangent grads: dOd)
+  const void* dto;   // dOd rows (mode B)
+  const void* qT;    // Q^T   [BH][DP][LQP]
+  const void* tqT;   // Qd^T  [BH][DP][LQP] (mode B)
+  const void* doT;   // dO^T  [BH][DP][LQP]
+  const void* dtoT;  // dOd^T [BH][DP][LQP] (mode B)
+  const float* stats;  // [BH][LQP/BMQ][NSTAT][BMQ]
+  float* dqacc;        // [BH][LQP][DP], accumulates sum(dS K) (+ sum(dSd Kd))
+  void* dk;
+  void* dv;
+  int64_t q_sb, q_sh, q_sl;  // shared by Q, Qd
+  int64_t k_sb, k_sh, k_sl;  // shared by K, Kd
+  int64_t v_sb, v_sh, v_sl;  // shared by V, Vd
+  int64_t do_sb, do_sh, do_sl;  // shared by dO, dOd
+  int64_t dk_sb, dk_sh, dk_sl;
+  int64_t dv_sb, dv_sh, dv_sl;
+  int B, H, Lq, Lk, LQP;
+  float scale, scale_log2;
+};
+
+template <int D, int MODE>
+struct BwdCfg {
+  static constexpr int NW = 4;
+  static constexpr int BK = 32 * NW;  // keys per workgroup
+  static constexpr int DP = D < 32 ? 32 : D;
+  static constexpr bool FULL = MODE == kBwdFull;
+  static constexpr int BMQ = (FULL || D > 128) ? 32 : 64;  // queries per tile
+  static constexpr int NQB = BMQ / 32;
+  static constexpr int KS = D / 16;   // d slices of the score GEMMs
+  static constexpr int DB = DP / 32;  // 32-row d blocks of dK^T, dV^T, dQ^T
+  static constexpr int CR = D / 8;    // 16-byte chunks per row-tile row
+  static constexpr int CT = BMQ / 8;  // chunks per transposed-tile row
+  static constexpr int NSTAT = FULL ? 4 : 2;
+  static constexpr int NT = FULL ? 4 : 2;  // row tiles (Q, dO [, Qd, dOd]) = transposed tiles
+  static constexpr int ROW_BYTES = BMQ * D * 2;
+  static constexpr int TR_BYTES = DP * BMQ * 2;
+  static constexpr int STAT_BYTES = NSTAT * BMQ * 4;
+  static constexpr int OFF_ROW = 0;
+  static constexpr int OFF_TR = NT * ROW_BYTES;
+  static constexpr int OFF_STAT = OFF_TR + NT * TR_BYTES;
+  static constexpr int STAGE = (OFF_STAT + STAT_BYTES + 1023) / 1024 * 1024;
+  static constexpr int XCH_BYTES = BMQ * BK * 2;  // one [BMQ][BK] bf16 exchange tile
+  static constexpr int NXCH = FULL ? 2 : 1;
+  static constexpr int LDS_BYTES = 2 * STAGE + NXCH * XCH_BYTES;
+  static constexpr int NRI = BMQ * CR / 64;  // wave-wide 1 KiB loads per row tile
+  static constexpr int NTI = DP * CT / 64;   // ... per transposed tile
+  // dQ items: (d block, query block) pairs, dealt to the waves round-robin
+  static constexpr int NITEMS = DB * NQB;
+  static constexpr int IPW = (NITEMS + NW - 1) / NW;
+  static constexpr int NDW = DB > NW ? DB / NW : 1;  // distinct d blocks per wave
+  static constexpr int KSX = BK / 16;               // key slices of dQ^T = K^T dS^T
+  static_assert(STAT_BYTES <= 1024, "statistics must fit one wave-wide load");
+};
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
+  using C = BwdCfg<D, MODE>;
+  constexpr int BMQ = C::BMQ, NQB = C::NQB, KS = C::KS, DB = C::DB, CR = C::CR, CT = C::CT;
+  constexpr bool FULL = C::FULL;
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+  char* xch = smem + 2 * C::STAGE;
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  const int nkt = (p.Lk + C::BK - 1) / C::BK;
+  const int work = xcd_remap(blockIdx.x, nkt * p.B * p.H);
+  const int bh = work / nkt, kt = work - bh * nkt;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int nqt = p.LQP / BMQ;
+
+  const int key = kt * C::BK + wave * 32 + col;  // this lane's key (C-layout column)
+  const bool key_ok = key < p.Lk;
+
+  // ---- stationary K, V (and Kd, Vd) rows: B operands of the score GEMMs
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes);
+  __amdgpu_buffer_rsrc_t rtk = rk, rtv = rv;
+  if constexpr (FULL) {
+    rtk = make_rsrc((const char*)p.tk + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+    rtv = make_rsrc((const char*)p.tv + (b * p.v_sb + h * p.v_sh) * 2, v_bytes);
+  }
+  i32x4_t kreg[KS], vreg[KS], tkreg[KS], tvreg[KS];
+  {
+    const uint32_t ko = (uint32_t)((int64_t)key * p.k_sl * 2) + half * 16;
+    const uint32_t vo = (uint32_t)((int64_t)key * p.v_sl * 2) + half * 16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kreg[s] = buf_load16(rk, ko + s * 32);
+      vreg[s] = buf_load16(rv, vo + s * 32);
+      if constexpr (FULL) {
+        tkreg[s] = buf_load16(rtk, ko + s * 32);
+        tvreg[s] = buf_load16(rtv, vo + s * 32);
+      }
+    }
+  }
+  // ---- K^T (and Kd^T) slices for dQ^T = K^T dS^T: lane (d = 32*dblk + col, half)
+  // holds K[kt*BK + 16*s + 8*half + e][d], e = 0..7, gathered 2 bytes at a time.
+  i32x4_t ktreg[C::NDW][C::KSX], tktreg[C::NDW][C::KSX];
+#pragma unroll
+  for (int i = 0; i < C::NDW; ++i) {
+    const int dblk = (C::DB > C::NW) ? wave + C::NW * i : (wave % C::DB);
+    const int d = dblk * 32 + col;
+#pragma unroll
+    for (int s = 0; s < C::KSX; ++s) {
+      uint32_t w[4], tw[4];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        uint32_t lohi[2], tlohi[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int kk = kt * C::BK + 16 * s + 8 * half + 2 * e2 + u;
+          const bool ok = (d < D) && (kk < p.Lk);
+          const uint32_t off = (uint32_t)((int64_t)(ok ? kk : 0) * p.k_sl * 2) + (ok ? d : 0) * 2;
+          lohi[u] = ok ? (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rk, (int)off, 0, 0) : 0u;
+          if constexpr (FULL)
+            tlohi[u] = ok ? (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rtk, (int)off, 0, 0) : 0u;
+        }
+        w[e2] = lohi[0] | (lohi[1] << 16);
+        if constexpr (FULL) tw[e2] = tlohi[0] | (tlohi[1] << 16);
+      }
+      ktreg[i][s] = i32x4_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      if constexpr (FULL) tktreg[i][s] = i32x4_t{(int)tw[0], (int)tw[1], (int)tw[2], (int)tw[3]};
+    }
+  }
+
+  // ---- DMA of one query tile into a stage
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
+  const uint32_t tr_bytes = (uint32_t)((int64_t)C::DP * p.LQP * 2);
+  const uint32_t st_bytes = (uint32_t)((int64_t)p.LQP * C::NSTAT * 4);
+  const __amdgpu_buffer_rsrc_t rrow[4] = {
+      make_rsrc((const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2, q_bytes),
+      make_rsrc((const char*)p.dout + (b * p.do_sb + h * p.do_sh) * 2, do_bytes),
+      make_rsrc((const char*)(FULL ? p.tq : p.q) + (b * p.q_sb + h * p.q_sh) * 2, q_bytes),
+      make_rsrc((const char*)(FULL ? p.dto : p.dout) + (b * p.do_sb + h * p.do_sh) * 2, do_bytes)};
+  const __amdgpu_buffer_rsrc_t rtr[4] = {
+      make_rsrc((const char*)p.qT + (int64_t)bh * tr_bytes, tr_bytes),
+      make_rsrc((const char*)p.doT + (int64_t)bh * tr_bytes, tr_bytes),
+      make_rsrc((const char*)(FULL ? p.tqT : p.qT) + (int64_t)bh * tr_bytes, tr_bytes),
+      make_rsrc((const char*)(FULL ? p.dtoT : p.doT) + (int64_t)bh * tr_bytes, tr_bytes)};
+  const __amdgpu_buffer_rsrc_t rst = make_rsrc((const char*)p.stats + (int64_t)bh * st_bytes, st_bytes);
+  const int64_t row_sl[4] = {p.q_sl, p.do_sl, p.q_sl, p.do_sl};
+
+  constexpr int RPW = (C::NRI + C::NW - 1) / C::NW;
+  constexpr int TPW = (C::NTI + C::NW - 1) / C::NW;
+  uint32_t roff_q[RPW], roff_do[RPW], toff[TPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CR, phys = pch % CR;
+    const int logical = phys ^ swz<CR>(perm32(row & 31) & 15);
+    roff_q[j] = (uint32_t)((int64_t)row * p.q_sl * 2) + logical * 16;
+    roff_do[j] = (uint32_t)((int64_t)row * p.do_sl * 2) + logical * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int d = pch / CT, phys = pch % CT;
+    const int logical = phys ^ swz<CT>(d & 15);
+    toff[j] = (uint32_t)(d * p.LQP * 2) + logical * 16;
+  }
+
+  auto issue_tile = [&](int qt, int stage) {
+    char* st = smem + stage * C::STAGE;
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t) {
+      const uint32_t rs = (uint32_t)((int64_t)qt * BMQ * row_sl[t] * 2);
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        const int i = wave + j * C::NW;
+        if (i < C::NRI) buf_load16_lds(rrow[t], st + C::OFF_ROW + t * C::ROW_BYTES + i * 1024, (t & 1) ? roff_do[j] : roff_q[j], rs);
+      }
+      const uint32_t ts = (uint32_t)qt * BMQ * 2;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const int i = wave + j * C::NW;
+        if (i < C::NTI) buf_load16_lds(rtr[t], st + C::OFF_TR + t * C::TR_BYTES + i * 1024, toff[j], ts);
+      }
+    }
+    if (wave == C::NW - 1 && lane * 16 < C::STAT_BYTES)
+      buf_load16_lds(rst, st + C::OFF_STAT, lane * 16, (uint32_t)qt * C::STAT_BYTES);
+  };
+
+  // ---- LDS read offsets
+  const int rswz = swz<CR>(col & 15), tswz = swz<CT>(col & 15);
+  const int rrow_off = perm32(col) * CR * 16;
+  const int trow_off = col * CT * 16;
+
+  f32x16_t dkacc[DB], dvacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      dkacc[d][v] = 0.f;
+      dvacc[d][v] = 0.f;
+    }
+  }
+
+  issue_tile(0, 0);
+  for (int qt = 0; qt < nqt; ++qt) {
+    wait_vmem();
+    __syncthreads();
+    if (qt + 1 < nqt) issue_tile(qt + 1, (qt + 1) & 1);
+    const char* st = smem + (qt & 1) * C::STAGE;
+    const char* rq_t = st + C::OFF_ROW;
+    const char* rdo_t = st + C::OFF_ROW + C::ROW_BYTES;
+    const char* rtq_t = st + C::OFF_ROW + 2 * C::ROW_BYTES;
+    const char* rdto_t = st + C::OFF_ROW + 3 * C::ROW_BYTES;
+    const float* sst = (const float*)(st + C::OFF_STAT);
+
+    // ---- phase 1: score tiles (rows = queries in perm32 order, cols = keys)
+    f32x16_t sacc[NQB], dpacc[NQB], tsacc[NQB], dpdacc[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        sacc[qb][v] = 0.f;
+        dpacc[qb][v] = 0.f;
+        tsacc[qb][v] = 0.f;
+        dpdacc[qb][v] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        const int off = qb * 32 * CR * 16 + rrow_off + (((2 * s + half) ^ rswz) << 4);
+        const i32x4_t aq = *(const i32x4_t*)(rq_t + off);
+        const i32x4_t ado = *(const i32x4_t*)(rdo_t + off);
+        sacc[qb] = mfma32(aq, kreg[s], sacc[qb], T());
+        dpacc[qb] = mfma32(ado, vreg[s], dpacc[qb], T());
+        if constexpr (FULL) {
+          const i32x4_t atq = *(const i32x4_t*)(rtq_t + off);
+          const i32x4_t adto = *(const i32x4_t*)(rdto_t + off);
+          tsacc[qb] = mfma32(atq, kreg[s], tsacc[qb], T());
+          tsacc[qb] = mfma32(aq, tkreg[s], tsacc[qb], T());
+          dpacc[qb] = mfma32(adto, tvreg[s], dpacc[qb], T());
+          dpdacc[qb] = mfma32(adto, vreg[s], dpdacc[qb], T());
+        }
+      }
+    }
+
+    // ---- phase 2: elementwise; value v of block qb is query qb*32 + 16t + 8*half + e (v = 8t + e)
+    i32x4_t pb[NQB][2], dsb[NQB][2], tpb[NQB][2], tdsb[NQB][2];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int q0 = qb * 32 + 16 * t + 8 * half;
+        float lse2[8], dlt[8], mu[8], rho[8];
+#pragma unroll
+        for (int e4 = 0; e4 < 2; ++e4) {
+          const float4 a = *(const float4*)(sst + 0 * BMQ + q0 + 4 * e4);
+          const float4 c = *(const float4*)(sst + 1 * BMQ + q0 + 4 * e4);
+          lse2[4 * e4 + 0] = a.x; lse2[4 * e4 + 1] = a.y; lse2[4 * e4 + 2] = a.z; lse2[4 * e4 + 3] = a.w;
+          dlt[4 * e4 + 0] = c.x; dlt[4 * e4 + 1] = c.y; dlt[4 * e4 + 2] = c.z; dlt[4 * e4 + 3] = c.w;
+          if constexpr (FULL) {
+            const float4 m4 = *(const float4*)(sst + 2 * BMQ + q0 + 4 * e4);
+            const float4 r4 = *(const float4*)(sst + 3 * BMQ + q0 + 4 * e4);
+            mu[4 * e4 + 0] = m4.x; mu[4 * e4 + 1] = m4.y; mu[4 * e4 + 2] = m4.z; mu[4 * e4 + 3] = m4.w;
+            rho[4 * e4 + 0] = r4.x; rho[4 * e4 + 1] = r4.y; rho[4 * e4 + 2] = r4.z; rho[4 * e4 + 3] = r4.w;
+          }
+        }
+        float pv[8], dsv[8], tpv[8], tdsv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int v = 8 * t + e;
+          float pe = fast_exp2(fmaf(sacc[qb][v], p.scale_log2, -lse2[e]));
+          pe = key_ok ? pe : 0.f;
+          pv[e] = pe;
+          if constexpr (!FULL) {
+            dsv[e] = pe * (dpacc[qb][v] - dlt[e]);
+          } else {
+            const float sd = tsacc[qb][v] * p.scale;
+            const float c = sd - mu[e];
+            const float dpd = dpdacc[qb][v];
+            const float dp = dpacc[qb][v] + dpd * c - sd * rho[e];
+            tpv[e] = pe * c;
+            dsv[e] = pe * (dp - dlt[e]);
+            tdsv[e] = pe * (dpd - rho[e]);
+          }
+        }
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          pb[qb][t][e2] = (int)Elem<T>::pack2(pv[2 * e2], pv[2 * e2 + 1]);
+          dsb[qb][t][e2] = (int)Elem<T>::pack2(dsv[2 * e2], dsv[2 * e2 + 1]);
+          if constexpr (FULL) {
+            tpb[qb][t][e2] = (int)Elem<T>::pack2(tpv[2 * e2], tpv[2 * e2 + 1]);
+            tdsb[qb][t][e2] = (int)Elem<T>::pack2(tdsv[2 * e2], tdsv[2 * e2 + 1]);
+          }
+        }
+        // dS (and dSd) -> exchange tile [query][key], 16-byte chunks XOR-swizzled by query
+        const int kl = wave * 32 + col;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int qi = q0 + e;
+          const int off = qi * (C::BK * 2) + (((kl >> 3) ^ (qi & 15)) << 4) + ((kl & 7) << 1);
+          const uint32_t w = (uint32_t)dsb[qb][t][e >> 1];
+          *(uint16_t*)(xch + off) = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff));
+          if constexpr (FULL) {
+            const uint32_t tw = (uint32_t)tdsb[qb][t][e >> 1];
+            *(uint16_t*)(xch + C::XCH_BYTES + off) = (uint16_t)((e & 1) ? (tw >> 16) : (tw & 0xffff));
+          }
+        }
+      }
+    }
+
+    // ---- phase 3: dV^T += dO^T P (+ dOd^T Pd), dK^T += Q^T dS (+ Qd^T dSd)
+    const char* tq_t = st + C::OFF_TR;
+    const char* tdo_t = st + C::OFF_TR + C::TR_BYTES;
+    const char* ttq_t = st + C::OFF_TR + 2 * C::TR_BYTES;
+    const char* tdto_t = st + C::OFF_TR + 3 * C::TR_BYTES;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int ch = ((qb * 4 + 2 * t + half) ^ tswz) << 4;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+          const int off = d * 32 * CT * 16 + trow_off + ch;
+          const i32x4_t ado = *(const i32x4_t*)(tdo_t + off);
+          const i32x4_t aq = *(const i32x4_t*)(tq_t + off);
+          dvacc[d] = mfma32(ado, pb[qb][t], dvacc[d], T());
+          dkacc[d] = mfma32(aq, dsb[qb][t], dkacc[d], T());
+          if constexpr (FULL) {
+            const i32x4_t adto = *(const i32x4_t*)(tdto_t + off);
+            const i32x4_t atq = *(const i32x4_t*)(ttq_t + off);
+            dvacc[d] = mfma32(adto, tpb[qb][t], dvacc[d], T());
+            dkacc[d] = mfma32(atq, tdsb[qb][t], dkacc[d], T());
+          }
+        }
+      }
+    }
+
+    __syncthreads();  // exchange tile complete
+
+    // ---- phase 4: dQ^T[dblk][q] = K^T dS^T (+ Kd^T dSd^T) over the 128 keys; atomics into dqacc
+#pragma unroll
+    for (int m = 0; m < C::IPW; ++m) {
+      const int item = wave + C::NW * m;
+      if (item < C::NITEMS) {
+        const int dblk = item % DB, qb = item / DB;
+        const int di = (C::DB > C::NW) ? m % C::NDW : 0;
+        f32x16_t acc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+        const int qi = qb * 32 + col;
+#pragma unroll
+        for (int s = 0; s < C::KSX; ++s) {
+          const int off = qi * (C::BK * 2) + (((2 * s + half) ^ (qi & 15)) << 4);
+          const i32x4_t bds = *(const i32x4_t*)(xch + off);
+          acc = mfma32(ktreg[di][s], bds, acc, T());
+          if constexpr (FULL) {
+            const i32x4_t btds = *(const i32x4_t*)(xch + C::XCH_BYTES + off);
+            acc = mfma32(tktreg[di][s], btds, acc, T());
+          }
+        }
+        const int qrow = qt * BMQ + qi;
+        float* dst = p.dqacc + ((int64_t)bh * p.LQP + qrow) * C::DP + dblk * 32 + 4 * half;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) atomicAdd(dst + 8 * j + r, acc[4 * j + r]);
+        }
+      }
+    }
+  }
+
+  // ---- store dK = s (dK^T)^T, dV = (dV^T)^T for this lane's key
+  if (key_ok) {
+    char* dkp = (char*)p.dk + ((b * p.dk_sb + h * p.dk_sh) + (int64_t)key * p.dk_sl) * 2;
+    char* dvp = (char*)p.dv + ((b * p.dv_sb + h * p.dv_sh) + (int64_t)key * p.dv_sl) * 2;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int dc = d * 32 + 8 * j + 4 * half;
+        if (D >= 32 || dc < D) {
+          u32x2_t wk = {Elem<T>::pack2(dkacc[d][4 * j] * p.scale, dkacc[d][4 * j + 1] * p.scale),
+                        Elem<T>::pack2(dkacc[d][4 * j + 2] * p.scale, dkacc[d][4 * j + 3] * p.scale)};
+          u32x2_t wv = {Elem<T>::pack2(dvacc[d][4 * j], dvacc[d][4 * j + 1]),
+                        Elem<T>::pack2(dvacc[d][4 * j + 2], dvacc[d][4 * j + 3])};
+          *(u32x2_t*)(dkp + dc * 2) = wk;
+          *(u32x2_t*)(dvp + dc * 2) = wv;
+        }
+      }
+    }
+  }
+}
+
+// Per-row statistics for the backward, one thread per (b*h, query row):
+//   A layout  [BH][LQP/BA][2][BA]: lse2 = LSE*log2(e), D = rowsum(dO*O)
+//   B layout  [BH][LQP/32][4][32]: lse2, D' = rowsum(dO*O) + rowsum(dOd*Od) - mu*rho, mu, rho
+//   BT layout [BH][LQP/BA][2][BA]: lse2, rho = rowsum(dOd*O)   (tangent gradients)
+// BA is the query tile of the dO-only kernel for this head dim.
+// Rows past Lq get lse2 = +inf (so P = 0) and zeros.
+struct PrepParams {
+  const void* o;
+  const void* to;
+  const void* dout;
+  const void* dto;
+  const float* lse;
+  const float* mu;
+  float* stats_a;   // may be null
+  float* stats_b;   // may be null
+  float* stats_bt;  // may be null
+  int64_t o_sb, o_sh, o_sl;
+  int64_t do_sb, do_sh, do_sl;
+  int H, Lq, LQP, D, BH, BA;
+};
+
+struct DqConvertParams {
+  const float* acc;  // [BH][LQP][DP]
+  void* dq;
+  int64_t sb, sh, sl;
+  int H, Lq, LQP, D, DP, BH;
+  float scale;
+};
+
+}  // namespace dmad

@@ -1,0 +1,35 @@
+// Instantiates the backward kernels for one (element type, head dim) pair:
+// compiled once per pair with -DDMAD_T=<0 bf16 | 1 f16> -DDMAD_D=<D>.
+#include "launch.h"
+
+#ifndef DMAD_T
+#error "DMAD_T must be defined"
+#endif
+#ifndef DMAD_D
+#error "DMAD_D must be defined"
+#endif
+
+namespace dmad {
+
+#if DMAD_T == 0
+using Elt = __bf16;
+#else
+using Elt = _Float16;
+#endif
+
+template <typename T, int D, int MODE>
+static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <>
+BwdLaunchFn bwd_select<Elt, DMAD_D>(int mode) {
+  if (mode == kBwdDoutOnly) return &bwd_launch<Elt, DMAD_D, kBwdDoutOnly>;
+#if DMAD_D <= 128
+  if (mode == kBwdFull) return &bwd_launch<Elt, DMAD_D, kBwdFull>;
+#endif
+  return nullptr;
+}
+
+}  // namespace dmad

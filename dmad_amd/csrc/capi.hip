@@ -19,6 +19,16 @@ template <> FwdLaunchFn fwd_select<_Float16, 32>(int, int);
 template <> FwdLaunchFn fwd_select<_Float16, 64>(int, int);
 template <> FwdLaunchFn fwd_select<_Float16, 128>(int, int);
 template <> FwdLaunchFn fwd_select<_Float16, 256>(int, int);
+template <> BwdLaunchFn bwd_select<__bf16, 16>(int);
+template <> BwdLaunchFn bwd_select<__bf16, 32>(int);
+template <> BwdLaunchFn bwd_select<__bf16, 64>(int);
+template <> BwdLaunchFn bwd_select<__bf16, 128>(int);
+template <> BwdLaunchFn bwd_select<__bf16, 256>(int);
+template <> BwdLaunchFn bwd_select<_Float16, 16>(int);
+template <> BwdLaunchFn bwd_select<_Float16, 32>(int);
+template <> BwdLaunchFn bwd_select<_Float16, 64>(int);
+template <> BwdLaunchFn bwd_select<_Float16, 128>(int);
+template <> BwdLaunchFn bwd_select<_Float16, 256>(int);
 }  // namespace dmad
 
 namespace {
@@ -93,6 +103,51 @@ dmad::FwdLaunchFn pick_fwd(int dtype, int64_t dqk, int64_t dv, int mode) {
     }
   }
   return nullptr;
+}
+
+dmad::BwdLaunchFn pick_bwd(int dtype, int64_t d, int mode) {
+  using namespace dmad;
+  if (dtype == DMAD_BF16) {
+    switch (d) {
+      case 16: return bwd_select<__bf16, 16>(mode);
+      case 32: return bwd_select<__bf16, 32>(mode);
+      case 64: return bwd_select<__bf16, 64>(mode);
+      case 128: return bwd_select<__bf16, 128>(mode);
+      case 256: return bwd_select<__bf16, 256>(mode);
+    }
+  } else if (dtype == DMAD_F16) {
+    switch (d) {
+      case 16: return bwd_select<_Float16, 16>(mode);
+      case 32: return bwd_select<_Float16, 32>(mode);
+      case 64: return bwd_select<_Float16, 64>(mode);
+      case 128: return bwd_select<_Float16, 128>(mode);
+      case 256: return bwd_select<_Float16, 256>(mode);
+    }
+  }
+  return nullptr;
+}
+
+// Backward workspace, carved in this order (each piece 256-byte aligned):
+//   transposed Q, dO [, Qd, dOd]   bf16/f16 [BH][DP][LQP] each
+//   statistics (A or B layout) [, BT layout]
+//   dQ accumulator fp32 [BH][LQP][DP] [, dQd accumulator]
+struct BwdWs {
+  int64_t tr, stats, stats_bt, acc, total;
+  int ntr;
+  bool tgrad;
+};
+
+BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t D) {
+  const int64_t BH = B * H, dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64);
+  BwdWs w{};
+  w.ntr = full ? 4 : 2;
+  w.tgrad = full == 2;
+  w.tr = round_up(BH * dp * lqp * 2, 256);
+  w.stats = round_up(BH * lqp * (full ? 4 : 2) * 4, 256);
+  w.stats_bt = w.tgrad ? round_up(BH * lqp * 2 * 4, 256) : 0;
+  w.acc = round_up(BH * lqp * dp * 4, 256);
+  w.total = w.ntr * w.tr + w.stats + w.stats_bt + w.acc * (w.tgrad ? 2 : 1);
+  return w;
 }
 
 }  // namespace
@@ -212,9 +267,12 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
 }
 
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes) {
-  (void)full; (void)B; (void)H; (void)Lq; (void)Lk; (void)D;
-  if (bytes) *bytes = 0;
-  return fail(DMAD_ERR_UNSUPPORTED, "backward not built yet");
+  (void)Lk;
+  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
+  if (full < 0 || full > 2) return fail(DMAD_ERR_INVALID, "full must be 0, 1 or 2");
+  if (B < 0 || H < 0 || Lq < 0 || !head_dim_ok(D)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  *bytes = (size_t)bwd_ws(full, B, H, Lq, D).total;
+  return ok();
 }
 
 int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
@@ -225,7 +283,155 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
                       void* dtq, void* dtk, void* dtv, const int64_t dq_strides[4], const int64_t dk_strides[4],
                       const int64_t dv_strides[4], float sm_scale, void* workspace, size_t workspace_bytes,
                       void* stream) {
-  return fail(DMAD_ERR_UNSUPPORTED, "backward not built yet");
+  if (dtype != DMAD_BF16 && dtype != DMAD_F16) return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+  if (B < 0 || H < 0 || Lq < 0 || Lk < 0) return fail(DMAD_ERR_INVALID, "negative size");
+  if (!head_dim_ok(D)) return fail(DMAD_ERR_UNSUPPORTED, "head dim must be in {16,32,64,128,256}, got %lld", (long long)D);
+  if (!(sm_scale > 0.f)) return fail(DMAD_ERR_UNSUPPORTED, "sm_scale must be positive");
+  const bool full = dto != nullptr;
+  const bool tgrad = dtq != nullptr || dtk != nullptr || dtv != nullptr;
+  if (tgrad && !(dtq && dtk && dtv)) return fail(DMAD_ERR_INVALID, "dtq, dtk, dtv must be all set or all null");
+  if (tgrad && !full) return fail(DMAD_ERR_INVALID, "tangent gradients need the cotangent dto");
+  if (full && D > 128) return fail(DMAD_ERR_UNSUPPORTED, "the full backward supports head dims up to 128");
+  if (B == 0 || H == 0 || (Lq == 0 && Lk == 0)) return ok();
+  if (Lk == 0) return fail(DMAD_ERR_INVALID, "Lk must be at least 1");
+  if (B * H > ((int64_t)1 << 24) || Lq >= ((int64_t)1 << 26) || Lk >= ((int64_t)1 << 26))
+    return fail(DMAD_ERR_UNSUPPORTED, "sizes too large");
+  int rc;
+  if ((rc = check_operand("q", q, q_strides, Lq, D))) return rc;
+  if ((rc = check_operand("k", k, k_strides, Lk, D))) return rc;
+  if ((rc = check_operand("v", v, v_strides, Lk, D))) return rc;
+  if ((rc = check_operand("o", o, o_strides, Lq, D))) return rc;
+  if ((rc = check_operand("dout", dout, do_strides, Lq, D))) return rc;
+  if ((rc = check_operand("dq", dq, dq_strides, Lq, D))) return rc;
+  if ((rc = check_operand("dk", dk, dk_strides, Lk, D))) return rc;
+  if ((rc = check_operand("dv", dv, dv_strides, Lk, D))) return rc;
+  if (lse == nullptr) return fail(DMAD_ERR_INVALID, "lse: null pointer");
+  if (full) {
+    if ((rc = check_operand("tq", tq, q_strides, Lq, D))) return rc;
+    if ((rc = check_operand("tk", tk, k_strides, Lk, D))) return rc;
+    if ((rc = check_operand("tv", tv, v_strides, Lk, D))) return rc;
+    if ((rc = check_operand("to", to, o_strides, Lq, D))) return rc;
+    if ((rc = check_operand("dto", dto, do_strides, Lq, D))) return rc;
+    if (mu == nullptr) return fail(DMAD_ERR_INVALID, "mu: null pointer");
+  }
+  if (tgrad) {
+    if ((rc = check_operand("dtq", dtq, dq_strides, Lq, D))) return rc;
+    if ((rc = check_operand("dtk", dtk, dk_strides, Lk, D))) return rc;
+    if ((rc = check_operand("dtv", dtv, dv_strides, Lk, D))) return rc;
+  }
+  const int fl = full ? (tgrad ? 2 : 1) : 0;
+  const BwdWs w = bwd_ws(fl, B, H, Lq, D);
+  if (workspace == nullptr || (int64_t)workspace_bytes < w.total)
+    return fail(DMAD_ERR_WORKSPACE, "workspace needs %lld bytes, got %lld", (long long)w.total, (long long)workspace_bytes);
+  if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
+  const int64_t dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), BH = B * H;
+  if (dp * lqp * 2 >= kMaxHeadBytes || lqp * dp * 4 * BH >= ((int64_t)1 << 46)) return fail(DMAD_ERR_UNSUPPORTED, "Lq too large");
+  const int mode = full ? dmad::kBwdFull : dmad::kBwdDoutOnly;
+  dmad::BwdLaunchFn fn = pick_bwd(dtype, D, mode);
+  dmad::BwdLaunchFn fn_a = tgrad ? pick_bwd(dtype, D, dmad::kBwdDoutOnly) : nullptr;
+  if (fn == nullptr || (tgrad && fn_a == nullptr)) return fail(DMAD_ERR_UNSUPPORTED, "no backward kernel for D=%lld", (long long)D);
+
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  char* trq = ws;
+  char* trdo = ws + w.tr;
+  char* trtq = full ? ws + 2 * w.tr : nullptr;
+  char* trdto = full ? ws + 3 * w.tr : nullptr;
+  float* stats = (float*)(ws + w.ntr * w.tr);
+  float* stats_bt = w.tgrad ? (float*)(ws + w.ntr * w.tr + w.stats) : nullptr;
+  float* acc = (float*)(ws + w.ntr * w.tr + w.stats + w.stats_bt);
+  float* tacc = w.tgrad ? acc + w.acc / 4 : nullptr;
+
+  hipError_t e;
+  auto tr = [&](const void* x, const int64_t* st, char* y) {
+    dmad::TransposeParams tp{x, y, st[0], st[1], st[2], (int)H, (int)Lq, (int)D, (int)lqp, (int)dp};
+    return dmad::launch_transpose_pad(tp, (int)BH, s);
+  };
+  if ((e = tr(q, q_strides, trq)) != hipSuccess || (e = tr(dout, do_strides, trdo)) != hipSuccess)
+    return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
+  if (full && ((e = tr(tq, q_strides, trtq)) != hipSuccess || (e = tr(dto, do_strides, trdto)) != hipSuccess))
+    return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
+
+  const int ba = dmad::bwd_bmq((int)D, dmad::kBwdDoutOnly);
+  dmad::PrepParams pp{};
+  pp.o = o;
+  pp.to = full ? to : nullptr;
+  pp.dout = dout;
+  pp.dto = full ? dto : nullptr;
+  pp.lse = lse;
+  pp.mu = full ? mu : nullptr;
+  pp.stats_a = full ? nullptr : stats;
+  pp.stats_b = full ? stats : nullptr;
+  pp.stats_bt = stats_bt;
+  pp.o_sb = o_strides[0];
+  pp.o_sh = o_strides[1];
+  pp.o_sl = o_strides[2];
+  pp.do_sb = do_strides[0];
+  pp.do_sh = do_strides[1];
+  pp.do_sl = do_strides[2];
+  pp.H = (int)H;
+  pp.Lq = (int)Lq;
+  pp.LQP = (int)lqp;
+  pp.D = (int)D;
+  pp.BH = (int)BH;
+  pp.BA = ba;
+  if ((e = dmad::launch_bwd_prep(pp, dtype, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "prep launch: %s", hipGetErrorString(e));
+  if ((e = dmad::launch_zero(acc, w.acc / 4 * (w.tgrad ? 2 : 1), s)) != hipSuccess)
+    return fail(DMAD_ERR_HIP, "zero launch: %s", hipGetErrorString(e));
+
+  dmad::BwdParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.tq = full ? tq : q;
+  p.tk = full ? tk : k;
+  p.tv = full ? tv : v;
+  p.dout = dout;
+  p.dto = full ? dto : dout;
+  p.qT = trq;
+  p.tqT = full ? trtq : trq;
+  p.doT = trdo;
+  p.dtoT = full ? trdto : trdo;
+  p.stats = stats;
+  p.dqacc = acc;
+  p.dk = dk;
+  p.dv = dv;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_sl = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_sl = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_sl = v_strides[2];
+  p.do_sb = do_strides[0]; p.do_sh = do_strides[1]; p.do_sl = do_strides[2];
+  p.dk_sb = dk_strides[0]; p.dk_sh = dk_strides[1]; p.dk_sl = dk_strides[2];
+  p.dv_sb = dv_strides[0]; p.dv_sh = dv_strides[1]; p.dv_sl = dv_strides[2];
+  p.B = (int)B;
+  p.H = (int)H;
+  p.Lq = (int)Lq;
+  p.Lk = (int)Lk;
+  p.LQP = (int)lqp;
+  p.scale = sm_scale;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  const int64_t nkt = (Lk + 127) / 128;
+  if (nkt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  if ((e = fn(p, (int)(nkt * BH), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  if (tgrad) {
+    // tangent gradients: the dO-only kernel with (dO, D) := (dOd, rho)
+    dmad::BwdParams pt = p;
+    pt.dout = dto;
+    pt.doT = trdto;
+    pt.stats = stats_bt;
+    pt.dqacc = tacc;
+    pt.dk = dtk;
+    pt.dv = dtv;
+    if ((e = fn_a(pt, (int)(nkt * BH), s)) != hipSuccess)
+      return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  }
+  dmad::DqConvertParams cp{acc, dq, dq_strides[0], dq_strides[1], dq_strides[2], (int)H, (int)Lq, (int)lqp, (int)D, (int)dp, (int)BH, sm_scale};
+  if ((e = dmad::launch_dq_convert(cp, dtype, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
+  if (tgrad) {
+    cp.acc = tacc;
+    cp.dq = dtq;
+    if ((e = dmad::launch_dq_convert(cp, dtype, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
+  }
+  return ok();
 }
 
 }  // extern "C"

@@ -143,7 +143,8 @@ def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_sc
     dtv = torch.empty_like(dv) if tgrads else None
     lib = nat.lib()
     ws_bytes = nat.ctypes.c_size_t(0)
-    nat.check(lib.dmad_attn_bwd_workspace_bytes(int(full), B, H, Lq, Lk, D, nat.ctypes.byref(ws_bytes)))
+    ws_mode = (2 if tgrads else 1) if full else 0
+    nat.check(lib.dmad_attn_bwd_workspace_bytes(ws_mode, B, H, Lq, Lk, D, nat.ctypes.byref(ws_bytes)))
     ws = torch.empty(max(int(ws_bytes.value), 1), device=q.device, dtype=torch.uint8)
     nat.check(
         lib.dmad_attn_jvp_bwd(
@@ -196,6 +197,9 @@ class _attention(torch.autograd.Function):
                 raise RuntimeError("Backward with MagiMask is not supported.")
             raise NotImplementedError("block-sparse (MagiMask) JVP attention is not implemented by dmad_amd")
         tangent_grad = any(x is not None and x.requires_grad for x in (tq, tk, tv))
+        # an output that does not reach the loss arrives in backward as None
+        # (not zeros), so an unused `to` keeps the dO-only kernel
+        ctx.set_materialize_grads(False)
         o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale)
         if is_grad or tangent_grad:
             ctx.save_for_backward(q, k, v, tq, tk, tv, o, to, lse, mu)
