@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Benchmark of the flash-attention JVP path on one MI355X.
+
+One step = one Wan2.1-14B DiT layer's attention work on the JVP path:
+  * self-attention forward + JVP     B=1, H=40, L=32760, D=128, bf16   (12 L^2 D H flop)
+  * self-attention backward, dO only (what the reference computes)       (10 L^2 D H flop)
+  * text cross-attention forward + JVP, Lq=32760 over 512 keys, Kd=Vd=0  (8 Lq Lk D H flop)
+Inputs are resident in HBM before timing starts (synthetic, seeded: Q, K RMS-normalised
+over H*D and rotated by 3D RoPE on the 21x30x52 latent grid, V ~ N(0,1), tangents
+~ N(0, 0.1^2), dO ~ N(0,1)).
+
+Prints one JSON line: value = algorithmic TFLOP/s of the whole step (flops as above,
+exp/softmax work not counted, the convention of flash_attention_jvp_triton.py:716-724),
+plus a roofline record for the dominant kernel timed live with HIP events, and a
+CPU baseline (the oracle's float32 PyTorch math path on the host cores, on a bounded
+sample, extrapolated).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 flop/clk/CU
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--heads", type=int, default=40, help="attention heads (14B: 40, 1.3B: 12)")
+    ap.add_argument("--seq", type=int, default=32760)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--full-bwd", action="store_true", help="also time the full-derivative backward (extra field)")
+    return ap.parse_args()
+
+
+def _traffic_from_profiles(name):
+    """HBM bytes per launch of `name` from a committed rocprofv3 counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(L, D, H, seconds):
+    """Oracle float32 math path on the host: torch.func.jvp for (O, Od), autograd for dQ/dK/dV.
+
+    Runs 2048-row query chunks of one head at full Lk until `seconds` of work are
+    done; FLOP/s are extrapolated linearly (the work is linear in rows and heads).
+    """
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle.attention import math_attention
+
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn((1, 1, L, D), generator=g)
+    v = torch.randn((1, 1, L, D), generator=g)
+    tk = torch.randn((1, 1, L, D), generator=g) * 0.1
+    tv = torch.randn((1, 1, L, D), generator=g) * 0.1
+    rows, done, t = 2048, 0, 0.0
+    s = D ** -0.5
+    while t < seconds:
+        q = torch.randn((1, 1, rows, D), generator=g)
+        tq = torch.randn((1, 1, rows, D), generator=g) * 0.1
+        do = torch.randn((1, 1, rows, D), generator=g)
+        t0 = time.perf_counter()
+        fn = lambda a, b, c: math_attention(a, b, c, s)[0]  # noqa: E731
+        torch.func.jvp(fn, (q, k, v), (tq, tk, tv))
+        leaves = [x.clone().requires_grad_(True) for x in (q, k, v)]
+        o = math_attention(*leaves, s)[0]
+        torch.autograd.grad(o, leaves, do)
+        t += time.perf_counter() - t0
+        done += rows
+    flops = 22.0 * done * L * D
+    return {
+        "value": round(flops / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"1 head x {done} query rows x {L} keys, D={D}, fp32 torch.func.jvp + autograd "
+                  f"(fwd+JVP+dO-only bwd) in {t:.1f} s; extrapolates to "
+                  f"{H * L / done * t / 60:.0f} min for the 14B layer",
+    }
+
+
+def main():
+    args = _args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build runs the attention of one device "
+              "(no collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from dmad_amd import _native
+    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+    from dmad_amd.workload import make_inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    H, L, D, LKX = args.heads, args.seq, 128, 512
+    grid = (21, 30, 52) if L == 32760 else ((21, 45, 80) if L == 75600 else None)
+    x = make_inputs(1, H, L, L, D, dtype=torch.bfloat16, seed=0, device=dev, grid=grid, with_grads=True,
+                    gen_device=dev)
+    q, k, v, tq, tk, tv, do = (x[n] for n in ("q", "k", "v", "tq", "tk", "tv", "do"))
+    xc = make_inputs(1, H, L, LKX, D, dtype=torch.bfloat16, seed=1, device=dev, gen_device=dev)
+    kc, vc = xc["k"], xc["v"]
+    s = D ** -0.5
+    lib = _native.lib()
+
+    f_fwd = 12.0 * H * L * L * D
+    f_bwd = 10.0 * H * L * L * D
+    f_cross = 8.0 * H * L * LKX * D
+    f_step = f_fwd + f_bwd + f_cross
+
+    ev = {name: [] for name in ("fwd", "bwd")}
+
+    def step(record):
+        def timed(name, fn):
+            if record:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                # torch creates the HIP events on first record; the library then
+                # re-records them around the kernel itself
+                a.record()
+                b.record()
+                _native.check(lib.dmad_set_kernel_events(a.cuda_event, b.cuda_event))
+                out = fn()
+                _native.check(lib.dmad_set_kernel_events(None, None))
+                ev[name].append((a, b))
+                return out
+            return fn()
+
+        o, to, lse, mu = timed("fwd", lambda: jvp_attention_forward(q, k, v, tq, tk, tv, s))
+        timed("bwd", lambda: jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s,
+                                                    False))
+        jvp_attention_forward(q, kc, vc, tq, None, None, s)
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step(True)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    k_ms = {n: sum(a.elapsed_time(b) for a, b in lst) / len(lst) for n, lst in ev.items()}
+    value = f_step / (ms_step * 1e-3) / 1e12
+
+    dom = max(k_ms, key=k_ms.get)
+    dom_flops = {"fwd": f_fwd, "bwd": f_bwd}[dom]
+    dom_name = {"fwd": "attn_fwd_kernel<bf16,128,128,jvp>", "bwd": "attn_bwd_kernel<bf16,128,dout_only>"}[dom]
+    achieved = dom_flops / (k_ms[dom] * 1e-3) / 1e12
+    out = {
+        "metric": "attn fwd+JVP+bwd TFLOP/s & %MFMA peak; ms/layer at Wan2.1-14B L=32760",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded; RMSNorm + 3D RoPE Q/K, N(0,1) V, N(0,0.1^2) tangents, N(0,1) dO)",
+        "config": {
+            "workload": f"Wan2.1 self-attn fwd+JVP+bwd(dO-only) + text cross-attn fwd+JVP, one layer",
+            "B": 1, "H": H, "L": L, "D": D, "cross_keys": LKX,
+            "step_tflop": round(f_step / 1e12, 3),
+        },
+        "pct_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "ms_self_fwd_jvp_kernel": round(k_ms["fwd"], 3),
+        "ms_self_bwd_kernel": round(k_ms["bwd"], 3),
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": _traffic_from_profiles(dom_name),
+        },
+        "wall_s_timed": round(wall, 3),
+    }
+    if args.full_bwd:
+        o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+        dto = x["dto"]
+        jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, dto, s, False)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, dto, s, False)
+        b.record()
+        torch.cuda.synchronize()
+        out["ms_self_bwd_full"] = round(a.elapsed_time(b), 3)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(L, D, H, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

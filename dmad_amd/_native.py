@@ -46,6 +46,7 @@ SIGNATURES = {
                                  _P, _P, _I64P, _P, _P, _F, _P, _SZ, _P]),
     "dmad_attn_fwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
                              _I64P, _I64P, _I64P, _P, _I64P, _P, _F, _P, _SZ, _P]),
+    "dmad_set_kernel_events": (_INT, [_P, _P]),
     "dmad_attn_bwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _SZP]),
     "dmad_attn_jvp_bwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64,
                                  _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,

@@ -26,10 +26,11 @@
 //     statistics (log2-domain LSE, D or D', mu, rho) prepared by bwd_prep;
 //   * P and dS leave the score C tiles already in B-operand layout (perm32),
 //     so dK^T and dV^T accumulate in registers with no data movement;
-//   * dS is written to LDS as [query][key] and each wave then forms one 32-row
-//     slice of dQ^T = K^T dS^T over all 128 keys of the workgroup, added to a
-//     float32 dQ buffer with global atomics (one add per element per
-//     workgroup); a final pass scales and casts it.
+//   * dS is written to LDS as [query][key] and each wave then forms one
+//     32-column slice of dQ = dS K over all 128 keys of the workgroup, added to
+//     a float32 dQ buffer with global atomics (one add per element per
+//     workgroup, 32 consecutive floats per half-wave); a final pass scales and
+//     casts it.
 #pragma once
 #include "common.h"
 
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
       }
     }
   }
-  // ---- K^T (and Kd^T) slices for dQ^T = K^T dS^T: lane (d = 32*dblk + col, half)
+  // ---- K^T (and Kd^T) slices, the B operand of dQ = dS K: lane (d = 32*dblk + col, half)
   // holds K[kt*BK + 16*s + 8*half + e][d], e = 0..7, gathered 2 bytes at a time.
   i32x4_t ktreg[C::NDW][C::KSX], tktreg[C::NDW][C::KSX];
 #pragma unroll
@@ -384,7 +385,9 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
 
     __syncthreads();  // exchange tile complete
 
-    // ---- phase 4: dQ^T[dblk][q] = K^T dS^T (+ Kd^T dSd^T) over the 128 keys; atomics into dqacc
+    // ---- phase 4: dQ[q][dblk] = dS K (+ dSd Kd) over the 128 keys of the workgroup.
+    // A = dS rows from the exchange tile, B = K^T slices; the C tile has lane <-> d,
+    // so each atomic instruction covers two runs of 32 consecutive floats.
 #pragma unroll
     for (int m = 0; m < C::IPW; ++m) {
       const int item = wave + C::NW * m;
@@ -398,19 +401,18 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
 #pragma unroll
         for (int s = 0; s < C::KSX; ++s) {
           const int off = qi * (C::BK * 2) + (((2 * s + half) ^ (qi & 15)) << 4);
-          const i32x4_t bds = *(const i32x4_t*)(xch + off);
-          acc = mfma32(ktreg[di][s], bds, acc, T());
+          const i32x4_t ads = *(const i32x4_t*)(xch + off);
+          acc = mfma32(ads, ktreg[di][s], acc, T());
           if constexpr (FULL) {
-            const i32x4_t btds = *(const i32x4_t*)(xch + C::XCH_BYTES + off);
-            acc = mfma32(tktreg[di][s], btds, acc, T());
+            const i32x4_t atds = *(const i32x4_t*)(xch + C::XCH_BYTES + off);
+            acc = mfma32(atds, tktreg[di][s], acc, T());
           }
         }
-        const int qrow = qt * BMQ + qi;
-        float* dst = p.dqacc + ((int64_t)bh * p.LQP + qrow) * C::DP + dblk * 32 + 4 * half;
+        float* dst = p.dqacc + ((int64_t)bh * p.LQP + qt * BMQ + qb * 32 + 4 * half) * C::DP + dblk * 32 + col;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) atomicAdd(dst + 8 * j + r, acc[4 * j + r]);
+          for (int r = 0; r < 4; ++r) atomicAdd(dst + (8 * j + r) * C::DP, acc[4 * j + r]);
         }
       }
     }

@@ -34,6 +34,11 @@ template <> BwdLaunchFn bwd_select<_Float16, 256>(int);
 namespace {
 
 thread_local std::string g_last_error;
+thread_local hipEvent_t g_ev_before = nullptr, g_ev_after = nullptr;
+
+void mark(hipEvent_t ev, hipStream_t s) {
+  if (ev != nullptr) (void)hipEventRecord(ev, s);
+}
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -158,6 +163,13 @@ int dmad_abi_version(void) { return 1; }
 
 const char* dmad_last_error(void) { return g_last_error.c_str(); }
 
+int dmad_set_kernel_events(void* before, void* after) {
+  if ((before == nullptr) != (after == nullptr)) return fail(DMAD_ERR_INVALID, "set both events or neither");
+  g_ev_before = (hipEvent_t)before;
+  g_ev_after = (hipEvent_t)after;
+  return ok();
+}
+
 int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dv, size_t* bytes) {
   if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
   if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
@@ -252,7 +264,9 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   const int64_t nqt = (Lq + 127) / 128;
   if (nqt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  mark(g_ev_before, s);
   e = fn(p, (int)(nqt * BH), s);
+  mark(g_ev_after, s);
   if (e != hipSuccess) return fail(DMAD_ERR_HIP, "attention launch: %s", hipGetErrorString(e));
   return ok();
 }
@@ -411,6 +425,7 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   const int64_t nkt = (Lk + 127) / 128;
   if (nkt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  mark(g_ev_before, s);
   if ((e = fn(p, (int)(nkt * BH), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   if (tgrad) {
     // tangent gradients: the dO-only kernel with (dO, D) := (dOd, rho)
@@ -424,6 +439,7 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
     if ((e = fn_a(pt, (int)(nkt * BH), s)) != hipSuccess)
       return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   }
+  mark(g_ev_after, s);
   dmad::DqConvertParams cp{acc, dq, dq_strides[0], dq_strides[1], dq_strides[2], (int)H, (int)Lq, (int)lqp, (int)D, (int)dp, (int)BH, sm_scale};
   if ((e = dmad::launch_dq_convert(cp, dtype, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
   if (tgrad) {

@@ -77,8 +77,9 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
                   const int64_t v_strides[4], void* o, const int64_t o_strides[4], float* lse, float sm_scale,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Bytes of workspace dmad_attn_jvp_bwd needs. full != 0 selects the full
- * derivative (cotangent of the tangent output included). */
+/* Bytes of workspace dmad_attn_jvp_bwd needs. full: 0 = dO-only gradients,
+ * 1 = full derivative (dto given), 2 = full derivative plus tangent gradients
+ * (dto, dtq, dtk, dtv given). */
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes);
 
 /*
@@ -102,6 +103,16 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
                       void* dtq, void* dtk, void* dtv, const int64_t dq_strides[4], const int64_t dk_strides[4],
                       const int64_t dv_strides[4], float sm_scale, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/*
+ * Timing hook (no counterpart in the reference; for benchmarks and profilers
+ * that time one kernel live). While set, every dmad_attn_jvp_fwd /
+ * dmad_attn_fwd / dmad_attn_jvp_bwd call on this thread records `before` and
+ * `after` (hipEvent_t) on its stream immediately around its main attention
+ * kernel(s), excluding the layout and statistics passes around them.
+ * Pass NULL, NULL to stop.
+ */
+int dmad_set_kernel_events(void* before, void* after);
 
 #ifdef __cplusplus
 }
