@@ -37,6 +37,9 @@ def _args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--full-bwd", action="store_true", help="also time the full-derivative backward (extra field)")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after timing, run one elementwise kernel that reads and writes this many MiB "
+                         "(a known-size reference for HBM byte counters under a profiler)")
     return ap.parse_args()
 
 
@@ -208,6 +211,14 @@ def main():
         b.record()
         torch.cuda.synchronize()
         out["ms_self_bwd_full"] = round(a.elapsed_time(b), 3)
+    if args.calibration_copy_mib:
+        n = args.calibration_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)  # reads n*4 bytes, writes n*4 bytes
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(L, D, H, args.cpu_seconds)
     print(json.dumps(out), flush=True)

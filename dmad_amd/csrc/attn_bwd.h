@@ -16,6 +16,10 @@
 // and the tangent gradients dQd = s dSd K, dKd = s dSd^T Q, dVd = P^T dOd
 // are mode A with (dO, D) replaced by (dOd, rho).
 //
+// This file holds the key-stationary pass (dK, dV and, for the full
+// derivative, their Kd/Vd-independent sums); dQ comes from the query-stationary
+// pass in attn_bwd_dq.h, so no gradient needs atomics.
+//
 // Work decomposition (one workgroup = 4 waves = 128 keys of one head):
 //   * lane l of wave w owns key 32w + l%32; its K, V (and Kd, Vd) rows stay in
 //     registers as the B operand of S = Q K^T and dP = dO V^T, so the C tiles
@@ -26,11 +30,6 @@
 //     statistics (log2-domain LSE, D or D', mu, rho) prepared by bwd_prep;
 //   * P and dS leave the score C tiles already in B-operand layout (perm32),
 //     so dK^T and dV^T accumulate in registers with no data movement;
-//   * dS is written to LDS as [query][key] and each wave then forms one
-//     32-column slice of dQ = dS K over all 128 keys of the workgroup, added to
-//     a float32 dQ buffer with global atomics (one add per element per
-//     workgroup, 32 consecutive floats per half-wave); a final pass scales and
-//     casts it.
 #pragma once
 #include "common.h"
 
@@ -52,7 +51,6 @@ struct BwdParams {
   const void* doT;   // dO^T  [BH][DP][LQP]
   const void* dtoT;  // dOd^T [BH][DP][LQP] (mode B)
   const float* stats;  // [BH][LQP/BMQ][NSTAT][BMQ]
-  float* dqacc;        // [BH][LQP][DP], accumulates sum(dS K) (+ sum(dSd Kd))
   void* dk;
   void* dv;
   int64_t q_sb, q_sh, q_sl;  // shared by Q, Qd
@@ -86,16 +84,9 @@ struct BwdCfg {
   static constexpr int OFF_TR = NT * ROW_BYTES;
   static constexpr int OFF_STAT = OFF_TR + NT * TR_BYTES;
   static constexpr int STAGE = (OFF_STAT + STAT_BYTES + 1023) / 1024 * 1024;
-  static constexpr int XCH_BYTES = BMQ * BK * 2;  // one [BMQ][BK] bf16 exchange tile
-  static constexpr int NXCH = FULL ? 2 : 1;
-  static constexpr int LDS_BYTES = 2 * STAGE + NXCH * XCH_BYTES;
+  static constexpr int LDS_BYTES = 2 * STAGE;
   static constexpr int NRI = BMQ * CR / 64;  // wave-wide 1 KiB loads per row tile
   static constexpr int NTI = DP * CT / 64;   // ... per transposed tile
-  // dQ items: (d block, query block) pairs, dealt to the waves round-robin
-  static constexpr int NITEMS = DB * NQB;
-  static constexpr int IPW = (NITEMS + NW - 1) / NW;
-  static constexpr int NDW = DB > NW ? DB / NW : 1;  // distinct d blocks per wave
-  static constexpr int KSX = BK / 16;               // key slices of dQ^T = K^T dS^T
   static_assert(STAT_BYTES <= 1024, "statistics must fit one wave-wide load");
 };
 
@@ -105,7 +96,6 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
   constexpr int BMQ = C::BMQ, NQB = C::NQB, KS = C::KS, DB = C::DB, CR = C::CR, CT = C::CT;
   constexpr bool FULL = C::FULL;
   __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
-  char* xch = smem + 2 * C::STAGE;
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -144,36 +134,6 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
       }
     }
   }
-  // ---- K^T (and Kd^T) slices, the B operand of dQ = dS K: lane (d = 32*dblk + col, half)
-  // holds K[kt*BK + 16*s + 8*half + e][d], e = 0..7, gathered 2 bytes at a time.
-  i32x4_t ktreg[C::NDW][C::KSX], tktreg[C::NDW][C::KSX];
-#pragma unroll
-  for (int i = 0; i < C::NDW; ++i) {
-    const int dblk = (C::DB > C::NW) ? wave + C::NW * i : (wave % C::DB);
-    const int d = dblk * 32 + col;
-#pragma unroll
-    for (int s = 0; s < C::KSX; ++s) {
-      uint32_t w[4], tw[4];
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        uint32_t lohi[2], tlohi[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int kk = kt * C::BK + 16 * s + 8 * half + 2 * e2 + u;
-          const bool ok = (d < D) && (kk < p.Lk);
-          const uint32_t off = (uint32_t)((int64_t)(ok ? kk : 0) * p.k_sl * 2) + (ok ? d : 0) * 2;
-          lohi[u] = ok ? (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rk, (int)off, 0, 0) : 0u;
-          if constexpr (FULL)
-            tlohi[u] = ok ? (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rtk, (int)off, 0, 0) : 0u;
-        }
-        w[e2] = lohi[0] | (lohi[1] << 16);
-        if constexpr (FULL) tw[e2] = tlohi[0] | (tlohi[1] << 16);
-      }
-      ktreg[i][s] = i32x4_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-      if constexpr (FULL) tktreg[i][s] = i32x4_t{(int)tw[0], (int)tw[1], (int)tw[2], (int)tw[3]};
-    }
-  }
-
   // ---- DMA of one query tile into a stage
   const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
   const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
@@ -340,19 +300,6 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
             tdsb[qb][t][e2] = (int)Elem<T>::pack2(tdsv[2 * e2], tdsv[2 * e2 + 1]);
           }
         }
-        // dS (and dSd) -> exchange tile [query][key], 16-byte chunks XOR-swizzled by query
-        const int kl = wave * 32 + col;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int qi = q0 + e;
-          const int off = qi * (C::BK * 2) + (((kl >> 3) ^ (qi & 15)) << 4) + ((kl & 7) << 1);
-          const uint32_t w = (uint32_t)dsb[qb][t][e >> 1];
-          *(uint16_t*)(xch + off) = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff));
-          if constexpr (FULL) {
-            const uint32_t tw = (uint32_t)tdsb[qb][t][e >> 1];
-            *(uint16_t*)(xch + C::XCH_BYTES + off) = (uint16_t)((e & 1) ? (tw >> 16) : (tw & 0xffff));
-          }
-        }
       }
     }
 
@@ -383,39 +330,6 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
       }
     }
 
-    __syncthreads();  // exchange tile complete
-
-    // ---- phase 4: dQ[q][dblk] = dS K (+ dSd Kd) over the 128 keys of the workgroup.
-    // A = dS rows from the exchange tile, B = K^T slices; the C tile has lane <-> d,
-    // so each atomic instruction covers two runs of 32 consecutive floats.
-#pragma unroll
-    for (int m = 0; m < C::IPW; ++m) {
-      const int item = wave + C::NW * m;
-      if (item < C::NITEMS) {
-        const int dblk = item % DB, qb = item / DB;
-        const int di = (C::DB > C::NW) ? m % C::NDW : 0;
-        f32x16_t acc;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[v] = 0.f;
-        const int qi = qb * 32 + col;
-#pragma unroll
-        for (int s = 0; s < C::KSX; ++s) {
-          const int off = qi * (C::BK * 2) + (((2 * s + half) ^ (qi & 15)) << 4);
-          const i32x4_t ads = *(const i32x4_t*)(xch + off);
-          acc = mfma32(ads, ktreg[di][s], acc, T());
-          if constexpr (FULL) {
-            const i32x4_t atds = *(const i32x4_t*)(xch + C::XCH_BYTES + off);
-            acc = mfma32(atds, tktreg[di][s], acc, T());
-          }
-        }
-        float* dst = p.dqacc + ((int64_t)bh * p.LQP + qt * BMQ + qb * 32 + 4 * half) * C::DP + dblk * 32 + col;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) atomicAdd(dst + (8 * j + r) * C::DP, acc[4 * j + r]);
-        }
-      }
-    }
   }
 
   // ---- store dK = s (dK^T)^T, dV = (dV^T)^T for this lane's key
@@ -461,12 +375,5 @@ struct PrepParams {
   int H, Lq, LQP, D, BH, BA;
 };
 
-struct DqConvertParams {
-  const float* acc;  // [BH][LQP][DP]
-  void* dq;
-  int64_t sb, sh, sl;
-  int H, Lq, LQP, D, DP, BH;
-  float scale;
-};
 
 }  // namespace dmad

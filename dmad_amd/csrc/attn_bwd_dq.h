@@ -1,0 +1,294 @@
+// dQ (and, for the full derivative, the Qd contribution) of the attention
+// backward, as a query-stationary pass: no atomics, every dQ element is
+// written once by the workgroup that owns its query row.
+//
+//   dO-only (mode A):  dS = P*(dO V^T - D),             dQ = s dS K
+//   full    (mode B):  dS, dSd as in attn_bwd.h,         dQ = s(dS K + dSd Kd)
+// with P = exp2(s*log2(e) * Q K^T - lse2) recomputed from the saved LSE.
+//
+// Layout mirrors the forward kernel: one workgroup = 4 waves = 128 query rows
+// of one head; lane l of a wave owns query l%32, whose Q and dO (and Qd, dOd)
+// slices stay in registers as B operands of S^T = K Q^T and dP^T = V dO^T.
+// K, V (and Kd, Vd) rows and K^T (and Kd^T, from a transposed copy) stream
+// through a double-buffered LDS ring. dS^T leaves the score C tile in
+// B-operand layout (K rows are read in perm32 order), and dQ^T = K^T dS^T
+// accumulates in registers with lane <-> query, so the per-row statistics are
+// per-lane scalars.
+#pragma once
+#include "common.h"
+
+namespace dmad {
+
+struct DqParams {
+  const void* q;
+  const void* tq;
+  const void* dout;
+  const void* dto;
+  const void* k;
+  const void* tk;
+  const void* v;
+  const void* tv;
+  const void* kT;   // K^T  [BH][DP][LKP]
+  const void* tkT;  // Kd^T [BH][DP][LKP] (mode B)
+  const float* stats;  // per-row statistics in the layout of the key-stationary kernel
+  void* dq;
+  int64_t q_sb, q_sh, q_sl;     // shared by Q, Qd
+  int64_t do_sb, do_sh, do_sl;  // shared by dO, dOd
+  int64_t k_sb, k_sh, k_sl;     // shared by K, Kd
+  int64_t v_sb, v_sh, v_sl;     // shared by V, Vd
+  int64_t dq_sb, dq_sh, dq_sl;
+  int B, H, Lq, Lk, LQP, LKP;
+  int stat_tile;  // query tile of the statistics layout
+  float scale, scale_log2;
+};
+
+template <int D, int MODE>
+struct DqCfg {
+  static constexpr int NW = 4;
+  static constexpr int BM = 32 * NW;
+  static constexpr int DP = D < 32 ? 32 : D;
+  static constexpr bool FULL = MODE == 1;
+  static constexpr int BN = (FULL || D > 128) ? 32 : 64;
+  static constexpr int NB = BN / 32;
+  static constexpr int KS = D / 16;
+  static constexpr int DB = DP / 32;
+  static constexpr int CK = D / 8;   // chunks per K / V row
+  static constexpr int CT = BN / 8;  // chunks per K^T row
+  static constexpr int NROW = FULL ? 4 : 2;  // K, V [, Kd, Vd]
+  static constexpr int NTR = FULL ? 2 : 1;   // K^T [, Kd^T]
+  static constexpr int ROW_BYTES = BN * D * 2;
+  static constexpr int TR_BYTES = DP * BN * 2;
+  static constexpr int OFF_TR = NROW * ROW_BYTES;
+  static constexpr int STAGE = NROW * ROW_BYTES + NTR * TR_BYTES;
+  static constexpr int NRI = BN * CK / 64;
+  static constexpr int NTI = DP * CT / 64;
+  static constexpr int RPW = (NRI + NW - 1) / NW;
+  static constexpr int TPW = (NTI + NW - 1) / NW;
+  static constexpr int NSTAT = FULL ? 4 : 2;
+};
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(DqParams p) {
+  using C = DqCfg<D, MODE>;
+  constexpr int BN = C::BN, NB = C::NB, KS = C::KS, DB = C::DB, CK = C::CK, CT = C::CT;
+  constexpr bool FULL = C::FULL;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  // ---- per-lane query operands and statistics
+  const int qrow = qt * C::BM + wave * 32 + col;
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const char*)p.dout + (b * p.do_sb + h * p.do_sh) * 2, do_bytes);
+  i32x4_t qr[KS], dor[KS], tqr[KS], dtor[KS];
+  {
+    const uint32_t qo = (uint32_t)((int64_t)qrow * p.q_sl * 2) + half * 16;
+    const uint32_t oo = (uint32_t)((int64_t)qrow * p.do_sl * 2) + half * 16;
+    __amdgpu_buffer_rsrc_t rtq = rq, rdto = rdo;
+    if constexpr (FULL) {
+      rtq = make_rsrc((const char*)p.tq + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+      rdto = make_rsrc((const char*)p.dto + (b * p.do_sb + h * p.do_sh) * 2, do_bytes);
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qr[s] = buf_load16(rq, qo + s * 32);
+      dor[s] = buf_load16(rdo, oo + s * 32);
+      if constexpr (FULL) {
+        tqr[s] = buf_load16(rtq, qo + s * 32);
+        dtor[s] = buf_load16(rdto, oo + s * 32);
+      }
+    }
+  }
+  float lse2 = __builtin_inff(), dlt = 0.f, mu = 0.f, rho = 0.f;
+  if (qrow < p.LQP) {
+    const float* st = p.stats + ((int64_t)bh * (p.LQP / p.stat_tile) + qrow / p.stat_tile) * C::NSTAT * p.stat_tile +
+                      qrow % p.stat_tile;
+    lse2 = st[0];
+    dlt = st[p.stat_tile];
+    if constexpr (FULL) {
+      mu = st[2 * p.stat_tile];
+      rho = st[3 * p.stat_tile];
+    }
+  }
+
+  // ---- key-side resources and per-lane DMA offsets
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
+  const uint32_t kt_bytes = (uint32_t)((int64_t)C::DP * p.LKP * 2);
+  const __amdgpu_buffer_rsrc_t rrow[4] = {
+      make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes),
+      make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes),
+      make_rsrc((const char*)(FULL ? p.tk : p.k) + (b * p.k_sb + h * p.k_sh) * 2, k_bytes),
+      make_rsrc((const char*)(FULL ? p.tv : p.v) + (b * p.v_sb + h * p.v_sh) * 2, v_bytes)};
+  const __amdgpu_buffer_rsrc_t rtr[2] = {
+      make_rsrc((const char*)p.kT + (int64_t)bh * kt_bytes, kt_bytes),
+      make_rsrc((const char*)(FULL ? p.tkT : p.kT) + (int64_t)bh * kt_bytes, kt_bytes)};
+  const int64_t row_sl[4] = {p.k_sl, p.v_sl, p.k_sl, p.v_sl};
+  uint32_t roff_k[C::RPW], roff_v[C::RPW], toff[C::TPW];
+#pragma unroll
+  for (int j = 0; j < C::RPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CK, phys = pch % CK;
+    const int logical = phys ^ swz<CK>(perm32(row & 31) & 15);
+    roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
+    roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < C::TPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int d = pch / CT, phys = pch % CT;
+    const int logical = phys ^ swz<CT>(d & 15);
+    toff[j] = (uint32_t)(d * p.LKP * 2) + logical * 16;
+  }
+
+  auto issue_tile = [&](int kt, int stage) {
+    char* st = smem + stage * C::STAGE;
+#pragma unroll
+    for (int t = 0; t < C::NROW; ++t) {
+      const uint32_t rs = (uint32_t)((int64_t)kt * BN * row_sl[t] * 2);
+#pragma unroll
+      for (int j = 0; j < C::RPW; ++j) {
+        const int i = wave + j * C::NW;
+        if (i < C::NRI) buf_load16_lds(rrow[t], st + t * C::ROW_BYTES + i * 1024, (t & 1) ? roff_v[j] : roff_k[j], rs);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < C::NTR; ++t) {
+#pragma unroll
+      for (int j = 0; j < C::TPW; ++j) {
+        const int i = wave + j * C::NW;
+        if (i < C::NTI) buf_load16_lds(rtr[t], st + C::OFF_TR + t * C::TR_BYTES + i * 1024, toff[j], (uint32_t)kt * BN * 2);
+      }
+    }
+  };
+
+  const int rswz = swz<CK>(col & 15), tswz = swz<CT>(col & 15);
+  const int rrow_off = perm32(col) * CK * 16;
+  const int trow_off = col * CT * 16;
+
+  f32x16_t acc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[d][v] = 0.f;
+  }
+
+  const int ntiles = (p.Lk + BN - 1) / BN;
+  issue_tile(0, 0);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < ntiles) issue_tile(kt + 1, (kt + 1) & 1);
+    const char* st = smem + (kt & 1) * C::STAGE;
+
+    // ---- S^T, dP^T (and Sd^T, dPd^T) for BN keys x 32 queries
+    f32x16_t sacc[NB], dpacc[NB], tsacc[NB], dpdacc[NB];
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        sacc[kb][v] = 0.f;
+        dpacc[kb][v] = 0.f;
+        tsacc[kb][v] = 0.f;
+        dpdacc[kb][v] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) {
+        const int off = kb * 32 * CK * 16 + rrow_off + (((2 * s + half) ^ rswz) << 4);
+        const i32x4_t ak = *(const i32x4_t*)(st + off);
+        const i32x4_t av = *(const i32x4_t*)(st + C::ROW_BYTES + off);
+        sacc[kb] = mfma32(ak, qr[s], sacc[kb], T());
+        dpacc[kb] = mfma32(av, dor[s], dpacc[kb], T());
+        if constexpr (FULL) {
+          const i32x4_t atk = *(const i32x4_t*)(st + 2 * C::ROW_BYTES + off);
+          const i32x4_t atv = *(const i32x4_t*)(st + 3 * C::ROW_BYTES + off);
+          tsacc[kb] = mfma32(ak, tqr[s], tsacc[kb], T());
+          tsacc[kb] = mfma32(atk, qr[s], tsacc[kb], T());
+          dpacc[kb] = mfma32(atv, dtor[s], dpacc[kb], T());
+          dpdacc[kb] = mfma32(av, dtor[s], dpdacc[kb], T());
+        }
+      }
+    }
+
+    // ---- dS (and dSd); value v of block kb is key kt*BN + kb*32 + 16t + 8*half + e (v = 8t + e)
+    const bool tail = (kt + 1) * BN > p.Lk;
+    i32x4_t dsb[NB][2], tdsb[NB][2];
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float dsv[8], tdsv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int v = 8 * t + e;
+          float pe = fast_exp2(fmaf(sacc[kb][v], p.scale_log2, -lse2));
+          if (tail && kt * BN + kb * 32 + 16 * t + 8 * half + e >= p.Lk) pe = 0.f;
+          if constexpr (!FULL) {
+            dsv[e] = pe * (dpacc[kb][v] - dlt);
+          } else {
+            const float sd = tsacc[kb][v] * p.scale;
+            const float dpd = dpdacc[kb][v];
+            const float dp = dpacc[kb][v] + dpd * (sd - mu) - sd * rho;
+            dsv[e] = pe * (dp - dlt);
+            tdsv[e] = pe * (dpd - rho);
+          }
+        }
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          dsb[kb][t][e2] = (int)Elem<T>::pack2(dsv[2 * e2], dsv[2 * e2 + 1]);
+          if constexpr (FULL) tdsb[kb][t][e2] = (int)Elem<T>::pack2(tdsv[2 * e2], tdsv[2 * e2 + 1]);
+        }
+      }
+    }
+
+    // ---- dQ^T += K^T dS^T (+ Kd^T dSd^T)
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int ch = ((kb * 4 + 2 * t + half) ^ tswz) << 4;
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+          const int off = C::OFF_TR + d * 32 * CT * 16 + trow_off + ch;
+          const i32x4_t akt = *(const i32x4_t*)(st + off);
+          acc[d] = mfma32(akt, dsb[kb][t], acc[d], T());
+          if constexpr (FULL) {
+            const i32x4_t atkt = *(const i32x4_t*)(st + C::TR_BYTES + off);
+            acc[d] = mfma32(atkt, tdsb[kb][t], acc[d], T());
+          }
+        }
+      }
+    }
+  }
+
+  // ---- dQ = s (dQ^T)^T
+  if (qrow < p.Lq) {
+    char* dqp = (char*)p.dq + ((b * p.dq_sb + h * p.dq_sh) + (int64_t)qrow * p.dq_sl) * 2;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int dc = d * 32 + 8 * j + 4 * half;
+        if (D >= 32 || dc < D) {
+          u32x2_t w = {Elem<T>::pack2(acc[d][4 * j] * p.scale, acc[d][4 * j + 1] * p.scale),
+                       Elem<T>::pack2(acc[d][4 * j + 2] * p.scale, acc[d][4 * j + 3] * p.scale)};
+          *(u32x2_t*)(dqp + dc * 2) = w;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace dmad

@@ -97,30 +97,6 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepParams p) {
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void dq_convert_kernel(DqConvertParams p) {
-  const int per_row = p.D / 8;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)p.BH * p.Lq * per_row) return;
-  const int c = (int)(gid % per_row);
-  const int64_t r = gid / per_row;
-  const int bh = (int)(r / p.Lq), q = (int)(r - (int64_t)bh * p.Lq);
-  const int b = bh / p.H, h = bh - b * p.H;
-  const float* a = p.acc + ((int64_t)bh * p.LQP + q) * p.DP + c * 8;
-  const float4 x = *(const float4*)a, y = *(const float4*)(a + 4);
-  i32x4_t w;
-  w[0] = (int)Elem<T>::pack2(x.x * p.scale, x.y * p.scale);
-  w[1] = (int)Elem<T>::pack2(x.z * p.scale, x.w * p.scale);
-  w[2] = (int)Elem<T>::pack2(y.x * p.scale, y.y * p.scale);
-  w[3] = (int)Elem<T>::pack2(y.z * p.scale, y.w * p.scale);
-  *(i32x4_t*)((uint16_t*)p.dq + b * p.sb + h * p.sh + (int64_t)q * p.sl + c * 8) = w;
-}
-
-__global__ __launch_bounds__(256) void zero_kernel(float4* p, int64_t n4) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-}
-
 static int64_t blocks_for(int64_t n) { return (n + 255) / 256; }
 
 hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s) {
@@ -128,21 +104,6 @@ hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s) {
   if (nb == 0) return hipSuccess;
   if (dtype == 0) hipLaunchKernelGGL(bwd_prep_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, s, p);
   else hipLaunchKernelGGL(bwd_prep_kernel<_Float16>, dim3((unsigned)nb), dim3(256), 0, s, p);
-  return hipGetLastError();
-}
-
-hipError_t launch_dq_convert(const DqConvertParams& p, int dtype, hipStream_t s) {
-  const int64_t nb = blocks_for((int64_t)p.BH * p.Lq * (p.D / 8));
-  if (nb == 0) return hipSuccess;
-  if (dtype == 0) hipLaunchKernelGGL(dq_convert_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(dq_convert_kernel<_Float16>, dim3((unsigned)nb), dim3(256), 0, s, p);
-  return hipGetLastError();
-}
-
-hipError_t launch_zero(float* p, int64_t nfloats, hipStream_t s) {
-  const int64_t n4 = nfloats / 4;
-  if (n4 == 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks_for(n4)), dim3(256), 0, s, (float4*)p, n4);
   return hipGetLastError();
 }
 

@@ -23,6 +23,21 @@ static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <typename T, int D, int MODE>
+static hipError_t dq_launch(const DqParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <>
+DqLaunchFn dq_select<Elt, DMAD_D>(int mode) {
+  if (mode == kBwdDoutOnly) return &dq_launch<Elt, DMAD_D, kBwdDoutOnly>;
+#if DMAD_D <= 128
+  if (mode == kBwdFull) return &dq_launch<Elt, DMAD_D, kBwdFull>;
+#endif
+  return nullptr;
+}
+
 template <>
 BwdLaunchFn bwd_select<Elt, DMAD_D>(int mode) {
   if (mode == kBwdDoutOnly) return &bwd_launch<Elt, DMAD_D, kBwdDoutOnly>;

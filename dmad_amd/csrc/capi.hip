@@ -29,6 +29,16 @@ template <> BwdLaunchFn bwd_select<_Float16, 32>(int);
 template <> BwdLaunchFn bwd_select<_Float16, 64>(int);
 template <> BwdLaunchFn bwd_select<_Float16, 128>(int);
 template <> BwdLaunchFn bwd_select<_Float16, 256>(int);
+template <> DqLaunchFn dq_select<__bf16, 16>(int);
+template <> DqLaunchFn dq_select<__bf16, 32>(int);
+template <> DqLaunchFn dq_select<__bf16, 64>(int);
+template <> DqLaunchFn dq_select<__bf16, 128>(int);
+template <> DqLaunchFn dq_select<__bf16, 256>(int);
+template <> DqLaunchFn dq_select<_Float16, 16>(int);
+template <> DqLaunchFn dq_select<_Float16, 32>(int);
+template <> DqLaunchFn dq_select<_Float16, 64>(int);
+template <> DqLaunchFn dq_select<_Float16, 128>(int);
+template <> DqLaunchFn dq_select<_Float16, 256>(int);
 }  // namespace dmad
 
 namespace {
@@ -132,26 +142,49 @@ dmad::BwdLaunchFn pick_bwd(int dtype, int64_t d, int mode) {
   return nullptr;
 }
 
+dmad::DqLaunchFn pick_dq(int dtype, int64_t d, int mode) {
+  using namespace dmad;
+  if (dtype == DMAD_BF16) {
+    switch (d) {
+      case 16: return dq_select<__bf16, 16>(mode);
+      case 32: return dq_select<__bf16, 32>(mode);
+      case 64: return dq_select<__bf16, 64>(mode);
+      case 128: return dq_select<__bf16, 128>(mode);
+      case 256: return dq_select<__bf16, 256>(mode);
+    }
+  } else if (dtype == DMAD_F16) {
+    switch (d) {
+      case 16: return dq_select<_Float16, 16>(mode);
+      case 32: return dq_select<_Float16, 32>(mode);
+      case 64: return dq_select<_Float16, 64>(mode);
+      case 128: return dq_select<_Float16, 128>(mode);
+      case 256: return dq_select<_Float16, 256>(mode);
+    }
+  }
+  return nullptr;
+}
+
 // Backward workspace, carved in this order (each piece 256-byte aligned):
-//   transposed Q, dO [, Qd, dOd]   bf16/f16 [BH][DP][LQP] each
-//   statistics (A or B layout) [, BT layout]
-//   dQ accumulator fp32 [BH][LQP][DP] [, dQd accumulator]
+//   transposed Q, dO [, Qd, dOd]   [BH][DP][LQP] each (input dtype)
+//   transposed K [, Kd]            [BH][DP][LKP] each
+//   statistics (A or B layout) [, BT layout]   float32
 struct BwdWs {
-  int64_t tr, stats, stats_bt, acc, total;
-  int ntr;
+  int64_t trq, trk, stats, stats_bt, total;
+  int nq, nk;
   bool tgrad;
 };
 
-BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t D) {
-  const int64_t BH = B * H, dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64);
+BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) {
+  const int64_t BH = B * H, dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign);
   BwdWs w{};
-  w.ntr = full ? 4 : 2;
+  w.nq = full ? 4 : 2;
+  w.nk = full ? 2 : 1;
   w.tgrad = full == 2;
-  w.tr = round_up(BH * dp * lqp * 2, 256);
+  w.trq = round_up(BH * dp * lqp * 2, 256);
+  w.trk = round_up(BH * dp * lkp * 2, 256);
   w.stats = round_up(BH * lqp * (full ? 4 : 2) * 4, 256);
   w.stats_bt = w.tgrad ? round_up(BH * lqp * 2 * 4, 256) : 0;
-  w.acc = round_up(BH * lqp * dp * 4, 256);
-  w.total = w.ntr * w.tr + w.stats + w.stats_bt + w.acc * (w.tgrad ? 2 : 1);
+  w.total = w.nq * w.trq + w.nk * w.trk + w.stats + w.stats_bt;
   return w;
 }
 
@@ -281,11 +314,10 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
 }
 
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes) {
-  (void)Lk;
   if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
   if (full < 0 || full > 2) return fail(DMAD_ERR_INVALID, "full must be 0, 1 or 2");
-  if (B < 0 || H < 0 || Lq < 0 || !head_dim_ok(D)) return fail(DMAD_ERR_INVALID, "bad sizes");
-  *bytes = (size_t)bwd_ws(full, B, H, Lq, D).total;
+  if (B < 0 || H < 0 || Lq < 0 || Lk < 0 || !head_dim_ok(D)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  *bytes = (size_t)bwd_ws(full, B, H, Lq, Lk, D).total;
   return ok();
 }
 
@@ -334,36 +366,41 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
     if ((rc = check_operand("dtv", dtv, dv_strides, Lk, D))) return rc;
   }
   const int fl = full ? (tgrad ? 2 : 1) : 0;
-  const BwdWs w = bwd_ws(fl, B, H, Lq, D);
+  const BwdWs w = bwd_ws(fl, B, H, Lq, Lk, D);
   if (workspace == nullptr || (int64_t)workspace_bytes < w.total)
     return fail(DMAD_ERR_WORKSPACE, "workspace needs %lld bytes, got %lld", (long long)w.total, (long long)workspace_bytes);
   if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
-  const int64_t dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), BH = B * H;
-  if (dp * lqp * 2 >= kMaxHeadBytes || lqp * dp * 4 * BH >= ((int64_t)1 << 46)) return fail(DMAD_ERR_UNSUPPORTED, "Lq too large");
+  const int64_t dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign), BH = B * H;
+  if (dp * lqp * 2 >= kMaxHeadBytes || dp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "sequence too long");
   const int mode = full ? dmad::kBwdFull : dmad::kBwdDoutOnly;
   dmad::BwdLaunchFn fn = pick_bwd(dtype, D, mode);
+  dmad::DqLaunchFn fq = pick_dq(dtype, D, mode);
   dmad::BwdLaunchFn fn_a = tgrad ? pick_bwd(dtype, D, dmad::kBwdDoutOnly) : nullptr;
-  if (fn == nullptr || (tgrad && fn_a == nullptr)) return fail(DMAD_ERR_UNSUPPORTED, "no backward kernel for D=%lld", (long long)D);
+  dmad::DqLaunchFn fq_a = tgrad ? pick_dq(dtype, D, dmad::kBwdDoutOnly) : nullptr;
+  if (fn == nullptr || fq == nullptr || (tgrad && (fn_a == nullptr || fq_a == nullptr)))
+    return fail(DMAD_ERR_UNSUPPORTED, "no backward kernel for D=%lld", (long long)D);
 
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   char* trq = ws;
-  char* trdo = ws + w.tr;
-  char* trtq = full ? ws + 2 * w.tr : nullptr;
-  char* trdto = full ? ws + 3 * w.tr : nullptr;
-  float* stats = (float*)(ws + w.ntr * w.tr);
-  float* stats_bt = w.tgrad ? (float*)(ws + w.ntr * w.tr + w.stats) : nullptr;
-  float* acc = (float*)(ws + w.ntr * w.tr + w.stats + w.stats_bt);
-  float* tacc = w.tgrad ? acc + w.acc / 4 : nullptr;
+  char* trdo = ws + w.trq;
+  char* trtq = full ? ws + 2 * w.trq : nullptr;
+  char* trdto = full ? ws + 3 * w.trq : nullptr;
+  char* trk = ws + w.nq * w.trq;
+  char* trtk = full ? trk + w.trk : nullptr;
+  float* stats = (float*)(ws + w.nq * w.trq + w.nk * w.trk);
+  float* stats_bt = w.tgrad ? (float*)((char*)stats + w.stats) : nullptr;
 
   hipError_t e;
-  auto tr = [&](const void* x, const int64_t* st, char* y) {
-    dmad::TransposeParams tp{x, y, st[0], st[1], st[2], (int)H, (int)Lq, (int)D, (int)lqp, (int)dp};
+  auto tr = [&](const void* x, const int64_t* st, char* y, int64_t L, int64_t LP) {
+    dmad::TransposeParams tp{x, y, st[0], st[1], st[2], (int)H, (int)L, (int)D, (int)LP, (int)dp};
     return dmad::launch_transpose_pad(tp, (int)BH, s);
   };
-  if ((e = tr(q, q_strides, trq)) != hipSuccess || (e = tr(dout, do_strides, trdo)) != hipSuccess)
+  if ((e = tr(q, q_strides, trq, Lq, lqp)) != hipSuccess || (e = tr(dout, do_strides, trdo, Lq, lqp)) != hipSuccess ||
+      (e = tr(k, k_strides, trk, Lk, lkp)) != hipSuccess)
     return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
-  if (full && ((e = tr(tq, q_strides, trtq)) != hipSuccess || (e = tr(dto, do_strides, trdto)) != hipSuccess))
+  if (full && ((e = tr(tq, q_strides, trtq, Lq, lqp)) != hipSuccess || (e = tr(dto, do_strides, trdto, Lq, lqp)) != hipSuccess ||
+               (e = tr(tk, k_strides, trtk, Lk, lkp)) != hipSuccess))
     return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
 
   const int ba = dmad::bwd_bmq((int)D, dmad::kBwdDoutOnly);
@@ -390,9 +427,8 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
   pp.BH = (int)BH;
   pp.BA = ba;
   if ((e = dmad::launch_bwd_prep(pp, dtype, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "prep launch: %s", hipGetErrorString(e));
-  if ((e = dmad::launch_zero(acc, w.acc / 4 * (w.tgrad ? 2 : 1), s)) != hipSuccess)
-    return fail(DMAD_ERR_HIP, "zero launch: %s", hipGetErrorString(e));
 
+  // key-stationary pass: dK, dV
   dmad::BwdParams p{};
   p.q = q;
   p.k = k;
@@ -407,7 +443,6 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
   p.doT = trdo;
   p.dtoT = full ? trdto : trdo;
   p.stats = stats;
-  p.dqacc = acc;
   p.dk = dk;
   p.dv = dv;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_sl = q_strides[2];
@@ -423,30 +458,61 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
   p.LQP = (int)lqp;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
-  const int64_t nkt = (Lk + 127) / 128;
-  if (nkt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+
+  // query-stationary pass: dQ
+  dmad::DqParams pq{};
+  pq.q = q;
+  pq.tq = full ? tq : q;
+  pq.dout = dout;
+  pq.dto = full ? dto : dout;
+  pq.k = k;
+  pq.tk = full ? tk : k;
+  pq.v = v;
+  pq.tv = full ? tv : v;
+  pq.kT = trk;
+  pq.tkT = full ? trtk : trk;
+  pq.stats = stats;
+  pq.dq = dq;
+  pq.q_sb = q_strides[0]; pq.q_sh = q_strides[1]; pq.q_sl = q_strides[2];
+  pq.do_sb = do_strides[0]; pq.do_sh = do_strides[1]; pq.do_sl = do_strides[2];
+  pq.k_sb = k_strides[0]; pq.k_sh = k_strides[1]; pq.k_sl = k_strides[2];
+  pq.v_sb = v_strides[0]; pq.v_sh = v_strides[1]; pq.v_sl = v_strides[2];
+  pq.dq_sb = dq_strides[0]; pq.dq_sh = dq_strides[1]; pq.dq_sl = dq_strides[2];
+  pq.B = (int)B;
+  pq.H = (int)H;
+  pq.Lq = (int)Lq;
+  pq.Lk = (int)Lk;
+  pq.LQP = (int)lqp;
+  pq.LKP = (int)lkp;
+  pq.stat_tile = full ? 32 : ba;
+  pq.scale = sm_scale;
+  pq.scale_log2 = sm_scale * 1.4426950408889634f;
+
+  const int64_t nkt = (Lk + 127) / 128, nqt = (Lq + 127) / 128;
+  if (nkt * BH >= ((int64_t)1 << 31) || nqt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
   mark(g_ev_before, s);
   if ((e = fn(p, (int)(nkt * BH), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  if (nqt > 0 && (e = fq(pq, (int)(nqt * BH), s)) != hipSuccess)
+    return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
   if (tgrad) {
-    // tangent gradients: the dO-only kernel with (dO, D) := (dOd, rho)
+    // tangent gradients: the dO-only passes with (dO, D) := (dOd, rho)
     dmad::BwdParams pt = p;
     pt.dout = dto;
     pt.doT = trdto;
     pt.stats = stats_bt;
-    pt.dqacc = tacc;
     pt.dk = dtk;
     pt.dv = dtv;
     if ((e = fn_a(pt, (int)(nkt * BH), s)) != hipSuccess)
       return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+    dmad::DqParams pqt = pq;
+    pqt.dout = dto;
+    pqt.stats = stats_bt;
+    pqt.stat_tile = ba;
+    pqt.dq = dtq;
+    if (nqt > 0 && (e = fq_a(pqt, (int)(nqt * BH), s)) != hipSuccess)
+      return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
   }
   mark(g_ev_after, s);
-  dmad::DqConvertParams cp{acc, dq, dq_strides[0], dq_strides[1], dq_strides[2], (int)H, (int)Lq, (int)lqp, (int)D, (int)dp, (int)BH, sm_scale};
-  if ((e = dmad::launch_dq_convert(cp, dtype, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
-  if (tgrad) {
-    cp.acc = tacc;
-    cp.dq = dtq;
-    if ((e = dmad::launch_dq_convert(cp, dtype, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
-  }
   return ok();
 }
 

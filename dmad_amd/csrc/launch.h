@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include "attn_fwd.h"
 #include "attn_bwd.h"
+#include "attn_bwd_dq.h"
 
 namespace dmad {
 
@@ -20,12 +21,17 @@ typedef hipError_t (*BwdLaunchFn)(const BwdParams&, int grid, hipStream_t);
 template <typename T, int D>
 BwdLaunchFn bwd_select(int mode);
 
+typedef hipError_t (*DqLaunchFn)(const DqParams&, int grid, hipStream_t);
+
+// Launcher for attn_bwd_dq_kernel<T, D, MODE>, or nullptr if unsupported.
+template <typename T, int D>
+DqLaunchFn dq_select(int mode);
+
 // Query tile of the backward kernel (the layout of its statistics).
 inline int bwd_bmq(int d, int mode) { return (mode == kBwdFull || d > 128) ? 32 : 64; }
 
 hipError_t launch_transpose_pad(const TransposeParams& p, int BH, hipStream_t s);
 hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s);
-hipError_t launch_dq_convert(const DqConvertParams& p, int dtype, hipStream_t s);
-hipError_t launch_zero(float* p, int64_t nfloats, hipStream_t s);
+
 
 }  // namespace dmad
