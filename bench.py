@@ -127,26 +127,19 @@ def main():
     f_cross = 8.0 * H * L * LKX * D
     f_step = f_fwd + f_bwd + f_cross
 
-    ev = {name: [] for name in ("fwd", "bwd")}
+    timers = []
 
     def step(record):
-        def timed(name, fn):
-            if record:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                # torch creates the HIP events on first record; the library then
-                # re-records them around the kernel itself
-                a.record()
-                b.record()
-                _native.check(lib.dmad_set_kernel_events(a.cuda_event, b.cuda_event))
-                out = fn()
-                _native.check(lib.dmad_set_kernel_events(None, None))
-                ev[name].append((a, b))
-                return out
-            return fn()
-
-        o, to, lse, mu = timed("fwd", lambda: jvp_attention_forward(q, k, v, tq, tk, tv, s))
-        timed("bwd", lambda: jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s,
-                                                    False))
+        if record:
+            tf, tb = _native.KernelTimer(1), _native.KernelTimer(2)
+            timers.append((tf, tb))
+            with tf:
+                o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+            with tb:
+                jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
+        else:
+            o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+            jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
         jvp_attention_forward(q, kc, vc, tq, None, None, s)
 
     for _ in range(args.warmup):
@@ -161,12 +154,21 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = e0.elapsed_time(e1) / args.steps
-    k_ms = {n: sum(a.elapsed_time(b) for a, b in lst) / len(lst) for n, lst in ev.items()}
+    k_ms = {"fwd": 0.0, "bwd_dkdv": 0.0, "bwd_dq": 0.0}
+    for tf, tb in timers:
+        k_ms["fwd"] += tf.elapsed()[0] / len(timers)
+        b = tb.elapsed()
+        k_ms["bwd_dkdv"] += b[0] / len(timers)
+        k_ms["bwd_dq"] += b[1] / len(timers)
     value = f_step / (ms_step * 1e-3) / 1e12
 
+    # algorithmic flops of each main kernel (GEMM flops it must do, counting the
+    # S and dP recomputation of the dQ pass)
+    k_flops = {"fwd": f_fwd, "bwd_dkdv": 8.0 * H * L * L * D, "bwd_dq": 6.0 * H * L * L * D}
+    k_names = {"fwd": "attn_fwd_kernel<bf16,128,128,jvp>", "bwd_dkdv": "attn_bwd_kernel<bf16,128,dout_only>",
+               "bwd_dq": "attn_bwd_dq_kernel<bf16,128,dout_only>"}
     dom = max(k_ms, key=k_ms.get)
-    dom_flops = {"fwd": f_fwd, "bwd": f_bwd}[dom]
-    dom_name = {"fwd": "attn_fwd_kernel<bf16,128,128,jvp>", "bwd": "attn_bwd_kernel<bf16,128,dout_only>"}[dom]
+    dom_flops, dom_name = k_flops[dom], k_names[dom]
     achieved = dom_flops / (k_ms[dom] * 1e-3) / 1e12
     out = {
         "metric": "attn fwd+JVP+bwd TFLOP/s & %MFMA peak; ms/layer at Wan2.1-14B L=32760",
@@ -188,7 +190,10 @@ def main():
         },
         "pct_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "ms_self_fwd_jvp_kernel": round(k_ms["fwd"], 3),
-        "ms_self_bwd_kernel": round(k_ms["bwd"], 3),
+        "ms_self_bwd_dkdv_kernel": round(k_ms["bwd_dkdv"], 3),
+        "ms_self_bwd_dq_kernel": round(k_ms["bwd_dq"], 3),
+        "kernel_pct_peak": {n: round(100 * k_flops[n] / (k_ms[n] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
+                            for n in k_ms},
         "roofline": {
             "kernel": dom_name,
             "bound": "mfma",

@@ -46,7 +46,7 @@ SIGNATURES = {
                                  _P, _P, _I64P, _P, _P, _F, _P, _SZ, _P]),
     "dmad_attn_fwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
                              _I64P, _I64P, _I64P, _P, _I64P, _P, _F, _P, _SZ, _P]),
-    "dmad_set_kernel_events": (_INT, [_P, _P]),
+    "dmad_set_kernel_events": (_INT, [ctypes.POINTER(ctypes.c_void_p), _INT]),
     "dmad_attn_bwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _SZP]),
     "dmad_attn_jvp_bwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64,
                                  _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
@@ -104,6 +104,35 @@ def ptr(t):
 
 def stream_ptr(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class KernelTimer:
+    """Times the main kernels of the next library calls with HIP events.
+
+    Use as a context manager around one call: `timer.ms[i]` is then the
+    duration of its i-th main kernel (see dmad_set_kernel_events).
+    """
+
+    def __init__(self, nkernels: int):
+        self.n = nkernels
+        self.events = []
+        self.ms = []
+
+    def __enter__(self):
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * self.n)]
+        for e in self.events:  # torch creates the HIP event on first record
+            e.record()
+        arr = (ctypes.c_void_p * len(self.events))(*[e.cuda_event for e in self.events])
+        check(lib().dmad_set_kernel_events(arr, len(self.events)))
+        return self
+
+    def __exit__(self, *exc):
+        check(lib().dmad_set_kernel_events(None, 0))
+        return False
+
+    def elapsed(self):
+        """Per-kernel milliseconds (synchronises on the events)."""
+        return [self.events[2 * i].elapsed_time(self.events[2 * i + 1]) for i in range(self.n)]
 
 
 def dtype_code(dtype: torch.dtype) -> int:

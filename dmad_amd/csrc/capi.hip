@@ -44,10 +44,14 @@ template <> DqLaunchFn dq_select<_Float16, 256>(int);
 namespace {
 
 thread_local std::string g_last_error;
-thread_local hipEvent_t g_ev_before = nullptr, g_ev_after = nullptr;
+constexpr int kMaxEvents = 8;
+thread_local hipEvent_t g_events[kMaxEvents];
+thread_local int g_nevents = 0;
 
-void mark(hipEvent_t ev, hipStream_t s) {
-  if (ev != nullptr) (void)hipEventRecord(ev, s);
+// Records the before (after == false) or after event of main kernel `i`.
+void mark(int i, bool after, hipStream_t s) {
+  const int e = 2 * i + (after ? 1 : 0);
+  if (e < g_nevents && g_events[e] != nullptr) (void)hipEventRecord(g_events[e], s);
 }
 
 int fail(int code, const char* fmt, ...) {
@@ -196,10 +200,12 @@ int dmad_abi_version(void) { return 1; }
 
 const char* dmad_last_error(void) { return g_last_error.c_str(); }
 
-int dmad_set_kernel_events(void* before, void* after) {
-  if ((before == nullptr) != (after == nullptr)) return fail(DMAD_ERR_INVALID, "set both events or neither");
-  g_ev_before = (hipEvent_t)before;
-  g_ev_after = (hipEvent_t)after;
+int dmad_set_kernel_events(void* const* events, int count) {
+  if (count < 0 || count > kMaxEvents || (count % 2) != 0)
+    return fail(DMAD_ERR_INVALID, "count must be an even number in [0, %d]", kMaxEvents);
+  if (count > 0 && events == nullptr) return fail(DMAD_ERR_INVALID, "events: null pointer");
+  for (int i = 0; i < count; ++i) g_events[i] = (hipEvent_t)events[i];
+  g_nevents = count;
   return ok();
 }
 
@@ -297,9 +303,9 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   const int64_t nqt = (Lq + 127) / 128;
   if (nqt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
-  mark(g_ev_before, s);
+  mark(0, false, s);
   e = fn(p, (int)(nqt * BH), s);
-  mark(g_ev_after, s);
+  mark(0, true, s);
   if (e != hipSuccess) return fail(DMAD_ERR_HIP, "attention launch: %s", hipGetErrorString(e));
   return ok();
 }
@@ -490,10 +496,13 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
 
   const int64_t nkt = (Lk + 127) / 128, nqt = (Lq + 127) / 128;
   if (nkt * BH >= ((int64_t)1 << 31) || nqt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
-  mark(g_ev_before, s);
+  mark(0, false, s);
   if ((e = fn(p, (int)(nkt * BH), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  mark(0, true, s);
+  mark(1, false, s);
   if (nqt > 0 && (e = fq(pq, (int)(nqt * BH), s)) != hipSuccess)
     return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
+  mark(1, true, s);
   if (tgrad) {
     // tangent gradients: the dO-only passes with (dO, D) := (dOd, rho)
     dmad::BwdParams pt = p;
@@ -502,17 +511,20 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
     pt.stats = stats_bt;
     pt.dk = dtk;
     pt.dv = dtv;
+    mark(2, false, s);
     if ((e = fn_a(pt, (int)(nkt * BH), s)) != hipSuccess)
       return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+    mark(2, true, s);
     dmad::DqParams pqt = pq;
     pqt.dout = dto;
     pqt.stats = stats_bt;
     pqt.stat_tile = ba;
     pqt.dq = dtq;
+    mark(3, false, s);
     if (nqt > 0 && (e = fq_a(pqt, (int)(nqt * BH), s)) != hipSuccess)
       return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
+    mark(3, true, s);
   }
-  mark(g_ev_after, s);
   return ok();
 }
 

@@ -106,13 +106,15 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
 
 /*
  * Timing hook (no counterpart in the reference; for benchmarks and profilers
- * that time one kernel live). While set, every dmad_attn_jvp_fwd /
- * dmad_attn_fwd / dmad_attn_jvp_bwd call on this thread records `before` and
- * `after` (hipEvent_t) on its stream immediately around its main attention
- * kernel(s), excluding the layout and statistics passes around them.
- * Pass NULL, NULL to stop.
+ * that time kernels live). `events` points to `count` hipEvent_t handles; while
+ * set, every dmad_attn_jvp_fwd / dmad_attn_fwd / dmad_attn_jvp_bwd call on
+ * this thread records events[2i] and events[2i+1] on its stream immediately
+ * before and after its i-th main kernel, excluding the layout and statistics
+ * passes. Main kernels in order: forward -> {attention}; backward -> {dK/dV
+ * pass, dQ pass[, tangent dK/dV pass, tangent dQ pass]}. Kernels without a
+ * pair of events are not timed. count = 0 (events may be NULL) stops.
  */
-int dmad_set_kernel_events(void* before, void* after);
+int dmad_set_kernel_events(void* const* events, int count);
 
 #ifdef __cplusplus
 }

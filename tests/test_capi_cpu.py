@@ -95,3 +95,14 @@ def test_workspace_query(nat):
     assert n.value == 40 * 128 * 32768 * 2
     assert nat.lib().dmad_attn_fwd_workspace_bytes(0, 1, 1, 10, 16, ctypes.byref(n)) == 0
     assert n.value == 32 * 64 * 2  # Dv < 32 pads to 32 rows, keys pad to 64
+
+
+def test_kernel_event_hook_validates(nat):
+    lib = nat.lib()
+    assert lib.dmad_set_kernel_events(None, 0) == 0
+    assert lib.dmad_set_kernel_events(None, 2) == 1
+    arr = (ctypes.c_void_p * 3)(None, None, None)
+    assert lib.dmad_set_kernel_events(arr, 3) == 1
+    arr = (ctypes.c_void_p * 10)()
+    assert lib.dmad_set_kernel_events(arr, 10) == 1
+    assert lib.dmad_set_kernel_events(None, 0) == 0
