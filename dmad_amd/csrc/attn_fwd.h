@@ -28,6 +28,8 @@
 // produced by transpose_pad_kernel; that costs one extra HBM pass over V and
 // Vd, far below the O(L^2) work of the pass itself.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace dmad {
@@ -53,8 +55,357 @@ struct FwdParams {
   float scale_log2;  // s * log2(e)
 };
 
+// Rescale threshold (log2 units): the running max used for exp2 only moves when
+// a row's tile max exceeds it by more than this, so the accumulators are
+// rescaled only on those (rare) steps and P~ <= 2^8. bf16 shares fp32's
+// exponent range; fp16 keeps the exact running max (P~ <= 1, H~ bounded as in
+// the reference) so nothing new can overflow.
+template <typename T> struct RescaleSlack { static constexpr float value = 8.0f; };
+template <> struct RescaleSlack<_Float16> { static constexpr float value = 0.0f; };
+
 template <int DQK, int DV, int MODE>
 struct FwdCfg {
+  static constexpr int NW = 8;         // waves per workgroup, 2 per SIMD
+  static constexpr int QW = 16;        // query rows per wave
+  static constexpr int BM = QW * NW;   // query rows per workgroup
+  static constexpr int DVP = DV;       // V^T rows read (16-row MFMA blocks)
+  static constexpr int VT_ROWS = DV < 32 ? 32 : DV;  // rows per head of the V^T workspace
+  static constexpr int BN = 32;        // keys per pipeline step (two 16-key score blocks)
+  static constexpr int KS = DQK / 32;  // 32-wide k slices of Q K^T
+  static constexpr int DB = DV / 16;   // 16-row blocks of O^T
+  static constexpr int CK = DQK / 8;   // 16-byte chunks per K row
+  static constexpr int CV = BN / 8;    // 16-byte chunks per V^T row
+  static constexpr bool JVP = MODE != kFwdPlain;
+  static constexpr bool KVT = MODE == kFwdJvp;
+  static constexpr int K_BYTES = BN * DQK * 2;
+  static constexpr int V_BYTES = DVP * BN * 2;
+  static constexpr int OFF_K = 0;
+  static constexpr int OFF_V = K_BYTES;
+  static constexpr int OFF_KT = K_BYTES + V_BYTES;
+  static constexpr int OFF_VT = 2 * K_BYTES + V_BYTES;
+  static constexpr int STAGE = (KVT ? 2 : 1) * (K_BYTES + V_BYTES);
+  static constexpr int NSTAGE = 4;  // tiles i-1 (V), i (V), i+1 (K) in use, i+2 landing
+  // this kernel needs 32-wide score slices and a four-stage ring that fits the LDS
+  static constexpr bool FITS = DQK >= 32 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr int NKI = BN * CK / 64;   // wave-wide 1 KiB loads per K tile
+  static constexpr int NVI = DVP * CV / 64;  // ... per V^T tile
+  static constexpr int KPW = (NKI + NW - 1) / NW;
+  static constexpr int VPW = (NVI + NW - 1) / NW;
+};
+
+// Key row of score block b (0, 1), MFMA row r (0..15), inside a 32-key tile.
+// Lane group g (rows 4g..4g+3) of block b then holds keys 8g + 4b + v, so the
+// two blocks together give each lane group 8 consecutive keys: the B-operand
+// layout of the following 32-key P V^T product, with no data movement.
+__device__ __forceinline__ int key_of_row16(int b, int r) { return ((r >> 2) << 3) + (b << 2) + (r & 3); }
+
+// XOR swizzle of the 16-byte chunk index of K-tile row R (0..31) for C chunks
+// per row: the 16 rows one lane group reads (fixed b, r = 0..15) land in 16
+// distinct 16-byte slots of the 256-byte LDS bank window.
+template <int C>
+__device__ __forceinline__ int kswz16(int R) {
+  const int u = ((R >> 1) & 12) | (R & 3);  // distinct for the 16 rows of either block
+  if constexpr (C >= 16) return u;
+  else if constexpr (C == 8) return u >> 1;
+  else return (u >> 2) & (C - 1);
+}
+
+// Value held by lane l^16, via v_permlane16_swap (rows of 16 lanes swap pairwise).
+__device__ __forceinline__ float other_row16(float x) {
+  uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+
+// Software pipeline over 32-key tiles, step i:
+//   top      wait for tile i+1's DMA, barrier, start the DMA of tile i+2
+//   phase A  MFMA: O~^T, C~^T += V^T P^T ... of tile i-1  ||  VALU: softmax of tile i
+//   phase B  MFMA: S^T, Sd^T of tile i+1 (overwrites tile i's score registers)
+// Each wave owns 16 query rows (lane l <-> query l%16); two waves share a SIMD,
+// so one wave's MFMA chain runs while the other waits on LDS or does softmax.
+template <typename T, int DQK, int DV, int MODE>
+__global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
+  struct C : FwdCfg<DQK, DV, MODE> {
+    static constexpr float rescale_log2() { return RescaleSlack<T>::value; }
+  };
+  constexpr int BN = C::BN, KS = C::KS, DB = C::DB, CK = C::CK, CV = C::CV, NST = C::NSTAGE;
+  __shared__ __attribute__((aligned(1024))) char smem[NST * C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  const char* qbase = (const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2;
+  const char* kbase = (const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2;
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + DQK) * 2);
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + DQK) * 2);
+  const uint32_t vt_bytes = (uint32_t)((int64_t)C::VT_ROWS * p.LKP * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, q_bytes);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.vt + (int64_t)bh * vt_bytes, vt_bytes);
+  __amdgpu_buffer_rsrc_t rtq = rq, rtk = rk, rtv = rv;
+  if constexpr (C::JVP) rtq = make_rsrc((const char*)p.tq + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  if constexpr (C::KVT) {
+    rtk = make_rsrc((const char*)p.tk + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+    rtv = make_rsrc((const char*)p.tvt + (int64_t)bh * vt_bytes, vt_bytes);
+  }
+
+  // ---- Q (and Qd) slices in registers: B operand of S^T = K Q^T
+  const int qrow = qt * C::BM + wave * C::QW + col;
+  const uint32_t qoff = (uint32_t)((int64_t)qrow * p.q_sl * 2) + grp * 16;
+  i32x4_t qr[KS], tqr[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qr[s] = buf_load16(rq, qoff + s * 64);
+    if constexpr (C::JVP) tqr[s] = buf_load16(rtq, qoff + s * 64);
+  }
+
+  // ---- per-lane DMA offsets (tile independent)
+  uint32_t koff[C::KPW], voff[C::VPW];
+#pragma unroll
+  for (int j = 0; j < C::KPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CK, phys = pch % CK;
+    const int logical = phys ^ kswz16<CK>(row);
+    koff[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < C::VPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int d = pch / CV, phys = pch % CV;
+    const int logical = phys ^ swz<CV>(d & 15);
+    voff[j] = (uint32_t)(d * p.LKP * 2) + logical * 16;
+  }
+  const uint32_t k_tile_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
+
+  auto stage_ptr = [&](int kt) -> const char* { return smem + (kt & (NST - 1)) * C::STAGE; };
+  auto issue_tile = [&](int kt) {
+    char* st = smem + (kt & (NST - 1)) * C::STAGE;
+    const uint32_t ks = (uint32_t)kt * k_tile_step;
+    const uint32_t vs = (uint32_t)kt * BN * 2;
+#pragma unroll
+    for (int j = 0; j < C::KPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NKI) {
+        buf_load16_lds(rk, st + C::OFF_K + i * 1024, koff[j], ks);
+        if constexpr (C::KVT) buf_load16_lds(rtk, st + C::OFF_KT + i * 1024, koff[j], ks);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::VPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NVI) {
+        buf_load16_lds(rv, st + C::OFF_V + i * 1024, voff[j], vs);
+        if constexpr (C::KVT) buf_load16_lds(rtv, st + C::OFF_VT + i * 1024, voff[j], vs);
+      }
+    }
+  };
+
+  // ---- LDS read offsets (tile independent)
+  int krow_off[2], kswzv[2];
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    const int R = key_of_row16(sb, col);
+    krow_off[sb] = R * CK * 16;
+    kswzv[sb] = kswz16<CK>(R);
+  }
+  const int vrow_off = col * CV * 16 + ((grp ^ swz<CV>(col)) << 4);
+
+  f32x4_t oacc[DB], cacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      oacc[d][v] = 0.f;
+      cacc[d][v] = 0.f;
+    }
+  }
+  float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
+  const int ntiles = (p.Lk + BN - 1) / BN;
+
+  // S^T (and Sd^T) of one 32-key tile: two 16-key blocks, A = K rows from LDS, B = Q slices
+  f32x4_t sc[2], tc[2];
+  auto scores = [&](const char* st) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int off = krow_off[sb] + (((4 * s + grp) ^ kswzv[sb]) << 4);
+        const i32x4_t ak = *(const i32x4_t*)(st + C::OFF_K + off);
+        if (s == 0) {
+          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+          sc[sb] = mfma16(ak, qr[0], z, T());
+          if constexpr (C::JVP) tc[sb] = mfma16(ak, tqr[0], z, T());
+        } else {
+          sc[sb] = mfma16(ak, qr[s], sc[sb], T());
+          if constexpr (C::JVP) tc[sb] = mfma16(ak, tqr[s], tc[sb], T());
+        }
+        if constexpr (C::KVT) {
+          const i32x4_t akt = *(const i32x4_t*)(st + C::OFF_KT + off);
+          tc[sb] = mfma16(akt, qr[s], tc[sb], T());
+        }
+      }
+    }
+  };
+
+  // Online softmax of one tile (log2 domain; the 4 lane groups of a query share m).
+  // Leaves P~ and H~ packed as B operands (keys 8*grp + e in pk, hk) and returns
+  // the accumulator rescale factor (1 when the running max did not move).
+  auto softmax = [&](int kt, auto TAIL, i32x4_t& pk, i32x4_t& hk) -> float {
+    if constexpr (decltype(TAIL)::value) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          if (kt * BN + 8 * grp + 4 * sb + v >= p.Lk) sc[sb][v] = -__builtin_inff();
+        }
+      }
+    }
+    float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    mx = fmaxf(mx, other_row16(mx));
+    mx = fmaxf(mx, other_half(mx)) * p.scale_log2;
+    const bool moved = __builtin_amdgcn_ballot_w64(mx > m_i + C::rescale_log2()) != 0;
+    const float m_new = moved ? fmaxf(m_i, mx) : m_i;
+    const float alpha = fast_exp2(m_i - m_new);
+    m_i = m_new;
+    const float neg_m = -m_new;
+    float pv[8], hv[8], ls = 0.f, rs = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sb = e >> 2, v = e & 3;
+      pv[e] = fast_exp2(fmaf(sc[sb][v], p.scale_log2, neg_m));
+      ls += pv[e];
+      if constexpr (C::JVP) {
+        hv[e] = pv[e] * (tc[sb][v] * p.scale);
+        rs += hv[e];
+      }
+    }
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      pk[e2] = (int)Elem<T>::pack2(pv[2 * e2], pv[2 * e2 + 1]);
+      if constexpr (C::JVP) hk[e2] = (int)Elem<T>::pack2(hv[2 * e2], hv[2 * e2 + 1]);
+    }
+    l_i = l_i * alpha + ls;
+    if constexpr (C::JVP) r_i = r_i * alpha + rs;
+    return alpha;
+  };
+
+  auto rescale = [&](float alpha) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        oacc[d][v] *= alpha;
+        if constexpr (C::JVP) cacc[d][v] *= alpha;
+      }
+    }
+  };
+
+  // O~^T += V^T P^T ; C~^T += Vd^T P^T + V^T H^T  (one 32-key MFMA per 16-row d block)
+  auto pv_update = [&](const char* st, const i32x4_t& pk, const i32x4_t& hk) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int off = d * 16 * CV * 16 + vrow_off;
+      const i32x4_t av = *(const i32x4_t*)(st + C::OFF_V + off);
+      oacc[d] = mfma16(av, pk, oacc[d], T());
+      if constexpr (C::KVT) {
+        const i32x4_t avt = *(const i32x4_t*)(st + C::OFF_VT + off);
+        cacc[d] = mfma16(avt, pk, cacc[d], T());
+      }
+      if constexpr (C::JVP) cacc[d] = mfma16(av, hk, cacc[d], T());
+    }
+  };
+
+  // ---- prologue: tiles 0..2 in flight, scores + softmax of tile 0, scores of tile 1
+  issue_tile(0);
+  if (ntiles > 1) issue_tile(1);
+  if (ntiles > 2) issue_tile(2);
+  wait_vmem();
+  __syncthreads();
+  i32x4_t pk, hk;
+  scores(stage_ptr(0));
+  if (ntiles == 1) {
+    softmax(0, std::true_type(), pk, hk);  // accumulators are still zero
+  } else {
+    softmax(0, std::false_type(), pk, hk);
+    scores(stage_ptr(1));
+  }
+  // ---- steady state: step i runs PV of tile i-1, softmax of tile i, scores of tile i+1
+  int i = 1;
+  for (; i + 1 < ntiles; ++i) {
+    wait_vmem();
+    __syncthreads();
+    if (i + 2 < ntiles) issue_tile(i + 2);  // reuses the stage of tile i-2
+    i32x4_t pn, hn;
+    pv_update(stage_ptr(i - 1), pk, hk);
+    const float alpha = softmax(i, std::false_type(), pn, hn);
+    scores(stage_ptr(i + 1));
+    rescale(alpha);  // unconditional: keeps the whole step one basic block
+    pk = pn;
+    hk = hn;
+  }
+  // ---- last step: tile ntiles-1 may hold keys >= Lk
+  if (ntiles > 1) {
+    i32x4_t pn, hn;
+    pv_update(stage_ptr(i - 1), pk, hk);
+    const float alpha = softmax(i, std::true_type(), pn, hn);
+    rescale(alpha);
+    pk = pn;
+    hk = hn;
+  }
+  pv_update(stage_ptr(ntiles - 1), pk, hk);
+
+  // ---- epilogue: lane (query col, group g) holds d = 16*dblk + 4g + v
+  float l = l_i + other_row16(l_i);
+  l = l + other_half(l);
+  const float inv_l = 1.0f / l;
+  float mu = 0.f;
+  if constexpr (C::JVP) {
+    float r = r_i + other_row16(r_i);
+    r = r + other_half(r);
+    mu = r * inv_l;
+  }
+  const int64_t obase = b * p.o_sb + h * p.o_sh;
+  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + DV) * 2);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
+  __amdgpu_buffer_rsrc_t rto = ro;
+  if constexpr (C::JVP) rto = make_rsrc((char*)p.to + obase * 2, o_bytes);
+  const uint32_t orow = (uint32_t)((int64_t)qrow * p.o_sl * 2);
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+    const int dc = d * 16 + 4 * grp;
+    float ov[4], tv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      ov[v] = oacc[d][v] * inv_l;
+      if constexpr (C::JVP) tv[v] = cacc[d][v] * inv_l - mu * ov[v];
+    }
+    const uint32_t off = orow + dc * 2;
+    u32x2_t w = {Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])};
+    buf_store8(ro, w, off);
+    if constexpr (C::JVP) {
+      u32x2_t wt = {Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])};
+      buf_store8(rto, wt, off);
+    }
+  }
+  if (grp == 0 && qrow < p.Lq) {
+    const int64_t si = (int64_t)bh * p.Lq + qrow;
+    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    if constexpr (C::JVP) p.mu[si] = mu;
+  }
+}
+
+// Single-stage-per-tile variant for head dims whose four-stage ring does not
+// fit in LDS (a 256-wide Q/K or V head in the full JVP mode): scores, softmax
+// and PV of each 64- or 32-key tile run back to back.
+template <int DQK, int DV, int MODE>
+struct FwdSimpleCfg {
   static constexpr int NW = 4;
   static constexpr int BM = 32 * NW;
   static constexpr int DVP = DV < 32 ? 32 : DV;
@@ -77,12 +428,11 @@ struct FwdCfg {
   static constexpr int NVI = DVP * CV / 64;  // ... per V^T tile
   static constexpr int KPW = (NKI + NW - 1) / NW;
   static constexpr int VPW = (NVI + NW - 1) / NW;
-  static constexpr int LKP_ALIGN = 64;  // V^T rows are padded to this many keys
 };
 
 template <typename T, int DQK, int DV, int MODE>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(FwdParams p) {
-  using C = FwdCfg<DQK, DV, MODE>;
+__global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
+  using C = FwdSimpleCfg<DQK, DV, MODE>;
   constexpr int BN = C::BN, NB = C::NB, KS = C::KS, DB = C::DB, CK = C::CK, CV = C::CV;
   __shared__ __attribute__((aligned(1024))) char smem[2 * C::STAGE];
 

@@ -17,6 +17,7 @@ namespace dmad {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
@@ -89,6 +90,18 @@ __device__ __forceinline__ f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c, _Fl
                                                 c, 0, 0, 0);
 }
 
+// 16x16x32 layouts: A (16 x 32): lane l holds row l%16, k = 8*(l/16) + e;
+// B (32 x 16): lane l holds col l%16, k = 8*(l/16) + e;
+// C (16 x 16): lane l holds col l%16, rows 4*(l/16) + v, v = 0..3.
+__device__ __forceinline__ f32x4_t mfma16(i32x4_t a, i32x4_t b, f32x4_t c, __bf16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16(i32x4_t a, i32x4_t b, f32x4_t c, _Float16) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                c, 0, 0, 0);
+}
+
 // ---------------------------------------------------------------- lane helpers
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
@@ -110,16 +123,20 @@ __device__ __forceinline__ int perm32(int i) {
 // XOR swizzle of the 16-byte chunk index for an LDS tile whose rows hold C
 // chunks; x is the row index modulo 16 (after any row permutation). Chosen so
 // that 16 lanes reading rows x = 0..15 at one logical chunk hit 16 distinct
-// 16-byte slots of a 256-byte bank window (and 8 lanes hit 8 distinct slots
-// of a 128-byte window).
+// 16-byte slots of the 256-byte window the 64 LDS banks serve per cycle (for
+// C >= 8 also 8 lanes in 8 distinct slots of a 128-byte window).
 template <int C>
 __device__ __forceinline__ int swz(int x) {
   if constexpr (C >= 16) return x & 15;
   else if constexpr (C == 8) return ((x >> 1) & 7) ^ ((x & 1) << 2);
-  else return (x >> 1) & (C - 1);
+  else return (x >> 2) & (C - 1);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
+enum SchedMask : int { kSchedVALU = 0x2, kSchedSALU = 0x4, kSchedMFMA = 0x8, kSchedVMEM = 0x10, kSchedDSRead = 0x100,
+                       kSchedDSWrite = 0x200, kSchedTrans = 0x400 };
 
 // Workgroup -> work-item remap so that each XCD (blocks are dealt to the 8
 // XCDs round-robin by block id) processes a contiguous range of work items:

@@ -19,7 +19,10 @@ using Elt = _Float16;
 
 template <typename T, int DQK, int DV, int MODE>
 static hipError_t fwd_launch(const FwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_fwd_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(256), 0, s, p);
+  if constexpr (FwdCfg<DQK, DV, MODE>::FITS)
+    hipLaunchKernelGGL((attn_fwd_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(512), 0, s, p);
+  else
+    hipLaunchKernelGGL((attn_fwd_simple_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
