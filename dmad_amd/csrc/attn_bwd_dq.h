@@ -15,6 +15,9 @@
 // accumulates in registers with lane <-> query, so the per-row statistics are
 // per-lane scalars.
 #pragma once
+#include <type_traits>
+
+#include "attn_fwd.h"
 #include "common.h"
 
 namespace dmad {
@@ -287,6 +290,223 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(DqParams p) {
           *(u32x2_t*)(dqp + dc * 2) = w;
         }
       }
+    }
+  }
+}
+
+// 16-query-per-wave variant of the dO-only dQ pass (8 waves, 2 per SIMD,
+// 16x16x32 MFMAs), pipelined like the forward kernel:
+//   step i: MFMA dQ^T += K^T dS^T of tile i-1 || VALU P, dS of tile i;
+//           then MFMA S^T, dP^T of tile i+1.
+template <int D>
+struct DqPipeCfg {
+  static constexpr int NW = 8;
+  static constexpr int QW = 16;
+  static constexpr int BM = QW * NW;
+  static constexpr int BN = 32;
+  static constexpr int KS = D / 32;
+  static constexpr int DB = D / 16;
+  static constexpr int CK = D / 8;   // chunks per K / V row
+  static constexpr int CT = BN / 8;  // chunks per K^T row
+  static constexpr int KT_ROWS = D < 32 ? 32 : D;  // rows per head of the K^T workspace
+  static constexpr int ROW_BYTES = BN * D * 2;
+  static constexpr int OFF_K = 0;
+  static constexpr int OFF_V = ROW_BYTES;
+  static constexpr int OFF_KT = 2 * ROW_BYTES;
+  static constexpr int STAGE = 3 * ROW_BYTES;
+  static constexpr int NSTAGE = 4;
+  static constexpr bool FITS = D >= 32 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr int NRI = BN * CK / 64;
+  static constexpr int NTI = D * CT / 64;
+  static constexpr int RPW = (NRI + NW - 1) / NW;
+  static constexpr int TPW = (NTI + NW - 1) / NW;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(512) void attn_bwd_dq_pipe_kernel(DqParams p) {
+  using C = DqPipeCfg<D>;
+  constexpr int BN = C::BN, KS = C::KS, DB = C::DB, CK = C::CK, CT = C::CT, NST = C::NSTAGE;
+  __shared__ __attribute__((aligned(1024))) char smem[NST * C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  // ---- per-lane query operands and statistics
+  const int qrow = qt * C::BM + wave * C::QW + col;
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const char*)p.dout + (b * p.do_sb + h * p.do_sh) * 2, do_bytes);
+  i32x4_t qr[KS], dor[KS];
+  {
+    const uint32_t qo = (uint32_t)((int64_t)qrow * p.q_sl * 2) + grp * 16;
+    const uint32_t oo = (uint32_t)((int64_t)qrow * p.do_sl * 2) + grp * 16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qr[s] = buf_load16(rq, qo + s * 64);
+      dor[s] = buf_load16(rdo, oo + s * 64);
+    }
+  }
+  float lse2 = __builtin_inff(), dlt = 0.f;
+  if (qrow < p.LQP) {
+    const float* st = p.stats + ((int64_t)bh * (p.LQP / p.stat_tile) + qrow / p.stat_tile) * 2 * p.stat_tile +
+                      qrow % p.stat_tile;
+    lse2 = st[0];
+    dlt = st[p.stat_tile];
+  }
+
+  // ---- key-side resources and per-lane DMA offsets
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
+  const uint32_t kt_bytes = (uint32_t)((int64_t)C::KT_ROWS * p.LKP * 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes);
+  const __amdgpu_buffer_rsrc_t rkt = make_rsrc((const char*)p.kT + (int64_t)bh * kt_bytes, kt_bytes);
+  uint32_t roff_k[C::RPW], roff_v[C::RPW], toff[C::TPW];
+#pragma unroll
+  for (int j = 0; j < C::RPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CK, phys = pch % CK;
+    const int logical = phys ^ kswz16<CK>(row);
+    roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
+    roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < C::TPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int d = pch / CT, phys = pch % CT;
+    const int logical = phys ^ swz<CT>(d & 15);
+    toff[j] = (uint32_t)(d * p.LKP * 2) + logical * 16;
+  }
+  const uint32_t k_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
+  const uint32_t v_step = (uint32_t)((int64_t)BN * p.v_sl * 2);
+
+  auto stage_ptr = [&](int kt) -> const char* { return smem + (kt & (NST - 1)) * C::STAGE; };
+  auto issue_tile = [&](int kt) {
+    char* st = smem + (kt & (NST - 1)) * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < C::RPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NRI) {
+        buf_load16_lds(rk, st + C::OFF_K + i * 1024, roff_k[j], (uint32_t)kt * k_step);
+        buf_load16_lds(rv, st + C::OFF_V + i * 1024, roff_v[j], (uint32_t)kt * v_step);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::TPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NTI) buf_load16_lds(rkt, st + C::OFF_KT + i * 1024, toff[j], (uint32_t)kt * BN * 2);
+    }
+  };
+
+  int krow_off[2], kswzv[2];
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    const int R = key_of_row16(sb, col);
+    krow_off[sb] = R * CK * 16;
+    kswzv[sb] = kswz16<CK>(R);
+  }
+  const int trow_off = col * CT * 16 + ((grp ^ swz<CT>(col)) << 4);
+
+  f32x4_t acc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[d][v] = 0.f;
+  }
+  const int ntiles = (p.Lk + BN - 1) / BN;
+
+  // S^T, dP^T of one 32-key tile
+  f32x4_t sc[2], dpc[2];
+  auto scores = [&](const char* st) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int off = krow_off[sb] + (((4 * s + grp) ^ kswzv[sb]) << 4);
+        const i32x4_t ak = *(const i32x4_t*)(st + C::OFF_K + off);
+        const i32x4_t av = *(const i32x4_t*)(st + C::OFF_V + off);
+        if (s == 0) {
+          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+          sc[sb] = mfma16(ak, qr[0], z, T());
+          dpc[sb] = mfma16(av, dor[0], z, T());
+        } else {
+          sc[sb] = mfma16(ak, qr[s], sc[sb], T());
+          dpc[sb] = mfma16(av, dor[s], dpc[sb], T());
+        }
+      }
+    }
+  };
+  // dS of one tile, packed as the B operand (keys 8*grp + e)
+  auto dscore = [&](int kt, auto TAIL, i32x4_t& dsk) {
+    float dsv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sb = e >> 2, v = e & 3;
+      float pe = fast_exp2(fmaf(sc[sb][v], p.scale_log2, -lse2));
+      if constexpr (decltype(TAIL)::value) {
+        if (kt * BN + 8 * grp + 4 * sb + v >= p.Lk) pe = 0.f;
+      }
+      dsv[e] = pe * (dpc[sb][v] - dlt);
+    }
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) dsk[e2] = (int)Elem<T>::pack2(dsv[2 * e2], dsv[2 * e2 + 1]);
+  };
+  auto dq_update = [&](const char* st, const i32x4_t& dsk) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const i32x4_t akt = *(const i32x4_t*)(st + C::OFF_KT + d * 16 * CT * 16 + trow_off);
+      acc[d] = mfma16(akt, dsk, acc[d], T());
+    }
+  };
+
+  issue_tile(0);
+  if (ntiles > 1) issue_tile(1);
+  if (ntiles > 2) issue_tile(2);
+  wait_vmem();
+  __syncthreads();
+  i32x4_t dsk;
+  scores(stage_ptr(0));
+  if (ntiles == 1) {
+    dscore(0, std::true_type(), dsk);
+  } else {
+    dscore(0, std::false_type(), dsk);
+    scores(stage_ptr(1));
+  }
+  int i = 1;
+  for (; i + 1 < ntiles; ++i) {
+    wait_vmem();
+    __syncthreads();
+    if (i + 2 < ntiles) issue_tile(i + 2);
+    i32x4_t dsn;
+    dq_update(stage_ptr(i - 1), dsk);
+    dscore(i, std::false_type(), dsn);
+    scores(stage_ptr(i + 1));
+    dsk = dsn;
+  }
+  if (ntiles > 1) {
+    i32x4_t dsn;
+    dq_update(stage_ptr(i - 1), dsk);
+    dscore(i, std::true_type(), dsn);
+    dsk = dsn;
+  }
+  dq_update(stage_ptr(ntiles - 1), dsk);
+
+  // ---- dQ = s (dQ^T)^T: lane (query col, group g) holds d = 16*dblk + 4g + v
+  if (qrow < p.Lq) {
+    char* dqp = (char*)p.dq + ((b * p.dq_sb + h * p.dq_sh) + (int64_t)qrow * p.dq_sl) * 2;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int dc = d * 16 + 4 * grp;
+      u32x2_t w = {Elem<T>::pack2(acc[d][0] * p.scale, acc[d][1] * p.scale),
+                   Elem<T>::pack2(acc[d][2] * p.scale, acc[d][3] * p.scale)};
+      *(u32x2_t*)(dqp + dc * 2) = w;
     }
   }
 }
