@@ -31,6 +31,7 @@
 //   * P and dS leave the score C tiles already in B-operand layout (perm32),
 //     so dK^T and dV^T accumulate in registers with no data movement;
 #pragma once
+#include "attn_fwd.h"
 #include "common.h"
 
 namespace dmad {
@@ -354,11 +355,254 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
   }
 }
 
+// 16-key-per-wave variant of the dO-only dK/dV pass (8 waves = 128 keys,
+// 2 waves per SIMD, 16x16x32 MFMAs), pipelined over 32-query tiles:
+//   step j: MFMA dV^T += dO^T P, dK^T += Q^T dS of tile j-1 || VALU P, dS of tile j;
+//           then MFMA S, dP of tile j+1.
+// Lane l owns key 16*wave + l%16; query rows of every 16-row score block are
+// read in key_of_row16 order so each lane group holds 8 consecutive queries,
+// the B-operand layout of the 32-query dV^T / dK^T products.
+template <int D>
+struct KvPipeCfg {
+  static constexpr int NW = 8;
+  static constexpr int KW = 16;        // keys per wave
+  static constexpr int BK = KW * NW;   // keys per workgroup
+  static constexpr int BMQ = 32;       // queries per pipeline step
+  static constexpr int KS = D / 32;
+  static constexpr int DB = D / 16;
+  static constexpr int CR = D / 8;     // chunks per Q / dO row
+  static constexpr int CT = BMQ / 8;   // chunks per Q^T / dO^T row
+  static constexpr int TR_ROWS = D < 32 ? 32 : D;  // rows per head of the transposed workspaces
+  static constexpr int ROW_BYTES = BMQ * D * 2;
+  static constexpr int TR_BYTES = D * BMQ * 2;
+  static constexpr int OFF_Q = 0;
+  static constexpr int OFF_DO = ROW_BYTES;
+  static constexpr int OFF_QT = 2 * ROW_BYTES;
+  static constexpr int OFF_DOT = 2 * ROW_BYTES + TR_BYTES;
+  static constexpr int OFF_ST = 2 * ROW_BYTES + 2 * TR_BYTES;
+  static constexpr int STAT_BYTES = 2 * BMQ * 4;
+  static constexpr int STAGE = (OFF_ST + STAT_BYTES + 1023) / 1024 * 1024;
+  static constexpr int NSTAGE = 4;
+  static constexpr bool FITS = D >= 32 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr int NRI = BMQ * CR / 64;
+  static constexpr int NTI = D * CT / 64;
+  static constexpr int RPW = (NRI + NW - 1) / NW;
+  static constexpr int TPW = (NTI + NW - 1) / NW;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(512) void attn_bwd_kv_pipe_kernel(BwdParams p) {
+  using C = KvPipeCfg<D>;
+  constexpr int BMQ = C::BMQ, KS = C::KS, DB = C::DB, CR = C::CR, CT = C::CT, NST = C::NSTAGE;
+  __shared__ __attribute__((aligned(1024))) char smem[NST * C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+
+  const int nkt = (p.Lk + C::BK - 1) / C::BK;
+  const int work = xcd_remap(blockIdx.x, nkt * p.B * p.H);
+  const int bh = work / nkt, kt = work - bh * nkt;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int nqt = p.LQP / BMQ;
+
+  const int key = kt * C::BK + wave * C::KW + col;
+  const bool key_ok = key < p.Lk;
+
+  // ---- stationary K, V rows: B operands of S = Q K^T and dP = dO V^T
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes);
+  i32x4_t kreg[KS], vreg[KS];
+  {
+    const uint32_t ko = (uint32_t)((int64_t)key * p.k_sl * 2) + grp * 16;
+    const uint32_t vo = (uint32_t)((int64_t)key * p.v_sl * 2) + grp * 16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kreg[s] = buf_load16(rk, ko + s * 64);
+      vreg[s] = buf_load16(rv, vo + s * 64);
+    }
+  }
+
+  // ---- query-side resources and per-lane DMA offsets
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
+  const uint32_t tr_bytes = (uint32_t)((int64_t)C::TR_ROWS * p.LQP * 2);
+  const uint32_t st_bytes = (uint32_t)((int64_t)p.LQP * 2 * 4);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const char*)p.dout + (b * p.do_sb + h * p.do_sh) * 2, do_bytes);
+  const __amdgpu_buffer_rsrc_t rqt = make_rsrc((const char*)p.qT + (int64_t)bh * tr_bytes, tr_bytes);
+  const __amdgpu_buffer_rsrc_t rdot = make_rsrc((const char*)p.doT + (int64_t)bh * tr_bytes, tr_bytes);
+  const __amdgpu_buffer_rsrc_t rst = make_rsrc((const char*)p.stats + (int64_t)bh * st_bytes, st_bytes);
+  uint32_t roff_q[C::RPW], roff_do[C::RPW], toff[C::TPW];
+#pragma unroll
+  for (int j = 0; j < C::RPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CR, phys = pch % CR;
+    const int logical = phys ^ kswz16<CR>(row);
+    roff_q[j] = (uint32_t)((int64_t)row * p.q_sl * 2) + logical * 16;
+    roff_do[j] = (uint32_t)((int64_t)row * p.do_sl * 2) + logical * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < C::TPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int d = pch / CT, phys = pch % CT;
+    const int logical = phys ^ swz<CT>(d & 15);
+    toff[j] = (uint32_t)(d * p.LQP * 2) + logical * 16;
+  }
+  const uint32_t q_step = (uint32_t)((int64_t)BMQ * p.q_sl * 2);
+  const uint32_t do_step = (uint32_t)((int64_t)BMQ * p.do_sl * 2);
+
+  auto stage_ptr = [&](int qt) -> const char* { return smem + (qt & (NST - 1)) * C::STAGE; };
+  auto issue_tile = [&](int qt) {
+    char* st = smem + (qt & (NST - 1)) * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < C::RPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NRI) {
+        buf_load16_lds(rq, st + C::OFF_Q + i * 1024, roff_q[j], (uint32_t)qt * q_step);
+        buf_load16_lds(rdo, st + C::OFF_DO + i * 1024, roff_do[j], (uint32_t)qt * do_step);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::TPW; ++j) {
+      const int i = wave + j * C::NW;
+      if (i < C::NTI) {
+        buf_load16_lds(rqt, st + C::OFF_QT + i * 1024, toff[j], (uint32_t)qt * BMQ * 2);
+        buf_load16_lds(rdot, st + C::OFF_DOT + i * 1024, toff[j], (uint32_t)qt * BMQ * 2);
+      }
+    }
+    if (wave == C::NW - 1 && lane * 16 < C::STAT_BYTES)
+      buf_load16_lds(rst, st + C::OFF_ST, lane * 16, (uint32_t)qt * C::STAT_BYTES);
+  };
+
+  int rrow_off[2], rswzv[2];
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    const int R = key_of_row16(sb, col);
+    rrow_off[sb] = R * CR * 16;
+    rswzv[sb] = kswz16<CR>(R);
+  }
+  const int trow_off = col * CT * 16 + ((grp ^ swz<CT>(col)) << 4);
+
+  f32x4_t dkacc[DB], dvacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      dkacc[d][v] = 0.f;
+      dvacc[d][v] = 0.f;
+    }
+  }
+
+  // S, dP of one 32-query tile (rows = queries in key_of_row16 order, cols = keys)
+  f32x4_t sc[2], dpc[2];
+  auto scores = [&](const char* st) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int off = rrow_off[sb] + (((4 * s + grp) ^ rswzv[sb]) << 4);
+        const i32x4_t aq = *(const i32x4_t*)(st + C::OFF_Q + off);
+        const i32x4_t ado = *(const i32x4_t*)(st + C::OFF_DO + off);
+        if (s == 0) {
+          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+          sc[sb] = mfma16(aq, kreg[0], z, T());
+          dpc[sb] = mfma16(ado, vreg[0], z, T());
+        } else {
+          sc[sb] = mfma16(aq, kreg[s], sc[sb], T());
+          dpc[sb] = mfma16(ado, vreg[s], dpc[sb], T());
+        }
+      }
+    }
+  };
+  // P and dS of one tile, packed as B operands (queries 8*grp + e)
+  auto elementwise = [&](const char* st, i32x4_t& pk, i32x4_t& dsk) {
+    const float* sst = (const float*)(st + C::OFF_ST);
+    const float4 l0 = *(const float4*)(sst + 8 * grp), l1 = *(const float4*)(sst + 8 * grp + 4);
+    const float4 d0 = *(const float4*)(sst + BMQ + 8 * grp), d1 = *(const float4*)(sst + BMQ + 8 * grp + 4);
+    const float lse2[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+    const float dlt[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    float pv[8], dsv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sb = e >> 2, v = e & 3;
+      float pe = fast_exp2(fmaf(sc[sb][v], p.scale_log2, -lse2[e]));
+      pe = key_ok ? pe : 0.f;
+      pv[e] = pe;
+      dsv[e] = pe * (dpc[sb][v] - dlt[e]);
+    }
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      pk[e2] = (int)Elem<T>::pack2(pv[2 * e2], pv[2 * e2 + 1]);
+      dsk[e2] = (int)Elem<T>::pack2(dsv[2 * e2], dsv[2 * e2 + 1]);
+    }
+  };
+  auto kv_update = [&](const char* st, const i32x4_t& pk, const i32x4_t& dsk) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int off = d * 16 * CT * 16 + trow_off;
+      const i32x4_t ado = *(const i32x4_t*)(st + C::OFF_DOT + off);
+      const i32x4_t aq = *(const i32x4_t*)(st + C::OFF_QT + off);
+      dvacc[d] = mfma16(ado, pk, dvacc[d], T());
+      dkacc[d] = mfma16(aq, dsk, dkacc[d], T());
+    }
+  };
+
+  issue_tile(0);
+  if (nqt > 1) issue_tile(1);
+  if (nqt > 2) issue_tile(2);
+  wait_vmem();
+  __syncthreads();
+  i32x4_t pk, dsk;
+  if (nqt > 0) {
+    scores(stage_ptr(0));
+    elementwise(stage_ptr(0), pk, dsk);
+    if (nqt > 1) scores(stage_ptr(1));
+  }
+  int j = 1;
+  for (; j + 1 < nqt; ++j) {
+    wait_vmem();
+    __syncthreads();
+    if (j + 2 < nqt) issue_tile(j + 2);
+    i32x4_t pn, dsn;
+    kv_update(stage_ptr(j - 1), pk, dsk);
+    elementwise(stage_ptr(j), pn, dsn);
+    scores(stage_ptr(j + 1));
+    pk = pn;
+    dsk = dsn;
+  }
+  if (nqt > 1) {
+    i32x4_t pn, dsn;
+    kv_update(stage_ptr(j - 1), pk, dsk);
+    elementwise(stage_ptr(j), pn, dsn);
+    pk = pn;
+    dsk = dsn;
+  }
+  if (nqt > 0) kv_update(stage_ptr(nqt - 1), pk, dsk);
+
+  // ---- store dK = s (dK^T)^T, dV = (dV^T)^T: lane (key col, group g) holds d = 16*dblk + 4g + v
+  if (key_ok) {
+    char* dkp = (char*)p.dk + ((b * p.dk_sb + h * p.dk_sh) + (int64_t)key * p.dk_sl) * 2;
+    char* dvp = (char*)p.dv + ((b * p.dv_sb + h * p.dv_sh) + (int64_t)key * p.dv_sl) * 2;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int dc = d * 16 + 4 * grp;
+      u32x2_t wk = {Elem<T>::pack2(dkacc[d][0] * p.scale, dkacc[d][1] * p.scale),
+                    Elem<T>::pack2(dkacc[d][2] * p.scale, dkacc[d][3] * p.scale)};
+      u32x2_t wv = {Elem<T>::pack2(dvacc[d][0], dvacc[d][1]), Elem<T>::pack2(dvacc[d][2], dvacc[d][3])};
+      *(u32x2_t*)(dkp + dc * 2) = wk;
+      *(u32x2_t*)(dvp + dc * 2) = wv;
+    }
+  }
+}
+
 // Per-row statistics for the backward, one thread per (b*h, query row):
 //   A layout  [BH][LQP/BA][2][BA]: lse2 = LSE*log2(e), D = rowsum(dO*O)
 //   B layout  [BH][LQP/32][4][32]: lse2, D' = rowsum(dO*O) + rowsum(dOd*Od) - mu*rho, mu, rho
 //   BT layout [BH][LQP/BA][2][BA]: lse2, rho = rowsum(dOd*O)   (tangent gradients)
-// BA is the query tile of the dO-only kernel for this head dim.
+// BA is the query tile of the dO-only key-stationary kernel for this head dim.
 // Rows past Lq get lse2 = +inf (so P = 0) and zeros.
 struct PrepParams {
   const void* o;

@@ -337,24 +337,32 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
     scores(stage_ptr(1));
   }
   // ---- steady state: step i runs PV of tile i-1, softmax of tile i, scores of tile i+1
+  // The rescale for step i's alpha runs at the top of step i+1: after the PV
+  // of tile i-1 and before that of tile i, and in its own (rarely taken)
+  // branch, so the softmax of step i stays in one block with its MFMAs.
+  bool moved = false;
+  float alpha = 1.f;
   int i = 1;
   for (; i + 1 < ntiles; ++i) {
     wait_vmem();
     __syncthreads();
     if (i + 2 < ntiles) issue_tile(i + 2);  // reuses the stage of tile i-2
+    if (moved) rescale(alpha);
     i32x4_t pn, hn;
     pv_update(stage_ptr(i - 1), pk, hk);
-    const float alpha = softmax(i, std::false_type(), pn, hn);
+    alpha = softmax(i, std::false_type(), pn, hn);
+    moved = alpha != 1.f;
+    moved = __builtin_amdgcn_ballot_w64(moved) != 0;
     scores(stage_ptr(i + 1));
-    rescale(alpha);  // unconditional: keeps the whole step one basic block
     pk = pn;
     hk = hn;
   }
+  if (moved) rescale(alpha);
   // ---- last step: tile ntiles-1 may hold keys >= Lk
   if (ntiles > 1) {
     i32x4_t pn, hn;
     pv_update(stage_ptr(i - 1), pk, hk);
-    const float alpha = softmax(i, std::true_type(), pn, hn);
+    alpha = softmax(i, std::true_type(), pn, hn);
     rescale(alpha);
     pk = pn;
     hk = hn;

@@ -28,6 +28,8 @@ template <typename T, int D>
 DqLaunchFn dq_select(int mode);
 
 // Query tile of the backward kernel (the layout of its statistics).
+// (The dO-only kernel runs attn_bwd_kernel; attn_bwd_kv_pipe_kernel, which
+// uses 32-query tiles, measured slower at the 14B shape and is not selected.)
 inline int bwd_bmq(int d, int mode) { return (mode == kBwdFull || d > 128) ? 32 : 64; }
 
 hipError_t launch_transpose_pad(const TransposeParams& p, int BH, hipStream_t s);
