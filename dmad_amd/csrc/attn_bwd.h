@@ -355,24 +355,27 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
   }
 }
 
-// 16-key-per-wave variant of the dO-only dK/dV pass (8 waves = 128 keys,
-// 2 waves per SIMD, 16x16x32 MFMAs), pipelined over 32-query tiles:
-//   step j: MFMA dV^T += dO^T P, dK^T += Q^T dS of tile j-1 || VALU P, dS of tile j;
-//           then MFMA S, dP of tile j+1.
-// Lane l owns key 16*wave + l%16; query rows of every 16-row score block are
-// read in key_of_row16 order so each lane group holds 8 consecutive queries,
-// the B-operand layout of the 32-query dV^T / dK^T products.
-template <int D>
+// Pipelined dO-only dK/dV pass: 4 waves x 32 keys, 32x32x16 MFMAs, BMQ-query
+// steps through a four-stage LDS ring whose tiles are requested three steps
+// ahead. Step j (after one barrier) is a fixed stream of MFMAs:
+//   S, dP of tile j+1 (with the VALU P, dS of tile j interleaved), then
+//   dV^T += dO^T P, dK^T += Q^T dS of tile j (with tile j+3's requests interleaved);
+// every MFMA's LDS operand is read four MFMAs ahead. S and dP alternate between
+// two register sets, and the loop is unrolled by four so that each ring stage
+// is a separate LDS object known at compile time (the compiler then waits for a
+// buffer->LDS request only before reading the stage it fills). Keys at or
+// beyond Lk read K = V = 0 and are never stored, so P needs no key mask;
+// padded queries carry lse = +inf, so their P is 0.
+template <int D, int BMQ_>
 struct KvPipeCfg {
-  static constexpr int NW = 8;
-  static constexpr int KW = 16;        // keys per wave
-  static constexpr int BK = KW * NW;   // keys per workgroup
-  static constexpr int BMQ = 32;       // queries per pipeline step
-  static constexpr int KS = D / 32;
-  static constexpr int DB = D / 16;
+  static constexpr int NW = 4;
+  static constexpr int BK = 32 * NW;   // keys per workgroup
+  static constexpr int BMQ = BMQ_;     // queries per pipeline step
+  static constexpr int NQB = BMQ / 32;
+  static constexpr int KS = D / 16;
+  static constexpr int DB = D / 32;    // 32-row blocks of dK^T, dV^T
   static constexpr int CR = D / 8;     // chunks per Q / dO row
   static constexpr int CT = BMQ / 8;   // chunks per Q^T / dO^T row
-  static constexpr int TR_ROWS = D < 32 ? 32 : D;  // rows per head of the transposed workspaces
   static constexpr int ROW_BYTES = BMQ * D * 2;
   static constexpr int TR_BYTES = D * BMQ * 2;
   static constexpr int OFF_Q = 0;
@@ -383,22 +386,36 @@ struct KvPipeCfg {
   static constexpr int STAT_BYTES = 2 * BMQ * 4;
   static constexpr int STAGE = (OFF_ST + STAT_BYTES + 1023) / 1024 * 1024;
   static constexpr int NSTAGE = 4;
-  static constexpr bool FITS = D >= 32 && NSTAGE * STAGE <= 160 * 1024;
-  static constexpr int NRI = BMQ * CR / 64;
-  static constexpr int NTI = D * CT / 64;
-  static constexpr int RPW = (NRI + NW - 1) / NW;
-  static constexpr int TPW = (NTI + NW - 1) / NW;
+  static constexpr int NRI = BMQ * CR / 64;  // wave-wide 1 KiB loads per row tile
+  static constexpr int NTI = D * CT / 64;    // ... per transposed tile
+  static constexpr int ST_LANES = STAT_BYTES / 16 / NW;  // lanes per wave loading statistics
+  // every wave issues the same number of loads per tile (counted waits)
+  static constexpr bool FITS = D >= 32 && D <= 128 && NRI % NW == 0 && NTI % NW == 0 &&
+                               NSTAGE * STAGE <= 160 * 1024;
+  static constexpr int LOADS = 2 * (NRI / NW) + 2 * (NTI / NW) + 1;  // per wave per tile
 };
 
+// Query tile used by the dO-only dK/dV kernel for head dim D (the layout of the
+// backward statistics follows it).
+template <int D>
+constexpr int kv_pipe_bmq() { return D >= 128 ? 32 : 64; }
+
 template <typename T, int D>
-__global__ __launch_bounds__(512) void attn_bwd_kv_pipe_kernel(BwdParams p) {
-  using C = KvPipeCfg<D>;
-  constexpr int BMQ = C::BMQ, KS = C::KS, DB = C::DB, CR = C::CR, CT = C::CT, NST = C::NSTAGE;
-  __shared__ __attribute__((aligned(1024))) char smem[NST * C::STAGE];
+__global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
+  using C = KvPipeCfg<D, kv_pipe_bmq<D>()>;
+  constexpr int BMQ = C::BMQ, NQB = C::NQB, KS = C::KS, DB = C::DB, CR = C::CR, CT = C::CT, NST = C::NSTAGE;
+  static_assert(C::FITS, "configuration does not fit");
+  // one LDS object per ring stage: the compiler then orders LDS reads only
+  // after the buffer->LDS requests into the same stage
+  __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
+  static_assert(NST == 4, "four ring stages");
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = lane & 15, grp = lane >> 4;
+  const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
   const int work = xcd_remap(blockIdx.x, nkt * p.B * p.H);
@@ -406,8 +423,7 @@ __global__ __launch_bounds__(512) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
 
-  const int key = kt * C::BK + wave * C::KW + col;
-  const bool key_ok = key < p.Lk;
+  const int key = kt * C::BK + wave * 32 + col;
 
   // ---- stationary K, V rows: B operands of S = Q K^T and dP = dO V^T
   const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
@@ -416,36 +432,37 @@ __global__ __launch_bounds__(512) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes);
   i32x4_t kreg[KS], vreg[KS];
   {
-    const uint32_t ko = (uint32_t)((int64_t)key * p.k_sl * 2) + grp * 16;
-    const uint32_t vo = (uint32_t)((int64_t)key * p.v_sl * 2) + grp * 16;
+    const uint32_t ko = (uint32_t)((int64_t)key * p.k_sl * 2) + half * 16;
+    const uint32_t vo = (uint32_t)((int64_t)key * p.v_sl * 2) + half * 16;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      kreg[s] = buf_load16(rk, ko + s * 64);
-      vreg[s] = buf_load16(rv, vo + s * 64);
+      kreg[s] = buf_load16(rk, ko + s * 32);
+      vreg[s] = buf_load16(rv, vo + s * 32);
     }
   }
 
   // ---- query-side resources and per-lane DMA offsets
   const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
   const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
-  const uint32_t tr_bytes = (uint32_t)((int64_t)C::TR_ROWS * p.LQP * 2);
+  const uint32_t tr_bytes = (uint32_t)((int64_t)D * p.LQP * 2);
   const uint32_t st_bytes = (uint32_t)((int64_t)p.LQP * 2 * 4);
   const __amdgpu_buffer_rsrc_t rq = make_rsrc((const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
   const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const char*)p.dout + (b * p.do_sb + h * p.do_sh) * 2, do_bytes);
   const __amdgpu_buffer_rsrc_t rqt = make_rsrc((const char*)p.qT + (int64_t)bh * tr_bytes, tr_bytes);
   const __amdgpu_buffer_rsrc_t rdot = make_rsrc((const char*)p.doT + (int64_t)bh * tr_bytes, tr_bytes);
   const __amdgpu_buffer_rsrc_t rst = make_rsrc((const char*)p.stats + (int64_t)bh * st_bytes, st_bytes);
-  uint32_t roff_q[C::RPW], roff_do[C::RPW], toff[C::TPW];
+  constexpr int RPW = C::NRI / C::NW, TPW = C::NTI / C::NW;
+  uint32_t roff_q[RPW], roff_do[RPW], toff[TPW];
 #pragma unroll
-  for (int j = 0; j < C::RPW; ++j) {
+  for (int j = 0; j < RPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int row = pch / CR, phys = pch % CR;
-    const int logical = phys ^ kswz16<CR>(row);
+    const int logical = phys ^ swz<CR>(perm32(row & 31) & 15);
     roff_q[j] = (uint32_t)((int64_t)row * p.q_sl * 2) + logical * 16;
     roff_do[j] = (uint32_t)((int64_t)row * p.do_sl * 2) + logical * 16;
   }
 #pragma unroll
-  for (int j = 0; j < C::TPW; ++j) {
+  for (int j = 0; j < TPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int d = pch / CT, phys = pch % CT;
     const int logical = phys ^ swz<CT>(d & 15);
@@ -453,147 +470,215 @@ __global__ __launch_bounds__(512) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   }
   const uint32_t q_step = (uint32_t)((int64_t)BMQ * p.q_sl * 2);
   const uint32_t do_step = (uint32_t)((int64_t)BMQ * p.do_sl * 2);
+  static_assert(C::ST_LANES * C::NW * 16 == C::STAT_BYTES, "statistics split evenly over the waves");
+  const bool st_lane = lane >= wave * C::ST_LANES && lane < (wave + 1) * C::ST_LANES;
 
-  auto stage_ptr = [&](int qt) -> const char* { return smem + (qt & (NST - 1)) * C::STAGE; };
-  auto issue_tile = [&](int qt) {
-    char* st = smem + (qt & (NST - 1)) * C::STAGE;
-#pragma unroll
-    for (int j = 0; j < C::RPW; ++j) {
-      const int i = wave + j * C::NW;
-      if (i < C::NRI) {
-        buf_load16_lds(rq, st + C::OFF_Q + i * 1024, roff_q[j], (uint32_t)qt * q_step);
-        buf_load16_lds(rdo, st + C::OFF_DO + i * 1024, roff_do[j], (uint32_t)qt * do_step);
-      }
+  // stage of tile qt is qt % 4, always known at compile time
+  auto stage = [&](auto kk) -> lds_char_t* {
+    constexpr int k = decltype(kk)::value & 3;
+    if constexpr (k == 0) return (lds_char_t*)stg0;
+    else if constexpr (k == 1) return (lds_char_t*)stg1;
+    else if constexpr (k == 2) return (lds_char_t*)stg2;
+    else return (lds_char_t*)stg3;
+  };
+  // Load li (0 <= li < C::LOADS) of tile qt into stage st. Tiles at or beyond
+  // the end read zeros or in-range rows (buffer range checks) into a stage
+  // nobody reads again.
+  auto issue_load = [&](lds_char_t* st, int qt, int li) {
+    if (li < 2 * RPW) {
+      const int jj = li >> 1, i = wave + jj * C::NW;
+      if (li & 1) buf_load16_lds(rdo, st + C::OFF_DO + i * 1024, roff_do[jj], (uint32_t)qt * do_step);
+      else buf_load16_lds(rq, st + C::OFF_Q + i * 1024, roff_q[jj], (uint32_t)qt * q_step);
+    } else if (li < 2 * RPW + 2 * TPW) {
+      const int jj = (li - 2 * RPW) >> 1, i = wave + jj * C::NW;
+      if (li & 1) buf_load16_lds(rdot, st + C::OFF_DOT + i * 1024, toff[jj], (uint32_t)qt * BMQ * 2);
+      else buf_load16_lds(rqt, st + C::OFF_QT + i * 1024, toff[jj], (uint32_t)qt * BMQ * 2);
+    } else {
+      if (st_lane) buf_load16_lds(rst, st + C::OFF_ST, lane * 16, (uint32_t)qt * C::STAT_BYTES);
     }
-#pragma unroll
-    for (int j = 0; j < C::TPW; ++j) {
-      const int i = wave + j * C::NW;
-      if (i < C::NTI) {
-        buf_load16_lds(rqt, st + C::OFF_QT + i * 1024, toff[j], (uint32_t)qt * BMQ * 2);
-        buf_load16_lds(rdot, st + C::OFF_DOT + i * 1024, toff[j], (uint32_t)qt * BMQ * 2);
-      }
-    }
-    if (wave == C::NW - 1 && lane * 16 < C::STAT_BYTES)
-      buf_load16_lds(rst, st + C::OFF_ST, lane * 16, (uint32_t)qt * C::STAT_BYTES);
   };
 
-  int rrow_off[2], rswzv[2];
-#pragma unroll
-  for (int sb = 0; sb < 2; ++sb) {
-    const int R = key_of_row16(sb, col);
-    rrow_off[sb] = R * CR * 16;
-    rswzv[sb] = kswz16<CR>(R);
-  }
-  const int trow_off = col * CT * 16 + ((grp ^ swz<CT>(col)) << 4);
+  const int rswz = swz<CR>(col & 15), tswz = swz<CT>(col & 15);
+  const int rrow_off = perm32(col) * CR * 16;
+  const int trow_off = col * CT * 16;
 
-  f32x4_t dkacc[DB], dvacc[DB];
+  f32x16_t dkacc[DB], dvacc[DB];
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < 16; ++v) {
       dkacc[d][v] = 0.f;
       dvacc[d][v] = 0.f;
     }
   }
 
-  // S, dP of one 32-query tile (rows = queries in key_of_row16 order, cols = keys)
-  f32x4_t sc[2], dpc[2];
-  auto scores = [&](const char* st) {
+  // One step is a fixed stream of MFMAs: NMA score MFMAs (S, dP of the next
+  // tile; block qb holds queries 32 qb + perm32(row)) then NMB update MFMAs
+  // (dV^T, dK^T of this tile). Each MFMA's LDS operand is read PF slots ahead;
+  // the P, dS arithmetic of this tile rides in the score slots and the tile
+  // requests three steps ahead ride in the update slots.
+  constexpr int PF = 4;
+  constexpr int NMA = 2 * KS * NQB;
+  constexpr int NMB = 4 * NQB * DB;
+  constexpr int NVAL = 16 * NQB;  // P, dS values per lane per tile
+  static_assert(NVAL % NMA == 0 || NMA % NVAL == 0, "value slots");
+  static_assert(C::LOADS <= NMB, "load slots");
+  const f32x16_t zero16 = {};
+  auto op_ptr = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int m) -> lds_i32x4_t* {
+    if (m < NMA) {
+      const int s = m / (2 * NQB), r = m % (2 * NQB), qb = r >> 1;
+      return (lds_i32x4_t*)(s_next + ((r & 1) ? C::OFF_DO : C::OFF_Q) + qb * 32 * CR * 16 + rrow_off +
+                              (((2 * s + half) ^ rswz) << 4));
+    }
+    const int mm = m - NMA, u = mm / (2 * DB), r = mm % (2 * DB), d = r >> 1;
+    return (lds_i32x4_t*)(s_cur + ((r & 1) ? C::OFF_QT : C::OFF_DOT) + d * 32 * CT * 16 + trow_off +
+                            (((2 * u + half) ^ tswz) << 4));
+  };
+  // statistics of one tile: lse (log2 units) and Delta for queries 32 qb + 16 t + 8 half + 0..7
+  auto load_stats = [&](const lds_char_t* st, f32x4_t (&lsev)[2 * NQB][2], f32x4_t (&dltv)[2 * NQB][2]) {
+    const lds_char_t* sst = st + C::OFF_ST;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
+    for (int u = 0; u < 2 * NQB; ++u) {
+      const int q0 = 16 * u + 8 * half;
+      lsev[u][0] = *(lds_f32x4_t*)(sst + 4 * q0);
+      lsev[u][1] = *(lds_f32x4_t*)(sst + 4 * (q0 + 4));
+      dltv[u][0] = *(lds_f32x4_t*)(sst + 4 * (BMQ + q0));
+      dltv[u][1] = *(lds_f32x4_t*)(sst + 4 * (BMQ + q0 + 4));
+    }
+  };
+  // value v of this tile: block v / 16, value (v % 16) of its C tile = query 32 qb + 16 t + 8 half + e
+  auto value = [&](int v, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], const f32x4_t (&lsev)[2 * NQB][2],
+                   const f32x4_t (&dltv)[2 * NQB][2], float (&pv)[2], float (&dsv)[2]) {
+    const int qb = v / 16, t = (v % 16) / 8, e = v % 8, u = 2 * qb + t;
+    const float l2 = lsev[u][e >> 2][e & 3], dl = dltv[u][e >> 2][e & 3];
+    const float pe = fast_exp2(fmaf(sc[qb][8 * t + e], p.scale_log2, -l2));
+    pv[v & 1] = pe;
+    dsv[v & 1] = pe * (dpc[qb][8 * t + e] - dl);
+  };
+  auto pack = [&](int v, const float (&pv)[2], const float (&dsv)[2], i32x4_t (&pb)[2 * NQB],
+                  i32x4_t (&dsb)[2 * NQB]) {
+    const int u = v / 8, e2 = (v % 8) >> 1;
+    pb[u][e2] = (int)Elem<T>::pack2(pv[0], pv[1]);
+    dsb[u][e2] = (int)Elem<T>::pack2(dsv[0], dsv[1]);
+  };
+  auto mfma_slot = [&](int m, i32x4_t op, f32x16_t (&sn)[NQB], f32x16_t (&dpn)[NQB],
+                       const i32x4_t (&pb)[2 * NQB], const i32x4_t (&dsb)[2 * NQB]) {
+    if (m < NMA) {
+      const int s = m / (2 * NQB), r = m % (2 * NQB), qb = r >> 1;
+      if (r & 1) dpn[qb] = mfma32(op, vreg[s], s == 0 ? zero16 : dpn[qb], T());
+      else sn[qb] = mfma32(op, kreg[s], s == 0 ? zero16 : sn[qb], T());
+    } else {
+      const int mm = m - NMA, u = mm / (2 * DB), r = mm % (2 * DB), d = r >> 1;
+      if (r & 1) dkacc[d] = mfma32(op, dsb[u], dkacc[d], T());
+      else dvacc[d] = mfma32(op, pb[u], dvacc[d], T());
+    }
+  };
+
+  // step j (j + 1 < nqt, j % 4 == kk): S, dP of tile j + 1 || P, dS of tile j; update with tile j;
+  // request tile j + 3
+  auto step = [&](auto kk, int j, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], f32x16_t (&sn)[NQB],
+                  f32x16_t (&dpn)[NQB]) {
+    constexpr int k = decltype(kk)::value;
+    ring_sync<C::LOADS>();  // tile j + 1 has landed (tile j + 2 may be in flight)
+    const lds_char_t* s_next = stage(IC<k + 1>{});
+    const lds_char_t* s_cur = stage(IC<k>{});
+    lds_char_t* s_req = stage(IC<k + 3>{});
+    f32x4_t lsev[2 * NQB][2], dltv[2 * NQB][2];
+    load_stats(s_cur, lsev, dltv);
+    i32x4_t opr[PF];
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        const int off = rrow_off[sb] + (((4 * s + grp) ^ rswzv[sb]) << 4);
-        const i32x4_t aq = *(const i32x4_t*)(st + C::OFF_Q + off);
-        const i32x4_t ado = *(const i32x4_t*)(st + C::OFF_DO + off);
-        if (s == 0) {
-          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-          sc[sb] = mfma16(aq, kreg[0], z, T());
-          dpc[sb] = mfma16(ado, vreg[0], z, T());
-        } else {
-          sc[sb] = mfma16(aq, kreg[s], sc[sb], T());
-          dpc[sb] = mfma16(ado, vreg[s], dpc[sb], T());
+    for (int m = 0; m < PF; ++m) opr[m] = *op_ptr(s_next, s_cur, m);
+    i32x4_t pb[2 * NQB], dsb[2 * NQB];
+    float pv[2], dsv[2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < NMA + NMB; ++m) {
+      mfma_slot(m, opr[m % PF], sn, dpn, pb, dsb);
+      if (m + PF < NMA + NMB) opr[m % PF] = *op_ptr(s_next, s_cur, m + PF);
+      if (m < NMA) {
+        constexpr int VPS = NVAL >= NMA ? NVAL / NMA : 1;
+#pragma unroll
+        for (int k = 0; k < VPS; ++k) {
+          const int v = m * VPS + k;
+          if (v < NVAL && (NVAL >= NMA || m % (NMA / NVAL) == 0)) {
+            const int vv = NVAL >= NMA ? v : m / (NMA / NVAL);
+            value(vv, sc, dpc, lsev, dltv, pv, dsv);
+            if (vv & 1) pack(vv, pv, dsv, pb, dsb);
+          }
         }
+      } else if (m - NMA < C::LOADS) {
+        issue_load(s_req, j + 3, m - NMA);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // P and dS of one tile, packed as B operands (queries 8*grp + e)
-  auto elementwise = [&](const char* st, i32x4_t& pk, i32x4_t& dsk) {
-    const float* sst = (const float*)(st + C::OFF_ST);
-    const float4 l0 = *(const float4*)(sst + 8 * grp), l1 = *(const float4*)(sst + 8 * grp + 4);
-    const float4 d0 = *(const float4*)(sst + BMQ + 8 * grp), d1 = *(const float4*)(sst + BMQ + 8 * grp + 4);
-    const float lse2[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-    const float dlt[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-    float pv[8], dsv[8];
+  // final tile: P, dS then the update MFMAs
+  auto last_step = [&](auto kk, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB]) {
+    const lds_char_t* s_cur = stage(kk);
+    f32x4_t lsev[2 * NQB][2], dltv[2 * NQB][2];
+    load_stats(s_cur, lsev, dltv);
+    i32x4_t pb[2 * NQB], dsb[2 * NQB];
+    float pv[2], dsv[2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int sb = e >> 2, v = e & 3;
-      float pe = fast_exp2(fmaf(sc[sb][v], p.scale_log2, -lse2[e]));
-      pe = key_ok ? pe : 0.f;
-      pv[e] = pe;
-      dsv[e] = pe * (dpc[sb][v] - dlt[e]);
+    for (int v = 0; v < NVAL; ++v) {
+      value(v, sc, dpc, lsev, dltv, pv, dsv);
+      if (v & 1) pack(v, pv, dsv, pb, dsb);
     }
+    f32x16_t unused_s[NQB], unused_p[NQB];
 #pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      pk[e2] = (int)Elem<T>::pack2(pv[2 * e2], pv[2 * e2 + 1]);
-      dsk[e2] = (int)Elem<T>::pack2(dsv[2 * e2], dsv[2 * e2 + 1]);
-    }
-  };
-  auto kv_update = [&](const char* st, const i32x4_t& pk, const i32x4_t& dsk) {
-#pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      const int off = d * 16 * CT * 16 + trow_off;
-      const i32x4_t ado = *(const i32x4_t*)(st + C::OFF_DOT + off);
-      const i32x4_t aq = *(const i32x4_t*)(st + C::OFF_QT + off);
-      dvacc[d] = mfma16(ado, pk, dvacc[d], T());
-      dkacc[d] = mfma16(aq, dsk, dkacc[d], T());
-    }
+    for (int m = NMA; m < NMA + NMB; ++m) mfma_slot(m, *op_ptr(s_cur, s_cur, m), unused_s, unused_p, pb, dsb);
   };
 
-  issue_tile(0);
-  if (nqt > 1) issue_tile(1);
-  if (nqt > 2) issue_tile(2);
-  wait_vmem();
-  __syncthreads();
-  i32x4_t pk, dsk;
   if (nqt > 0) {
-    scores(stage_ptr(0));
-    elementwise(stage_ptr(0), pk, dsk);
-    if (nqt > 1) scores(stage_ptr(1));
-  }
-  int j = 1;
-  for (; j + 1 < nqt; ++j) {
-    wait_vmem();
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+    wait_vmem_n<2 * C::LOADS>();  // K, V rows and tile 0
     __syncthreads();
-    if (j + 2 < nqt) issue_tile(j + 2);
-    i32x4_t pn, dsn;
-    kv_update(stage_ptr(j - 1), pk, dsk);
-    elementwise(stage_ptr(j), pn, dsn);
-    scores(stage_ptr(j + 1));
-    pk = pn;
-    dsk = dsn;
+    f32x16_t sa[NQB], pa[NQB], sb[NQB], pbb[NQB];
+    {
+      const lds_char_t* s0 = stage(IC<0>{});
+      i32x4_t dummy_p[2 * NQB], dummy_d[2 * NQB];
+#pragma unroll
+      for (int m = 0; m < NMA; ++m) mfma_slot(m, *op_ptr(s0, s0, m), sa, pa, dummy_p, dummy_d);
+    }
+    int j = 0;
+    for (; j + 4 < nqt; j += 4) {
+      step(IC<0>{}, j, sa, pa, sb, pbb);
+      step(IC<1>{}, j + 1, sb, pbb, sa, pa);
+      step(IC<2>{}, j + 2, sa, pa, sb, pbb);
+      step(IC<3>{}, j + 3, sb, pbb, sa, pa);
+    }
+    const int rest = nqt - j;  // 1..4 tiles left
+    if (rest >= 2) step(IC<0>{}, j, sa, pa, sb, pbb);
+    if (rest >= 3) step(IC<1>{}, j + 1, sb, pbb, sa, pa);
+    if (rest >= 4) step(IC<2>{}, j + 2, sa, pa, sb, pbb);
+    if (rest == 1) last_step(IC<0>{}, sa, pa);
+    else if (rest == 2) last_step(IC<1>{}, sb, pbb);
+    else if (rest == 3) last_step(IC<2>{}, sa, pa);
+    else last_step(IC<3>{}, sb, pbb);
+    wait_vmem();  // no requests beyond the last tile stay in flight
   }
-  if (nqt > 1) {
-    i32x4_t pn, dsn;
-    kv_update(stage_ptr(j - 1), pk, dsk);
-    elementwise(stage_ptr(j), pn, dsn);
-    pk = pn;
-    dsk = dsn;
-  }
-  if (nqt > 0) kv_update(stage_ptr(nqt - 1), pk, dsk);
 
-  // ---- store dK = s (dK^T)^T, dV = (dV^T)^T: lane (key col, group g) holds d = 16*dblk + 4g + v
-  if (key_ok) {
+  // ---- store dK = s (dK^T)^T, dV = (dV^T)^T for this lane's key
+  if (key < p.Lk) {
     char* dkp = (char*)p.dk + ((b * p.dk_sb + h * p.dk_sh) + (int64_t)key * p.dk_sl) * 2;
     char* dvp = (char*)p.dv + ((b * p.dv_sb + h * p.dv_sh) + (int64_t)key * p.dv_sl) * 2;
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
-      const int dc = d * 16 + 4 * grp;
-      u32x2_t wk = {Elem<T>::pack2(dkacc[d][0] * p.scale, dkacc[d][1] * p.scale),
-                    Elem<T>::pack2(dkacc[d][2] * p.scale, dkacc[d][3] * p.scale)};
-      u32x2_t wv = {Elem<T>::pack2(dvacc[d][0], dvacc[d][1]), Elem<T>::pack2(dvacc[d][2], dvacc[d][3])};
-      *(u32x2_t*)(dkp + dc * 2) = wk;
-      *(u32x2_t*)(dvp + dc * 2) = wv;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int dc = d * 32 + 8 * jj + 4 * half;
+        u32x2_t wk = {Elem<T>::pack2(dkacc[d][4 * jj] * p.scale, dkacc[d][4 * jj + 1] * p.scale),
+                      Elem<T>::pack2(dkacc[d][4 * jj + 2] * p.scale, dkacc[d][4 * jj + 3] * p.scale)};
+        u32x2_t wv = {Elem<T>::pack2(dvacc[d][4 * jj], dvacc[d][4 * jj + 1]),
+                      Elem<T>::pack2(dvacc[d][4 * jj + 2], dvacc[d][4 * jj + 3])};
+        *(u32x2_t*)(dkp + dc * 2) = wk;
+        *(u32x2_t*)(dvp + dc * 2) = wv;
+      }
     }
   }
 }

@@ -17,9 +17,16 @@ using Elt = __bf16;
 using Elt = _Float16;
 #endif
 
+// bwd_bmq() assumes the pipelined dO-only kernel serves 32 <= D <= 128.
+static_assert(DMAD_D < 32 || DMAD_D > 128 || KvPipeCfg<DMAD_D, kv_pipe_bmq<DMAD_D>()>::FITS,
+              "attn_bwd_kv_pipe_kernel must fit for this head dim");
+
 template <typename T, int D, int MODE>
 static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);
+  if constexpr (MODE == kBwdDoutOnly && KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS)
+    hipLaunchKernelGGL((attn_bwd_kv_pipe_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

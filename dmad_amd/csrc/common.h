@@ -36,7 +36,15 @@ __device__ __forceinline__ i32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
 }
 
+typedef __attribute__((address_space(3))) char lds_char_t;
+typedef __attribute__((address_space(3))) const i32x4_t lds_i32x4_t;
+typedef __attribute__((address_space(3))) const f32x4_t lds_f32x4_t;
+
 // 16 bytes per lane straight into LDS: lane i lands at lds_base + 16*i.
+__device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, lds_char_t* lds_base, uint32_t voff,
+                                               uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_base, 16, (int)voff, (int)soff, 0, 0);
+}
 __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff,
                                                uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_base, 16, (int)voff, (int)soff, 0, 0);
@@ -50,6 +58,25 @@ __device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, u32x2_t v, 
 // vmcnt(0): wait for this wave's outstanding vector-memory operations
 // (including buffer->LDS transfers). expcnt and lgkmcnt are left unconstrained.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// vmcnt(N): all but this wave's N most recent vector-memory operations are done.
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for a buffer->LDS ring: first vmcnt(N) lgkmcnt(0) (this
+// wave's LDS reads have returned and all but its N most recent vector-memory
+// requests have landed), then s_barrier. No memory fence is emitted (a fence
+// would wait for every in-flight buffer->LDS request, including the ones meant
+// to stay in flight); the asm memory clobber keeps the compiler from moving
+// memory accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void ring_sync() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt(0x0070 | (N & 15) | ((N >> 4) << 14));
+  asm volatile("s_barrier" ::: "memory");
+}
 
 // ---------------------------------------------------------------- element types
 template <typename T> struct Elem;
@@ -133,6 +160,12 @@ __device__ __forceinline__ int swz(int x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Compile-time integer as a value (for generic lambdas).
+template <int K>
+struct IC {
+  static constexpr int value = K;
+};
 
 // Scheduling-group masks for __builtin_amdgcn_sched_group_barrier.
 enum SchedMask : int { kSchedVALU = 0x2, kSchedSALU = 0x4, kSchedMFMA = 0x8, kSchedVMEM = 0x10, kSchedDSRead = 0x100,

@@ -27,10 +27,18 @@ typedef hipError_t (*DqLaunchFn)(const DqParams&, int grid, hipStream_t);
 template <typename T, int D>
 DqLaunchFn dq_select(int mode);
 
-// Query tile of the backward kernel (the layout of its statistics).
-// (The dO-only kernel runs attn_bwd_kernel; attn_bwd_kv_pipe_kernel, which
-// uses 32-query tiles, measured slower at the 14B shape and is not selected.)
-inline int bwd_bmq(int d, int mode) { return (mode == kBwdFull || d > 128) ? 32 : 64; }
+// Query tile of the dK/dV kernel, which fixes the layout of the backward
+// statistics: attn_bwd_kv_pipe_kernel's tile for dO-only 32 <= D <= 128,
+// 32 for the full-derivative and D = 256 kernels, 64 for dO-only D = 16.
+inline int bwd_bmq(int d, int mode) {
+  if (mode == kBwdFull || d > 128) return 32;
+  switch (d) {
+    case 32: return kv_pipe_bmq<32>();
+    case 64: return kv_pipe_bmq<64>();
+    case 128: return kv_pipe_bmq<128>();
+    default: return 64;
+  }
+}
 
 hipError_t launch_transpose_pad(const TransposeParams& p, int BH, hipStream_t s);
 hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s);
