@@ -606,8 +606,11 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
             if (vv & 1) pack(vv, pv, dsv, pb, dsb);
           }
         }
-      } else if (m - NMA < C::LOADS) {
-        issue_load(s_req, j + 3, m - NMA);
+      }
+      // tile j + 3's requests, spread evenly over the step
+#pragma unroll
+      for (int li = 0; li < C::LOADS; ++li) {
+        if (li * (NMA + NMB) / C::LOADS == m) issue_load(s_req, j + 3, li);
       }
       __builtin_amdgcn_sched_barrier(0);
     }

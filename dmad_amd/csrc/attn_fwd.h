@@ -409,6 +409,362 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
   }
 }
 
+// Streamed variant of attn_fwd_kernel for shapes whose K and V^T tiles split
+// evenly over the eight waves (DQK = DV = 128 in particular). Step i, after one
+// barrier, is a fixed stream of MFMAs:
+//   phase A  S^T, Sd^T of tile i+1, with the online softmax of tile i on the VALU
+//   (rescale of the accumulators, only when some row's running max moved)
+//   phase B  O~^T, C~^T += V^T P^T ... of tile i, with tile i+3's requests
+// Every MFMA's LDS operand is read four operands ahead. The ring has four
+// stages, each its own LDS object, and the loop is unrolled by four so each
+// stage reference is known at compile time: the compiler then waits for a
+// buffer->LDS request only before reading the stage it fills, and tiles are
+// requested three steps before use.
+template <int DQK, int DV, int MODE>
+struct FwdStreamCfg : FwdCfg<DQK, DV, MODE> {
+  using Base = FwdCfg<DQK, DV, MODE>;
+  static constexpr int KSPLIT = Base::KVT ? 2 : 1;  // K tile loads come as K (, Kd) pairs
+  static constexpr bool OK = Base::FITS && Base::NKI % Base::NW == 0 && Base::NVI % Base::NW == 0;
+  static constexpr int KPW = Base::NKI / Base::NW, VPW = Base::NVI / Base::NW;
+  static constexpr int LOADS = (KPW + VPW) * KSPLIT;  // vector-memory requests per wave per tile
+  static constexpr int NOPA = 2 * Base::KS * KSPLIT;  // LDS operands of phase A
+  static constexpr int NOPB = Base::DB * KSPLIT;      // LDS operands of phase B
+};
+
+template <typename T, int DQK, int DV, int MODE>
+__global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
+  struct C : FwdStreamCfg<DQK, DV, MODE> {
+    static constexpr float rescale_log2() { return RescaleSlack<T>::value; }
+  };
+  static_assert(C::OK, "shape not supported by the streamed kernel");
+  constexpr int BN = C::BN, KS = C::KS, DB = C::DB, CK = C::CK, CV = C::CV;
+  constexpr int KSPLIT = C::KSPLIT, NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
+  __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  const char* qbase = (const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2;
+  const char* kbase = (const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2;
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + DQK) * 2);
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + DQK) * 2);
+  const uint32_t vt_bytes = (uint32_t)((int64_t)C::VT_ROWS * p.LKP * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, q_bytes);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.vt + (int64_t)bh * vt_bytes, vt_bytes);
+  __amdgpu_buffer_rsrc_t rtq = rq, rtk = rk, rtv = rv;
+  if constexpr (C::JVP) rtq = make_rsrc((const char*)p.tq + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  if constexpr (C::KVT) {
+    rtk = make_rsrc((const char*)p.tk + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+    rtv = make_rsrc((const char*)p.tvt + (int64_t)bh * vt_bytes, vt_bytes);
+  }
+
+  // ---- Q (and Qd) slices in registers: B operand of S^T = K Q^T
+  const int qrow = qt * C::BM + wave * C::QW + col;
+  const uint32_t qoff = (uint32_t)((int64_t)qrow * p.q_sl * 2) + grp * 16;
+  i32x4_t qr[KS], tqr[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qr[s] = buf_load16(rq, qoff + s * 64);
+    if constexpr (C::JVP) tqr[s] = buf_load16(rtq, qoff + s * 64);
+  }
+
+  // ---- per-lane DMA offsets (tile independent)
+  uint32_t koff[C::KPW], voff[C::VPW];
+#pragma unroll
+  for (int j = 0; j < C::KPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CK, phys = pch % CK;
+    const int logical = phys ^ kswz16<CK>(row);
+    koff[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < C::VPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int d = pch / CV, phys = pch % CV;
+    const int logical = phys ^ swz<CV>(d & 15);
+    voff[j] = (uint32_t)(d * p.LKP * 2) + logical * 16;
+  }
+  const uint32_t k_tile_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
+
+  auto stage = [&](auto kk) -> lds_char_t* {
+    constexpr int k = decltype(kk)::value & 3;
+    if constexpr (k == 0) return (lds_char_t*)stg0;
+    else if constexpr (k == 1) return (lds_char_t*)stg1;
+    else if constexpr (k == 2) return (lds_char_t*)stg2;
+    else return (lds_char_t*)stg3;
+  };
+  // request li (0 <= li < C::LOADS) of tile kt into stage st; tiles at or beyond
+  // the end read zeros or in-range rows into a stage nobody reads again
+  auto issue_load = [&](lds_char_t* st, int kt, int li) {
+    if (li < C::KPW * KSPLIT) {
+      const int jj = li / KSPLIT, i = wave + jj * C::NW;
+      const uint32_t ks = (uint32_t)kt * k_tile_step;
+      if (KSPLIT == 2 && (li & 1)) buf_load16_lds(rtk, st + C::OFF_KT + i * 1024, koff[jj], ks);
+      else buf_load16_lds(rk, st + C::OFF_K + i * 1024, koff[jj], ks);
+    } else {
+      const int lv = li - C::KPW * KSPLIT, jj = lv / KSPLIT, i = wave + jj * C::NW;
+      const uint32_t vs = (uint32_t)kt * BN * 2;
+      if (KSPLIT == 2 && (lv & 1)) buf_load16_lds(rtv, st + C::OFF_VT + i * 1024, voff[jj], vs);
+      else buf_load16_lds(rv, st + C::OFF_V + i * 1024, voff[jj], vs);
+    }
+  };
+
+  // ---- LDS read offsets (tile independent): kx[2 s + sb] for K chunk s of
+  // 16-key block sb, vx for V^T rows; stage, tile part and d block are immediates
+  int kx[2 * KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const int R = key_of_row16(sb, col);
+      kx[2 * s + sb] = R * CK * 16 + (((4 * s + grp) ^ kswz16<CK>(R)) << 4);
+    }
+  }
+  int vx = col * CV * 16 + ((grp ^ swz<CV>(col)) << 4);
+  // Re-defines the offsets at each step (an empty asm), so that stage base +
+  // offset is formed per step and folds into the LDS instructions' immediate
+  // instead of being hoisted into one register per stage.
+  auto pin_offsets = [&]() {
+#pragma unroll
+    for (int x = 0; x < 2 * KS; ++x) asm volatile("" : "+v"(kx[x]));
+    asm volatile("" : "+v"(vx));
+  };
+
+  f32x4_t oacc[DB], cacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      oacc[d][v] = 0.f;
+      cacc[d][v] = 0.f;
+    }
+  }
+  float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
+  const int ntiles = (p.Lk + BN - 1) / BN;
+
+  // LDS operand o of a step: o < NOPA reads a K (then Kd) chunk of the next
+  // tile (s = k slice, sb = 16-key block), o >= NOPA a V^T (then Vd^T) block of this tile
+  auto op_ptr = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int o) -> lds_i32x4_t* {
+    if (o < NOPA) {
+      const int kd = o / (2 * KS), r = o % (2 * KS);
+      return (lds_i32x4_t*)(s_next + (kd ? C::OFF_KT : C::OFF_K) + kx[r]);
+    }
+    const int ob = o - NOPA, vd = ob / DB, d = ob % DB;
+    return (lds_i32x4_t*)(s_cur + (vd ? C::OFF_VT : C::OFF_V) + d * 16 * CV * 16 + vx);
+  };
+  const f32x4_t zero4 = {};
+  // the MFMAs of operand o
+  auto mfma_op = [&](int o, i32x4_t a, f32x4_t (&sc)[2], f32x4_t (&tc)[2], i32x4_t pk, i32x4_t hk) {
+    if (o < NOPA) {
+      const int kd = o / (2 * KS), r = o % (2 * KS), s = r >> 1, sb = r & 1;
+      if (kd == 0) {
+        sc[sb] = mfma16(a, qr[s], s == 0 ? zero4 : sc[sb], T());
+        if constexpr (C::JVP) tc[sb] = mfma16(a, tqr[s], s == 0 ? zero4 : tc[sb], T());
+      } else {
+        tc[sb] = mfma16(a, qr[s], tc[sb], T());
+      }
+    } else {
+      const int ob = o - NOPA, vd = ob / DB, d = ob % DB;
+      if (vd == 0) {
+        oacc[d] = mfma16(a, pk, oacc[d], T());
+        if constexpr (C::JVP) cacc[d] = mfma16(a, hk, cacc[d], T());
+      } else {
+        cacc[d] = mfma16(a, pk, cacc[d], T());
+      }
+    }
+  };
+
+  // Online softmax of one tile split into 16 micro-steps (log2 domain; the 4
+  // lane groups of a query share m). Leaves P~ and H~ packed as B operands
+  // (keys 8*grp + e in pk, hk) and alpha, the accumulator rescale factor.
+  struct Soft {
+    float mx, alpha, neg_m, ls, rs;
+    float pv[2], hv[2];
+    bool moved;
+  };
+  auto soft_micro = [&](int u, Soft& sm, const f32x4_t (&sc)[2], const f32x4_t (&tc)[2], i32x4_t& pk,
+                        i32x4_t& hk) {
+    if (u == 0) {
+      sm.mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                    fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+      sm.ls = 0.f;
+      sm.rs = 0.f;
+    } else if (u == 1) {
+      sm.mx = fmaxf(sm.mx, other_row16(sm.mx));
+    } else if (u == 2) {
+      sm.mx = fmaxf(sm.mx, other_half(sm.mx)) * p.scale_log2;
+      sm.moved = __builtin_amdgcn_ballot_w64(sm.mx > m_i + C::rescale_log2()) != 0;
+      const float m_new = sm.moved ? fmaxf(m_i, sm.mx) : m_i;
+      sm.alpha = fast_exp2(m_i - m_new);
+      m_i = m_new;
+      sm.neg_m = -m_new;
+    } else if (u < 11) {
+      const int e = u - 3, sb = e >> 2, v = e & 3;
+      sm.pv[e & 1] = fast_exp2(fmaf(sc[sb][v], p.scale_log2, sm.neg_m));
+      sm.ls += sm.pv[e & 1];
+      if constexpr (C::JVP) {
+        sm.hv[e & 1] = sm.pv[e & 1] * (tc[sb][v] * p.scale);
+        sm.rs += sm.hv[e & 1];
+      }
+      if (e & 1) {
+        pk[e >> 1] = (int)Elem<T>::pack2(sm.pv[0], sm.pv[1]);
+        if constexpr (C::JVP) hk[e >> 1] = (int)Elem<T>::pack2(sm.hv[0], sm.hv[1]);
+      }
+    } else if (u < 15) {
+    } else {
+      l_i = l_i * sm.alpha + sm.ls;
+      if constexpr (C::JVP) r_i = r_i * sm.alpha + sm.rs;
+    }
+  };
+  auto rescale = [&](float alpha) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        oacc[d][v] *= alpha;
+        if constexpr (C::JVP) cacc[d][v] *= alpha;
+      }
+    }
+  };
+
+  // step i (i + 1 < ntiles, i % 4 == kk): phase A on tile i+1's K, softmax of tile i (sc, tc);
+  // phase B on tile i's V; requests tile i+3
+  auto step = [&](auto kk, int i, const f32x4_t (&sc)[2], const f32x4_t (&tc)[2], f32x4_t (&sn)[2],
+                  f32x4_t (&tn)[2]) {
+    constexpr int k = decltype(kk)::value;
+    ring_sync<C::LOADS>();  // tile i+1 has landed (tile i+2 may be in flight)
+    pin_offsets();
+    const lds_char_t* s_next = stage(IC<k + 1>{});
+    const lds_char_t* s_cur = stage(IC<k>{});
+    lds_char_t* s_req = stage(IC<k + 3>{});
+    i32x4_t opr[PF];
+#pragma unroll
+    for (int o = 0; o < PF; ++o) opr[o] = *op_ptr(s_next, s_cur, o);
+    Soft sm;
+    i32x4_t pk, hk;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int o = 0; o < NOPA; ++o) {
+      mfma_op(o, opr[o % PF], sn, tn, pk, hk);
+      if (o + PF < NOP) opr[o % PF] = *op_ptr(s_next, s_cur, o + PF);
+#pragma unroll
+      for (int u = o * 16 / NOPA; u < (o + 1) * 16 / NOPA; ++u) soft_micro(u, sm, sc, tc, pk, hk);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // keep the softmax in phase A: the values are used here, before the branch
+    asm volatile("" : "+v"(pk), "+v"(hk), "+v"(l_i), "+v"(r_i));
+    if (sm.moved) rescale(sm.alpha);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int o = NOPA; o < NOP; ++o) {
+      mfma_op(o, opr[o % PF], sn, tn, pk, hk);
+      if (o + PF < NOP) opr[o % PF] = *op_ptr(s_next, s_cur, o + PF);
+      if (o - NOPA < C::LOADS) issue_load(s_req, i + 3, o - NOPA);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // last tile (may hold keys >= Lk): masked softmax, rescale, PV
+  auto last_step = [&](auto kk, int i, f32x4_t (&sc)[2], const f32x4_t (&tc)[2]) {
+    const lds_char_t* s_cur = stage(kk);
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (i * BN + 8 * grp + 4 * sb + v >= p.Lk) sc[sb][v] = -__builtin_inff();
+      }
+    }
+    Soft sm;
+    i32x4_t pk, hk;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) soft_micro(u, sm, sc, tc, pk, hk);
+    rescale(sm.alpha);
+    f32x4_t un_s[2], un_t[2];
+#pragma unroll
+    for (int o = NOPA; o < NOP; ++o) mfma_op(o, *op_ptr(s_cur, s_cur, o), un_s, un_t, pk, hk);
+  };
+
+  // ---- prologue: tiles 0..2 requested, scores of tile 0
+#pragma unroll
+  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+#pragma unroll
+  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+#pragma unroll
+  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+  ring_sync<2 * C::LOADS>();  // Q slices and tile 0
+  f32x4_t sa[2], ta[2], sb2[2], tb[2];
+  {
+    const lds_char_t* s0 = stage(IC<0>{});
+    i32x4_t pk0 = {}, hk0 = {};
+#pragma unroll
+    for (int o = 0; o < NOPA; ++o) mfma_op(o, *op_ptr(s0, s0, o), sa, ta, pk0, hk0);
+  }
+  int i = 0;
+  for (; i + 4 < ntiles; i += 4) {
+    step(IC<0>{}, i, sa, ta, sb2, tb);
+    step(IC<1>{}, i + 1, sb2, tb, sa, ta);
+    step(IC<2>{}, i + 2, sa, ta, sb2, tb);
+    step(IC<3>{}, i + 3, sb2, tb, sa, ta);
+  }
+  const int rest = ntiles - i;  // 1..4 tiles left
+  if (rest >= 2) step(IC<0>{}, i, sa, ta, sb2, tb);
+  if (rest >= 3) step(IC<1>{}, i + 1, sb2, tb, sa, ta);
+  if (rest >= 4) step(IC<2>{}, i + 2, sa, ta, sb2, tb);
+  if (rest == 1) last_step(IC<0>{}, i, sa, ta);
+  else if (rest == 2) last_step(IC<1>{}, i + 1, sb2, tb);
+  else if (rest == 3) last_step(IC<2>{}, i + 2, sa, ta);
+  else last_step(IC<3>{}, i + 3, sb2, tb);
+  wait_vmem();  // no requests beyond the last tile stay in flight
+
+  // ---- epilogue: lane (query col, group g) holds d = 16*dblk + 4g + v
+  float l = l_i + other_row16(l_i);
+  l = l + other_half(l);
+  const float inv_l = 1.0f / l;
+  float mu = 0.f;
+  if constexpr (C::JVP) {
+    float r = r_i + other_row16(r_i);
+    r = r + other_half(r);
+    mu = r * inv_l;
+  }
+  const int64_t obase = b * p.o_sb + h * p.o_sh;
+  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + DV) * 2);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
+  __amdgpu_buffer_rsrc_t rto = ro;
+  if constexpr (C::JVP) rto = make_rsrc((char*)p.to + obase * 2, o_bytes);
+  const uint32_t orow = (uint32_t)((int64_t)qrow * p.o_sl * 2);
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+    const int dc = d * 16 + 4 * grp;
+    float ov[4], tv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      ov[v] = oacc[d][v] * inv_l;
+      if constexpr (C::JVP) tv[v] = cacc[d][v] * inv_l - mu * ov[v];
+    }
+    const uint32_t off = orow + dc * 2;
+    u32x2_t w = {Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])};
+    buf_store8(ro, w, off);
+    if constexpr (C::JVP) {
+      u32x2_t wt = {Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])};
+      buf_store8(rto, wt, off);
+    }
+  }
+  if (grp == 0 && qrow < p.Lq) {
+    const int64_t si = (int64_t)bh * p.Lq + qrow;
+    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    if constexpr (C::JVP) p.mu[si] = mu;
+  }
+}
+
 // Single-stage-per-tile variant for head dims whose four-stage ring does not
 // fit in LDS (a 256-wide Q/K or V head in the full JVP mode): scores, softmax
 // and PV of each 64- or 32-key tile run back to back.

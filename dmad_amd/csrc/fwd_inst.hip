@@ -19,7 +19,9 @@ using Elt = _Float16;
 
 template <typename T, int DQK, int DV, int MODE>
 static hipError_t fwd_launch(const FwdParams& p, int grid, hipStream_t s) {
-  if constexpr (FwdCfg<DQK, DV, MODE>::FITS)
+  if constexpr (FwdStreamCfg<DQK, DV, MODE>::OK)
+    hipLaunchKernelGGL((attn_fwd_stream_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(512), 0, s, p);
+  else if constexpr (FwdCfg<DQK, DV, MODE>::FITS)
     hipLaunchKernelGGL((attn_fwd_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(512), 0, s, p);
   else
     hipLaunchKernelGGL((attn_fwd_simple_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(256), 0, s, p);
