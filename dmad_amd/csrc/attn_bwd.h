@@ -686,6 +686,334 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   }
 }
 
+// dO-only dK/dV pass reading the transposed operands Q^T, dO^T straight from
+// the row-major Q, dO tiles with lds_read_tr16 (no transposed copies in HBM or
+// LDS). 4 waves x 32 keys, 64-query steps through a four-stage ring, the same
+// fixed MFMA stream as attn_bwd_kv_pipe_kernel:
+//   S, dP of tile j+1 (P, dS of tile j on the VALU), then
+//   dV^T += dO^T P, dK^T += Q^T dS of tile j (tile j+3 requested meanwhile).
+template <int D, int BMQ_>
+struct KvTrCfg {
+  static constexpr int NW = 4;
+  static constexpr int BK = 32 * NW;
+  static constexpr int BMQ = BMQ_;
+  static constexpr int NQB = BMQ / 32;
+  static constexpr int KS = D / 16;
+  static constexpr int DB = D / 32;
+  static constexpr int CR = D / 8;  // 16-byte chunks per Q / dO row
+  static constexpr int ROWB = D * 2;
+  static constexpr int ROW_BYTES = BMQ * ROWB;
+  static constexpr int OFF_Q = 0;
+  static constexpr int OFF_DO = ROW_BYTES;
+  static constexpr int OFF_ST = 2 * ROW_BYTES;
+  static constexpr int STAT_BYTES = 2 * BMQ * 4;
+  static constexpr int STAGE = (OFF_ST + STAT_BYTES + 1023) / 1024 * 1024;
+  static constexpr int NSTAGE = 4;
+  static constexpr int NRI = BMQ * CR / 64;  // wave-wide 1 KiB loads per row tile
+  static constexpr int RPW = NRI / NW;
+  static constexpr int ST_LANES = STAT_BYTES / 16 / NW;
+  static constexpr bool FITS = D == 128 && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr int LOADS = 2 * RPW + 1;
+};
+
+// Query tile of attn_bwd_kv_tr_kernel.
+constexpr int kKvTrBmq = 32;
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
+  using C = KvTrCfg<D, kKvTrBmq>;
+  constexpr int BMQ = C::BMQ, NQB = C::NQB, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
+  static_assert(C::FITS, "configuration does not fit");
+  static_assert(CR == 16, "trswz16 assumes 16 chunks per row");
+  __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  const int nkt = (p.Lk + C::BK - 1) / C::BK;
+  const int work = xcd_remap(blockIdx.x, nkt * p.B * p.H);
+  const int bh = work / nkt, kt = work - bh * nkt;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int nqt = p.LQP / BMQ;
+
+  const int key = kt * C::BK + wave * 32 + col;
+
+  // ---- stationary K, V rows: B operands of S = Q K^T and dP = dO V^T
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes);
+  i32x4_t kreg[KS], vreg[KS];
+  {
+    const uint32_t ko = (uint32_t)((int64_t)key * p.k_sl * 2) + half * 16;
+    const uint32_t vo = (uint32_t)((int64_t)key * p.v_sl * 2) + half * 16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kreg[s] = buf_load16(rk, ko + s * 32);
+      vreg[s] = buf_load16(rv, vo + s * 32);
+    }
+  }
+
+  // ---- query-side resources and per-lane DMA offsets
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
+  const uint32_t st_bytes = (uint32_t)((int64_t)p.LQP * 2 * 4);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const char*)p.dout + (b * p.do_sb + h * p.do_sh) * 2, do_bytes);
+  const __amdgpu_buffer_rsrc_t rst = make_rsrc((const char*)p.stats + (int64_t)bh * st_bytes, st_bytes);
+  constexpr int RPW = C::RPW;
+  uint32_t roff_q[RPW], roff_do[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CR, phys = pch % CR;
+    const int logical = phys ^ trswz16(row & 15);
+    roff_q[j] = (uint32_t)((int64_t)row * p.q_sl * 2) + logical * 16;
+    roff_do[j] = (uint32_t)((int64_t)row * p.do_sl * 2) + logical * 16;
+  }
+  const uint32_t q_step = (uint32_t)((int64_t)BMQ * p.q_sl * 2);
+  const uint32_t do_step = (uint32_t)((int64_t)BMQ * p.do_sl * 2);
+  static_assert(C::ST_LANES * C::NW * 16 == C::STAT_BYTES, "statistics split evenly over the waves");
+  const bool st_lane = lane >= wave * C::ST_LANES && lane < (wave + 1) * C::ST_LANES;
+
+  auto stage = [&](auto kk) -> lds_char_t* {
+    constexpr int k = decltype(kk)::value & 3;
+    if constexpr (k == 0) return (lds_char_t*)stg0;
+    else if constexpr (k == 1) return (lds_char_t*)stg1;
+    else if constexpr (k == 2) return (lds_char_t*)stg2;
+    else return (lds_char_t*)stg3;
+  };
+  // request li (0 <= li < C::LOADS) of tile qt into stage st; tiles at or beyond
+  // the end read zeros or in-range rows into a stage nobody reads again
+  auto issue_load = [&](lds_char_t* st, int qt, int li) {
+    if (li < 2 * RPW) {
+      const int jj = li >> 1, i = wave + jj * C::NW;
+      if (li & 1) buf_load16_lds(rdo, st + C::OFF_DO + i * 1024, roff_do[jj], (uint32_t)qt * do_step);
+      else buf_load16_lds(rq, st + C::OFF_Q + i * 1024, roff_q[jj], (uint32_t)qt * q_step);
+    } else {
+      if (st_lane) buf_load16_lds(rst, st + C::OFF_ST, lane * 16, (uint32_t)qt * C::STAT_BYTES);
+    }
+  };
+
+  // ---- LDS read offsets. Row-wise reads (S, dP): row 32 qb + perm32(col), chunk 2s + half.
+  int sx[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int r = perm32(col);
+    sx[s] = r * ROWB + (((2 * s + half) ^ trswz16(r & 15)) << 4);
+  }
+  // Transposed reads (dO^T, Q^T blocks): lane group g = lane / 16 covers d0 = 32 db + 16 (g & 1)
+  // and queries 16 u + 8 (g >> 1) + (0..3 | 4..7); lane 4r + c of the group points at row r,
+  // elements d0 + 4c .. d0 + 4c + 3.
+  int tx[DB][2];
+  {
+    const int g = lane >> 4, r = (lane & 15) >> 2, c = lane & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int row = 8 * (g >> 1) + 4 * hh + r;  // plus 16 u
+        const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
+        tx[db][hh] = row * ROWB + ((chunk ^ trswz16(row & 15)) << 4) + 8 * (c & 1);
+      }
+    }
+  }
+  auto pin_offsets = [&]() {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(sx[s]));
+#pragma unroll
+    for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(tx[db][0]), "+v"(tx[db][1]));
+  };
+
+  f32x16_t dkacc[DB], dvacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      dkacc[d][v] = 0.f;
+      dvacc[d][v] = 0.f;
+    }
+  }
+
+  constexpr int PF = 4;
+  constexpr int NMA = 2 * KS * NQB;   // S, dP MFMAs
+  constexpr int NMB = 4 * NQB * DB;   // dV^T, dK^T MFMAs
+  constexpr int NS = NMA + NMB;
+  constexpr int NVAL = 16 * NQB;      // P, dS values per lane per tile
+  const f32x16_t zero16 = {};
+  // operand m: m < NMA reads Q / dO rows of the next tile (s = m / (2 NQB)),
+  // otherwise dO^T / Q^T of this tile (u = 16-query chunk, db = 32-row d block)
+  auto load_op = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int m) -> i32x4_t {
+    if (m < NMA) {
+      const int s = m / (2 * NQB), r = m % (2 * NQB), qb = r >> 1;
+      return *(lds_i32x4_t*)(s_next + ((r & 1) ? C::OFF_DO : C::OFF_Q) + qb * 32 * ROWB + sx[s]);
+    }
+    const int mm = m - NMA, u = mm / (2 * DB), r = mm % (2 * DB), db = r >> 1;
+    const lds_char_t* base = s_cur + ((r & 1) ? C::OFF_Q : C::OFF_DO) + u * 16 * ROWB;
+    const u32x2_t lo = lds_read_tr16(base + tx[db][0]);
+    const u32x2_t hi = lds_read_tr16(base + tx[db][1]);
+    return i32x4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+  };
+  // statistics of 16-query chunk u: lse (log2 units), Delta for queries 16 u + 8 half + 0..7
+  struct Stats {
+    f32x4_t l[2], d[2];
+  };
+  auto load_stats = [&](const lds_char_t* st, int u, Stats& sv) {
+    const lds_char_t* sst = st + C::OFF_ST;
+    const int q0 = 16 * u + 8 * half;
+    sv.l[0] = *(lds_f32x4_t*)(sst + 4 * q0);
+    sv.l[1] = *(lds_f32x4_t*)(sst + 4 * (q0 + 4));
+    sv.d[0] = *(lds_f32x4_t*)(sst + 4 * (BMQ + q0));
+    sv.d[1] = *(lds_f32x4_t*)(sst + 4 * (BMQ + q0 + 4));
+  };
+  // value v: block qb = v / 16, C-tile value (v % 16) = query 32 qb + 16 t + 8 half + e
+  auto value = [&](int v, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], const Stats& sv, float (&pv)[2],
+                   float (&dsv)[2]) {
+    const int qb = v / 16, t = (v % 16) / 8, e = v % 8;
+    const float l2 = sv.l[e >> 2][e & 3], dl = sv.d[e >> 2][e & 3];
+    const float pe = fast_exp2(fmaf(sc[qb][8 * t + e], p.scale_log2, -l2));
+    pv[v & 1] = pe;
+    dsv[v & 1] = pe * (dpc[qb][8 * t + e] - dl);
+  };
+  auto pack = [&](int v, const float (&pv)[2], const float (&dsv)[2], i32x4_t (&pb)[2 * NQB],
+                  i32x4_t (&dsb)[2 * NQB]) {
+    const int u = v / 8, e2 = (v % 8) >> 1;
+    pb[u][e2] = (int)Elem<T>::pack2(pv[0], pv[1]);
+    dsb[u][e2] = (int)Elem<T>::pack2(dsv[0], dsv[1]);
+  };
+  auto mfma_slot = [&](int m, i32x4_t op, f32x16_t (&sn)[NQB], f32x16_t (&dpn)[NQB], const i32x4_t (&pb)[2 * NQB],
+                       const i32x4_t (&dsb)[2 * NQB]) {
+    if (m < NMA) {
+      const int s = m / (2 * NQB), r = m % (2 * NQB), qb = r >> 1;
+      if (r & 1) dpn[qb] = mfma32(op, vreg[s], s == 0 ? zero16 : dpn[qb], T());
+      else sn[qb] = mfma32(op, kreg[s], s == 0 ? zero16 : sn[qb], T());
+    } else {
+      const int mm = m - NMA, u = mm / (2 * DB), r = mm % (2 * DB), db = r >> 1;
+      if (r & 1) dkacc[db] = mfma32(op, dsb[u], dkacc[db], T());
+      else dvacc[db] = mfma32(op, pb[u], dvacc[db], T());
+    }
+  };
+
+  // step j (j + 1 < nqt, j % 4 == kk)
+  auto step = [&](auto kk, int j, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], f32x16_t (&sn)[NQB],
+                  f32x16_t (&dpn)[NQB]) {
+    constexpr int k = decltype(kk)::value;
+    ring_sync<C::LOADS>();  // tile j + 1 has landed (tile j + 2 may be in flight)
+    pin_offsets();
+    const lds_char_t* s_next = stage(IC<k + 1>{});
+    const lds_char_t* s_cur = stage(IC<k>{});
+    lds_char_t* s_req = stage(IC<k + 3>{});
+    Stats sv[2];  // chunks u (in use) and u + 1 (landing)
+    load_stats(s_cur, 0, sv[0]);
+    i32x4_t opr[PF];
+#pragma unroll
+    for (int m = 0; m < PF; ++m) opr[m] = load_op(s_next, s_cur, m);
+    i32x4_t pb[2 * NQB], dsb[2 * NQB];
+    float pv[2], dsv[2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < NS; ++m) {
+      mfma_slot(m, opr[m % PF], sn, dpn, pb, dsb);
+      if (m + PF < NS) opr[m % PF] = load_op(s_next, s_cur, m + PF);
+      // values v at slot 3v/2: all of block u are packed before its first update MFMA
+#pragma unroll
+      for (int v = 0; v < NVAL; ++v) {
+        if (3 * v / 2 == m) {
+          if (v % 8 == 0 && v + 8 < NVAL) load_stats(s_cur, v / 8 + 1, sv[(v / 8 + 1) & 1]);
+          value(v, sc, dpc, sv[(v / 8) & 1], pv, dsv);
+          if (v & 1) pack(v, pv, dsv, pb, dsb);
+        }
+      }
+#pragma unroll
+      for (int li = 0; li < C::LOADS; ++li) {
+        if (li * NS / C::LOADS == m) issue_load(s_req, j + 3, li);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  static_assert(3 * (NVAL - 1) / 2 < NMA + 8 * NQB, "values of the last block must precede its updates");
+  auto last_step = [&](auto kk, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB]) {
+    const lds_char_t* s_cur = stage(kk);
+    i32x4_t pb[2 * NQB], dsb[2 * NQB];
+    float pv[2], dsv[2];
+    Stats sv;
+#pragma unroll
+    for (int v = 0; v < NVAL; ++v) {
+      if (v % 8 == 0) load_stats(s_cur, v / 8, sv);
+      value(v, sc, dpc, sv, pv, dsv);
+      if (v & 1) pack(v, pv, dsv, pb, dsb);
+    }
+    f32x16_t un_s[NQB], un_p[NQB];
+#pragma unroll
+    for (int m = NMA; m < NS; ++m) mfma_slot(m, load_op(s_cur, s_cur, m), un_s, un_p, pb, dsb);
+  };
+
+  if (nqt > 0) {
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+    ring_sync<2 * C::LOADS>();  // K, V rows and tile 0
+    f32x16_t sa[NQB], pa[NQB], sb[NQB], pbb[NQB];
+    {
+      const lds_char_t* s0 = stage(IC<0>{});
+      i32x4_t dummy_p[2 * NQB], dummy_d[2 * NQB];
+#pragma unroll
+      for (int m = 0; m < NMA; ++m) mfma_slot(m, load_op(s0, s0, m), sa, pa, dummy_p, dummy_d);
+    }
+    int j = 0;
+    for (; j + 4 < nqt; j += 4) {
+      step(IC<0>{}, j, sa, pa, sb, pbb);
+      step(IC<1>{}, j + 1, sb, pbb, sa, pa);
+      step(IC<2>{}, j + 2, sa, pa, sb, pbb);
+      step(IC<3>{}, j + 3, sb, pbb, sa, pa);
+    }
+    const int rest = nqt - j;  // 1..4 tiles left
+    if (rest >= 2) step(IC<0>{}, j, sa, pa, sb, pbb);
+    if (rest >= 3) step(IC<1>{}, j + 1, sb, pbb, sa, pa);
+    if (rest >= 4) step(IC<2>{}, j + 2, sa, pa, sb, pbb);
+    if (rest == 1) last_step(IC<0>{}, sa, pa);
+    else if (rest == 2) last_step(IC<1>{}, sb, pbb);
+    else if (rest == 3) last_step(IC<2>{}, sa, pa);
+    else last_step(IC<3>{}, sb, pbb);
+    wait_vmem();  // no requests beyond the last tile stay in flight
+  }
+
+  // ---- store dK = s (dK^T)^T, dV = (dV^T)^T for this lane's key
+  if (key < p.Lk) {
+    char* dkp = (char*)p.dk + ((b * p.dk_sb + h * p.dk_sh) + (int64_t)key * p.dk_sl) * 2;
+    char* dvp = (char*)p.dv + ((b * p.dv_sb + h * p.dv_sh) + (int64_t)key * p.dv_sl) * 2;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int dc = d * 32 + 8 * jj + 4 * half;
+        u32x2_t wk = {Elem<T>::pack2(dkacc[d][4 * jj] * p.scale, dkacc[d][4 * jj + 1] * p.scale),
+                      Elem<T>::pack2(dkacc[d][4 * jj + 2] * p.scale, dkacc[d][4 * jj + 3] * p.scale)};
+        u32x2_t wv = {Elem<T>::pack2(dvacc[d][4 * jj], dvacc[d][4 * jj + 1]),
+                      Elem<T>::pack2(dvacc[d][4 * jj + 2], dvacc[d][4 * jj + 3])};
+        *(u32x2_t*)(dkp + dc * 2) = wk;
+        *(u32x2_t*)(dvp + dc * 2) = wv;
+      }
+    }
+  }
+}
+
+// Query tile of the dO-only dK/dV kernel chosen for head dim D (it fixes the
+// layout of the backward statistics).
+template <int D>
+constexpr int dout_only_kv_bmq() {
+  if constexpr (KvTrCfg<D, kKvTrBmq>::FITS) return kKvTrBmq;
+  else if constexpr (KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS) return kv_pipe_bmq<D>();
+  else return BwdCfg<D, kBwdDoutOnly>::BMQ;
+}
+
 // Per-row statistics for the backward, one thread per (b*h, query row):
 //   A layout  [BH][LQP/BA][2][BA]: lse2 = LSE*log2(e), D = rowsum(dO*O)
 //   B layout  [BH][LQP/32][4][32]: lse2, D' = rowsum(dO*O) + rowsum(dOd*Od) - mu*rho, mu, rho

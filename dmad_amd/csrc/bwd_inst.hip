@@ -17,13 +17,12 @@ using Elt = __bf16;
 using Elt = _Float16;
 #endif
 
-// bwd_bmq() assumes the pipelined dO-only kernel serves 32 <= D <= 128.
-static_assert(DMAD_D < 32 || DMAD_D > 128 || KvPipeCfg<DMAD_D, kv_pipe_bmq<DMAD_D>()>::FITS,
-              "attn_bwd_kv_pipe_kernel must fit for this head dim");
-
+// The launch choice below mirrors dout_only_kv_bmq<D>().
 template <typename T, int D, int MODE>
 static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
-  if constexpr (MODE == kBwdDoutOnly && KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS)
+  if constexpr (MODE == kBwdDoutOnly && KvTrCfg<D, kKvTrBmq>::FITS)
+    hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
+  else if constexpr (MODE == kBwdDoutOnly && KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS)
     hipLaunchKernelGGL((attn_bwd_kv_pipe_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);

@@ -161,6 +161,24 @@ __device__ __forceinline__ int swz(int x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ds_read_b64_tr_b16 (gfx950 LDS transpose read), checked on the device with a
+// lane probe: in each group of 16 lanes, lane 4r + c (r, c = 0..3) points at 4
+// consecutive 16-bit elements that form columns 4c..4c+3 of row r of a 4 x 16
+// block; lane i of the group receives column i, i.e. (row 0..3, col i).
+__device__ __forceinline__ u32x2_t lds_read_tr16(const lds_char_t* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)p));
+}
+
+// XOR swizzle of the 16-byte chunk index for LDS row tiles of 16 chunks per row
+// that are read both row-wise (16 B per lane, 16 lanes on 16 consecutive rows)
+// and with lds_read_tr16 (8 B per lane, 4 aligned consecutive rows x 4 aligned
+// chunks per 32 lanes): a bijection on the row index modulo 16 whose upper two
+// bits are the row index modulo 4, so both patterns touch 16 distinct 16-byte
+// slots of the 256-byte bank window.
+__device__ __forceinline__ int trswz16(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
 // Compile-time integer as a value (for generic lambdas).
 template <int K>
 struct IC {

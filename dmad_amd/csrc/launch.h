@@ -28,15 +28,15 @@ template <typename T, int D>
 DqLaunchFn dq_select(int mode);
 
 // Query tile of the dK/dV kernel, which fixes the layout of the backward
-// statistics: attn_bwd_kv_pipe_kernel's tile for dO-only 32 <= D <= 128,
-// 32 for the full-derivative and D = 256 kernels, 64 for dO-only D = 16.
+// statistics (the full-derivative kernel always uses 32-query tiles).
 inline int bwd_bmq(int d, int mode) {
-  if (mode == kBwdFull || d > 128) return 32;
+  if (mode == kBwdFull) return BwdCfg<128, kBwdFull>::BMQ;
   switch (d) {
-    case 32: return kv_pipe_bmq<32>();
-    case 64: return kv_pipe_bmq<64>();
-    case 128: return kv_pipe_bmq<128>();
-    default: return 64;
+    case 16: return dout_only_kv_bmq<16>();
+    case 32: return dout_only_kv_bmq<32>();
+    case 64: return dout_only_kv_bmq<64>();
+    case 128: return dout_only_kv_bmq<128>();
+    default: return dout_only_kv_bmq<256>();
   }
 }
 
