@@ -511,4 +511,268 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_pipe_kernel(DqParams p) {
   }
 }
 
+// dO-only dQ pass reading K^T straight from the row-major K tile with
+// lds_read_tr16: 4 waves x 32 queries (lane <-> query, so the statistics are
+// per-lane scalars), 32-key steps through a four-stage ring of K, V row tiles.
+// Step j (after one barrier) is a fixed MFMA stream:
+//   S^T = K Q^T, dP^T = V dO^T of tile j+1 (P, dS of tile j on the VALU), then
+//   dQ^T += K^T dS^T of tile j (tile j+3 requested meanwhile).
+// Keys at or beyond Lk read K = V = 0; their (finite) dS meets a zero K^T
+// column, so no key mask is needed. Padded queries carry lse = +inf (P = 0).
+template <int D>
+struct DqTrCfg {
+  static constexpr int NW = 4;
+  static constexpr int BM = 32 * NW;
+  static constexpr int BN = 32;
+  static constexpr int KS = D / 16;
+  static constexpr int DB = D / 32;
+  static constexpr int CR = D / 8;
+  static constexpr int ROWB = D * 2;
+  static constexpr int ROW_BYTES = BN * ROWB;
+  static constexpr int OFF_K = 0;
+  static constexpr int OFF_V = ROW_BYTES;
+  static constexpr int STAGE = 2 * ROW_BYTES;
+  static constexpr int NSTAGE = 4;
+  static constexpr int NRI = BN * CR / 64;
+  static constexpr int RPW = NRI / NW;
+  static constexpr bool FITS = D == 128 && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr int LOADS = 2 * RPW;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
+  using C = DqTrCfg<D>;
+  constexpr int BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
+  static_assert(C::FITS, "configuration does not fit");
+  static_assert(CR == 16, "trswz16 assumes 16 chunks per row");
+  __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int ntiles = (p.Lk + BN - 1) / BN;
+
+  // ---- this lane's query: Q, dO rows (B operands) and statistics
+  const int query = qt * C::BM + wave * 32 + col;
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const char*)p.dout + (b * p.do_sb + h * p.do_sh) * 2, do_bytes);
+  i32x4_t qreg[KS], doreg[KS];
+  {
+    const uint32_t qo = (uint32_t)((int64_t)query * p.q_sl * 2) + half * 16;
+    const uint32_t oo = (uint32_t)((int64_t)query * p.do_sl * 2) + half * 16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qreg[s] = buf_load16(rq, qo + s * 32);
+      doreg[s] = buf_load16(rdo, oo + s * 32);
+    }
+  }
+  float lse2 = __builtin_inff(), dlt = 0.f;
+  if (query < p.LQP) {
+    const float* st = p.stats + ((int64_t)bh * (p.LQP / p.stat_tile) + query / p.stat_tile) * 2 * p.stat_tile +
+                      query % p.stat_tile;
+    lse2 = st[0];
+    dlt = st[p.stat_tile];
+  }
+
+  // ---- key-side resources and per-lane DMA offsets
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes);
+  constexpr int RPW = C::RPW;
+  uint32_t roff_k[RPW], roff_v[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CR, phys = pch % CR;
+    const int logical = phys ^ trswz16(row & 15);
+    roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
+    roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
+  }
+  const uint32_t k_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
+  const uint32_t v_step = (uint32_t)((int64_t)BN * p.v_sl * 2);
+
+  auto stage = [&](auto kk) -> lds_char_t* {
+    constexpr int k = decltype(kk)::value & 3;
+    if constexpr (k == 0) return (lds_char_t*)stg0;
+    else if constexpr (k == 1) return (lds_char_t*)stg1;
+    else if constexpr (k == 2) return (lds_char_t*)stg2;
+    else return (lds_char_t*)stg3;
+  };
+  // request li (0 <= li < C::LOADS) of tile kt into stage st; tiles at or beyond
+  // the end read zeros or in-range rows into a stage nobody reads again
+  auto issue_load = [&](lds_char_t* st, int kt, int li) {
+    const int jj = li >> 1, i = wave + jj * C::NW;
+    if (li & 1) buf_load16_lds(rv, st + C::OFF_V + i * 1024, roff_v[jj], (uint32_t)kt * v_step);
+    else buf_load16_lds(rk, st + C::OFF_K + i * 1024, roff_k[jj], (uint32_t)kt * k_step);
+  };
+
+  // ---- LDS read offsets: row-wise (K, V row perm32(col), chunk 2s + half) and
+  // transposed (K^T block db, keys 16 t + 8 (g >> 1) + (0..3 | 4..7))
+  int sx[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int r = perm32(col);
+    sx[s] = r * ROWB + (((2 * s + half) ^ trswz16(r & 15)) << 4);
+  }
+  int tx[DB][2];
+  {
+    const int g = lane >> 4, r = (lane & 15) >> 2, c = lane & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int row = 8 * (g >> 1) + 4 * hh + r;  // plus 16 t
+        const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
+        tx[db][hh] = row * ROWB + ((chunk ^ trswz16(row & 15)) << 4) + 8 * (c & 1);
+      }
+    }
+  }
+  auto pin_offsets = [&]() {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(sx[s]));
+#pragma unroll
+    for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(tx[db][0]), "+v"(tx[db][1]));
+  };
+
+  f32x16_t acc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[d][v] = 0.f;
+  }
+
+  constexpr int PF = 4;
+  constexpr int NMA = 2 * KS;  // S^T, dP^T MFMAs
+  constexpr int NMB = 2 * DB;  // dQ^T MFMAs (two 16-key chunks)
+  constexpr int NS = NMA + NMB;
+  constexpr int NVAL = 16;     // P, dS values per lane per tile
+  static_assert(NVAL <= NMA, "values ride in the score slots");
+  const f32x16_t zero16 = {};
+  auto load_op = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int m) -> i32x4_t {
+    if (m < NMA) return *(lds_i32x4_t*)(s_next + ((m & 1) ? C::OFF_V : C::OFF_K) + sx[m >> 1]);
+    const int mm = m - NMA, t = mm / DB, db = mm % DB;
+    const lds_char_t* base = s_cur + C::OFF_K + t * 16 * ROWB;
+    const u32x2_t lo = lds_read_tr16(base + tx[db][0]);
+    const u32x2_t hi = lds_read_tr16(base + tx[db][1]);
+    return i32x4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+  };
+  // value v = 8 t + e of the C tile: key 16 t + 8 half + e of the tile
+  auto value = [&](int v, const f32x16_t& sc, const f32x16_t& dpc, float (&dsv)[2]) {
+    const float pe = fast_exp2(fmaf(sc[v], p.scale_log2, -lse2));
+    dsv[v & 1] = pe * (dpc[v] - dlt);
+  };
+  auto mfma_slot = [&](int m, i32x4_t op, f32x16_t& sn, f32x16_t& dpn, const i32x4_t (&dsb)[2]) {
+    if (m < NMA) {
+      const int s = m >> 1;
+      if (m & 1) dpn = mfma32(op, doreg[s], s == 0 ? zero16 : dpn, T());
+      else sn = mfma32(op, qreg[s], s == 0 ? zero16 : sn, T());
+    } else {
+      const int mm = m - NMA, t = mm / DB, db = mm % DB;
+      acc[db] = mfma32(op, dsb[t], acc[db], T());
+    }
+  };
+
+  // step j (j + 1 < ntiles, j % 4 == kk)
+  auto step = [&](auto kk, int j, const f32x16_t& sc, const f32x16_t& dpc, f32x16_t& sn, f32x16_t& dpn) {
+    constexpr int k = decltype(kk)::value;
+    ring_sync<C::LOADS>();  // tile j + 1 has landed (tile j + 2 may be in flight)
+    pin_offsets();
+    const lds_char_t* s_next = stage(IC<k + 1>{});
+    const lds_char_t* s_cur = stage(IC<k>{});
+    lds_char_t* s_req = stage(IC<k + 3>{});
+    i32x4_t opr[PF];
+#pragma unroll
+    for (int m = 0; m < PF; ++m) opr[m] = load_op(s_next, s_cur, m);
+    i32x4_t dsb[2];
+    float dsv[2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < NS; ++m) {
+      mfma_slot(m, opr[m % PF], sn, dpn, dsb);
+      if (m + PF < NS) opr[m % PF] = load_op(s_next, s_cur, m + PF);
+      if (m < NVAL) {
+        value(m, sc, dpc, dsv);
+        if (m & 1) dsb[m >> 3][(m & 7) >> 1] = (int)Elem<T>::pack2(dsv[0], dsv[1]);
+      }
+#pragma unroll
+      for (int li = 0; li < C::LOADS; ++li) {
+        if (li * NS / C::LOADS == m) issue_load(s_req, j + 3, li);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto last_step = [&](auto kk, const f32x16_t& sc, const f32x16_t& dpc) {
+    const lds_char_t* s_cur = stage(kk);
+    i32x4_t dsb[2];
+    float dsv[2];
+#pragma unroll
+    for (int v = 0; v < NVAL; ++v) {
+      value(v, sc, dpc, dsv);
+      if (v & 1) dsb[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(dsv[0], dsv[1]);
+    }
+    f32x16_t un_s, un_p;
+#pragma unroll
+    for (int m = NMA; m < NS; ++m) mfma_slot(m, load_op(s_cur, s_cur, m), un_s, un_p, dsb);
+  };
+
+  if (ntiles > 0) {
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+    ring_sync<2 * C::LOADS>();  // Q, dO rows and tile 0
+    f32x16_t sa, pa, sb, pbb;
+    {
+      const lds_char_t* s0 = stage(IC<0>{});
+      i32x4_t dummy[2];
+#pragma unroll
+      for (int m = 0; m < NMA; ++m) mfma_slot(m, load_op(s0, s0, m), sa, pa, dummy);
+    }
+    int j = 0;
+    for (; j + 4 < ntiles; j += 4) {
+      step(IC<0>{}, j, sa, pa, sb, pbb);
+      step(IC<1>{}, j + 1, sb, pbb, sa, pa);
+      step(IC<2>{}, j + 2, sa, pa, sb, pbb);
+      step(IC<3>{}, j + 3, sb, pbb, sa, pa);
+    }
+    const int rest = ntiles - j;  // 1..4 tiles left
+    if (rest >= 2) step(IC<0>{}, j, sa, pa, sb, pbb);
+    if (rest >= 3) step(IC<1>{}, j + 1, sb, pbb, sa, pa);
+    if (rest >= 4) step(IC<2>{}, j + 2, sa, pa, sb, pbb);
+    if (rest == 1) last_step(IC<0>{}, sa, pa);
+    else if (rest == 2) last_step(IC<1>{}, sb, pbb);
+    else if (rest == 3) last_step(IC<2>{}, sa, pa);
+    else last_step(IC<3>{}, sb, pbb);
+    wait_vmem();  // no requests beyond the last tile stay in flight
+  }
+
+  // ---- dQ = s (dQ^T)^T: lane holds query col, rows d = 32 db + 8 jj + 4 half + (0..3)
+  if (query < p.Lq) {
+    char* dqp = (char*)p.dq + ((b * p.dq_sb + h * p.dq_sh) + (int64_t)query * p.dq_sl) * 2;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int dc = d * 32 + 8 * jj + 4 * half;
+        u32x2_t w = {Elem<T>::pack2(acc[d][4 * jj] * p.scale, acc[d][4 * jj + 1] * p.scale),
+                     Elem<T>::pack2(acc[d][4 * jj + 2] * p.scale, acc[d][4 * jj + 3] * p.scale)};
+        *(u32x2_t*)(dqp + dc * 2) = w;
+      }
+    }
+  }
+}
+
 }  // namespace dmad

@@ -31,7 +31,9 @@ static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
 
 template <typename T, int D, int MODE>
 static hipError_t dq_launch(const DqParams& p, int grid, hipStream_t s) {
-  if constexpr (MODE == kBwdDoutOnly && DqPipeCfg<D>::FITS)
+  if constexpr (MODE == kBwdDoutOnly && DqTrCfg<D>::FITS)
+    hipLaunchKernelGGL((attn_bwd_dq_tr_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
+  else if constexpr (MODE == kBwdDoutOnly && DqPipeCfg<D>::FITS)
     hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<T, D>), dim3(grid), dim3(512), 0, s, p);
   else
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);
