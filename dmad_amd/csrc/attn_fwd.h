@@ -178,7 +178,7 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
   for (int j = 0; j < C::VPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int d = pch / CV, phys = pch % CV;
-    const int logical = phys ^ swz<CV>(d & 15);
+    const int logical = phys ^ swz4r(d & 15);
     voff[j] = (uint32_t)(d * p.LKP * 2) + logical * 16;
   }
   const uint32_t k_tile_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
     krow_off[sb] = R * CK * 16;
     kswzv[sb] = kswz16<CK>(R);
   }
-  const int vrow_off = col * CV * 16 + ((grp ^ swz<CV>(col)) << 4);
+  const int vrow_off = col * CV * 16 + ((grp ^ swz4r(col)) << 4);
 
   f32x4_t oacc[DB], cacc[DB];
 #pragma unroll
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
   for (int j = 0; j < C::VPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int d = pch / CV, phys = pch % CV;
-    const int logical = phys ^ swz<CV>(d & 15);
+    const int logical = phys ^ swz4r(d & 15);
     voff[j] = (uint32_t)(d * p.LKP * 2) + logical * 16;
   }
   const uint32_t k_tile_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
       kx[2 * s + sb] = R * CK * 16 + (((4 * s + grp) ^ kswz16<CK>(R)) << 4);
     }
   }
-  int vx = col * CV * 16 + ((grp ^ swz<CV>(col)) << 4);
+  int vx = col * CV * 16 + ((grp ^ swz4r(col)) << 4);
   // Re-defines the offsets at each step (an empty asm), so that stage base +
   // offset is formed per step and folds into the LDS instructions' immediate
   // instead of being hoisted into one register per stage.

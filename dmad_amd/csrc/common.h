@@ -159,6 +159,13 @@ __device__ __forceinline__ int swz(int x) {
   else return (x >> 2) & (C - 1);
 }
 
+// XOR swizzle of the 16-byte chunk index for LDS tiles whose rows hold 4 chunks
+// (64 bytes), read 16 B per lane with lane <-> row x (x = 0..15) at one logical
+// chunk: the 16 lanes hit 16 distinct 16-byte slots of a 256-byte window and
+// each 8-lane half 8 distinct slots of a 128-byte window (ds_read_b128 serves 8
+// lanes per cycle; swz<4> meets only the first condition, a 2-way conflict).
+__device__ __forceinline__ int swz4r(int x) { return ((x >> 2) & 1) | ((x ^ (x >> 2)) & 2); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ds_read_b64_tr_b16 (gfx950 LDS transpose read), checked on the device with a
