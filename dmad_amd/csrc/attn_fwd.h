@@ -41,14 +41,17 @@ struct FwdParams {
   const void* k;
   const void* tq;
   const void* tk;
-  const void* vt;   // V^T  [B*H][DVP][LKP]
+  const void* vt;   // V^T  [B*H][DVP][LKP]  (kernels that read a transposed copy)
   const void* tvt;  // Vd^T [B*H][DVP][LKP]
+  const void* v;    // V, Vd rows (kernels that transpose on the LDS read)
+  const void* tv;
   void* o;
   void* to;
   float* lse;  // [B*H][Lq]
   float* mu;   // [B*H][Lq]
   int64_t q_sb, q_sh, q_sl;  // element strides, shared by Q and Qd
   int64_t k_sb, k_sh, k_sl;  // shared by K and Kd
+  int64_t v_sb, v_sh, v_sl;  // shared by V and Vd
   int64_t o_sb, o_sh, o_sl;  // shared by O and Od
   int B, H, Lq, Lk, LKP;
   float scale;       // softmax scale s

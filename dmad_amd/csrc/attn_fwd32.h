@@ -1,0 +1,429 @@
+// Forward(+JVP) kernel for 128-wide heads on 32x32x16 MFMAs.
+//
+// Same semantics as attn_fwd_kernel (the reference kernel `_attn_fwd`,
+// train/wan/rcm/utils/flash_attention_jvp_triton.py:107-232): log2-domain
+// online softmax, P~ and H~ rounded to the input type before the P V products,
+// fp32 accumulators, the :216-223 epilogue, LSE and mu per query row.
+//
+// Work decomposition: one workgroup = 4 waves (one per SIMD) = 128 query rows
+// of one head. Lane l of a wave owns query l%32; its Q (and Qd) row stays in
+// registers as the B operand of S^T = K Q^T (and Sd^T = K Qd^T + Kd Q^T), so a
+// 32x32 score tile gives each lane 16 keys of its own query and the row
+// statistics are per-lane scalars (the other 16 keys sit in lane l^32).
+// K, Kd, V, Vd stream as row-major 32-key tiles through a four-stage LDS ring
+// filled by buffer->LDS requests three steps ahead. K rows are read in perm32
+// order (A operand), so P~ and H~ leave the score tile already in the
+// B-operand layout of O^T += V^T P^T; V^T is read from the row-major V tile
+// with ds_read_b64_tr_b16, so V needs no transposed copy.
+//
+// Compared with 16-query waves, every K/V byte read from LDS feeds twice the
+// MFMA work, which halves the LDS traffic per flop (the 16-query kernel is
+// bound by LDS bandwidth at this head size).
+//
+// Step i (after one barrier) is a fixed stream of MFMAs:
+//   phase A  S^T, Sd^T of tile i+1 (K, Kd of stage i+1), with the online
+//            softmax of tile i on the VALU between them
+//   (rescale of O~, C~ when some row's running max moved)
+//   phase B  O~^T += V^T P~^T, C~^T += V^T H~^T + Vd^T P~^T of tile i, with
+//            the requests for tile i+3 spread between the MFMAs
+// Every MFMA's LDS operand is read four operands ahead.
+#pragma once
+#include "attn_fwd.h"
+
+namespace dmad {
+
+template <int MODE>
+struct Fwd32Cfg {
+  static constexpr int D = 128;
+  static constexpr int NW = 4;        // waves per workgroup
+  static constexpr int BM = 32 * NW;  // query rows per workgroup
+  static constexpr int BN = 32;       // keys per pipeline step
+  static constexpr int KS = D / 16;   // 16-wide k slices of Q K^T
+  static constexpr int DB = D / 32;   // 32-row blocks of O^T
+  static constexpr int CR = D / 8;    // 16-byte chunks per row
+  static constexpr int ROWB = D * 2;
+  static constexpr int TILE = BN * ROWB;
+  static constexpr bool JVP = MODE != kFwdPlain;
+  static constexpr bool KVT = MODE == kFwdJvp;
+  static constexpr int NTILE = KVT ? 4 : 2;  // row tiles per stage: K, V [, Kd, Vd]
+  static constexpr int OFF_K = 0, OFF_V = TILE, OFF_KT = 2 * TILE, OFF_VT = 3 * TILE;
+  static constexpr int STAGE = NTILE * TILE;
+  static constexpr int NSTAGE = 4;
+  static constexpr int RPW = BN * CR / 64 / NW;       // 1 KiB requests per tile per wave
+  static constexpr int LOADS = NTILE * RPW;           // requests per wave per step
+  static constexpr int NOPA = KS * (KVT ? 2 : 1);     // LDS operands of phase A
+  static constexpr int NOPB = 2 * DB * (KVT ? 2 : 1);  // LDS operands of phase B
+  static_assert(BN * CR % (64 * NW) == 0, "tile requests split evenly over the waves");
+  static_assert(NSTAGE * STAGE <= 160 * 1024, "ring exceeds the LDS");
+};
+
+// Head shapes served by attn_fwd32_kernel (the others use attn_fwd_kernel and
+// its variants, which read a transposed copy of V).
+constexpr bool fwd32_supported(int dqk, int dv) { return dqk == 128 && dv == 128; }
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
+  using C = Fwd32Cfg<MODE>;
+  constexpr int D = C::D, BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
+  constexpr int NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
+  constexpr float kSlack = RescaleSlack<T>::value;
+  static_assert(CR == 16, "trswz16 assumes 16 chunks per row");
+  __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int ntiles = (p.Lk + BN - 1) / BN;
+
+  // ---- this lane's query: Q (and Qd) row slices, B operands of the score MFMAs
+  const int query = qt * C::BM + wave * 32 + col;
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
+  const int64_t qhead = b * p.q_sb + h * p.q_sh;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const char*)p.q + qhead * 2, q_bytes);
+  i32x4_t qreg[KS], tqreg[KS];
+  {
+    const uint32_t qo = (uint32_t)((int64_t)query * p.q_sl * 2) + half * 16;
+    __amdgpu_buffer_rsrc_t rtq = rq;
+    if constexpr (C::JVP) rtq = make_rsrc((const char*)p.tq + qhead * 2, q_bytes);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qreg[s] = buf_load16(rq, qo + s * 32);
+      if constexpr (C::JVP) tqreg[s] = buf_load16(rtq, qo + s * 32);
+    }
+  }
+  // Q and Qd live in AGPRs for the whole kernel (MFMA operands read them there):
+  // the VGPRs hold the accumulators, the score tiles and the softmax. This
+  // unit is compiled with MFMAs in VGPR form (-amdgpu-mfma-vgpr-form).
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    asm volatile("" : "+a"(qreg[s]));
+    if constexpr (C::JVP) asm volatile("" : "+a"(tqreg[s]));
+  }
+
+  // ---- key-side resources and per-lane request offsets (tile independent)
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
+  const int64_t khead = b * p.k_sb + h * p.k_sh, vhead = b * p.v_sb + h * p.v_sh;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + khead * 2, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + vhead * 2, v_bytes);
+  __amdgpu_buffer_rsrc_t rtk = rk, rtv = rv;
+  if constexpr (C::KVT) {
+    rtk = make_rsrc((const char*)p.tk + khead * 2, k_bytes);
+    rtv = make_rsrc((const char*)p.tv + vhead * 2, v_bytes);
+  }
+  constexpr int RPW = C::RPW;
+  uint32_t roff_k[RPW], roff_v[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int pch = (wave + j * C::NW) * 64 + lane;
+    const int row = pch / CR, phys = pch % CR;
+    const int logical = phys ^ trswz16(row & 15);
+    roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
+    roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
+  }
+  const uint32_t k_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
+  const uint32_t v_step = (uint32_t)((int64_t)BN * p.v_sl * 2);
+
+  auto stage = [&](auto kk) -> lds_char_t* {
+    constexpr int k = decltype(kk)::value & 3;
+    if constexpr (k == 0) return (lds_char_t*)stg0;
+    else if constexpr (k == 1) return (lds_char_t*)stg1;
+    else if constexpr (k == 2) return (lds_char_t*)stg2;
+    else return (lds_char_t*)stg3;
+  };
+  // request li (0 <= li < LOADS) of tile kt into stage st; tiles at or beyond
+  // the end read zeros or in-range rows into a stage nobody reads again
+  auto issue_load = [&](lds_char_t* st, int kt, int li) {
+    const int t = li % C::NTILE, jj = li / C::NTILE, i = wave + jj * C::NW;
+    const uint32_t ks = (uint32_t)kt * k_step, vs = (uint32_t)kt * v_step;
+    if (t == 0) buf_load16_lds(rk, st + C::OFF_K + i * 1024, roff_k[jj], ks);
+    else if (t == 1) buf_load16_lds(rv, st + C::OFF_V + i * 1024, roff_v[jj], vs);
+    else if (t == 2) buf_load16_lds(rtk, st + C::OFF_KT + i * 1024, roff_k[jj], ks);
+    else buf_load16_lds(rtv, st + C::OFF_VT + i * 1024, roff_v[jj], vs);
+  };
+
+  // ---- LDS read offsets: K rows (row perm32(col), chunk 2s + half) and V^T
+  // through lds_read_tr16 (block db, keys 16 t + 8 (g >> 1) + (0..3 | 4..7))
+  int sx[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int r = perm32(col);
+    sx[s] = r * ROWB + (((2 * s + half) ^ trswz16(r & 15)) << 4);
+  }
+  int tx[DB][2];
+  {
+    const int g = lane >> 4, r = (lane & 15) >> 2, c = lane & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int row = 8 * (g >> 1) + 4 * hh + r;  // plus 16 t
+        const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
+        tx[db][hh] = row * ROWB + ((chunk ^ trswz16(row & 15)) << 4) + 8 * (c & 1);
+      }
+    }
+  }
+  // Re-defines the offsets at each step (an empty asm), so that stage base +
+  // offset folds into the LDS instructions' immediate per step.
+  auto pin_offsets = [&]() {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(sx[s]));
+#pragma unroll
+    for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(tx[db][0]), "+v"(tx[db][1]));
+  };
+
+  // Phase A operand o: K slice (KVT: even o) or Kd slice (odd o) s.
+  // Phase B operand o - NOPA = j: key chunk t = j / (NOPB / 2); within a chunk
+  // the order is V^T blocks (0, 1), Vd^T blocks (0, 1), V^T (2, 3), Vd^T (2, 3)
+  // so the two C~ updates of one block are two operands apart.
+  struct OpB {
+    int t, db;
+    bool vd;
+  };
+  auto op_b = [&](int j) -> OpB {
+    constexpr int PER_T = NOPB / 2;
+    const int t = j / PER_T, jj = j % PER_T;
+    if constexpr (C::KVT) {
+      const int pair = jj / 4, w = jj % 4;
+      return OpB{t, 2 * pair + (w & 1), w >= 2};
+    } else {
+      return OpB{t, jj, false};
+    }
+  };
+  auto load_op = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int o) -> i32x4_t {
+    if (o < NOPA) {
+      const int s = C::KVT ? o >> 1 : o;
+      const int off = (C::KVT && (o & 1)) ? C::OFF_KT : C::OFF_K;
+      return *(lds_i32x4_t*)(s_next + off + sx[s]);
+    }
+    const OpB ob = op_b(o - NOPA);
+    const lds_char_t* base = s_cur + (ob.vd ? C::OFF_VT : C::OFF_V) + ob.t * 16 * ROWB;
+    const u32x2_t lo = lds_read_tr16(base + tx[ob.db][0]);
+    const u32x2_t hi = lds_read_tr16(base + tx[ob.db][1]);
+    return i32x4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+  };
+
+  f32x16_t oacc[DB], cacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      oacc[d][v] = 0.f;
+      cacc[d][v] = 0.f;
+    }
+  }
+  const f32x16_t zero16 = {};
+  // the MFMAs of operand o (pk, hk: P~, H~ of the current tile, two 16-key chunks)
+  auto mfma_op = [&](int o, i32x4_t a, f32x16_t& sn, f32x16_t& tn, const i32x4_t (&pk)[2],
+                     const i32x4_t (&hk)[2]) {
+    if (o < NOPA) {
+      const int s = C::KVT ? o >> 1 : o;
+      if (C::KVT && (o & 1)) {
+        tn = mfma32(a, qreg[s], tn, T());
+      } else {
+        sn = mfma32(a, qreg[s], s == 0 ? zero16 : sn, T());
+        if constexpr (C::JVP) tn = mfma32(a, tqreg[s], s == 0 ? zero16 : tn, T());
+      }
+    } else {
+      const OpB ob = op_b(o - NOPA);
+      if (ob.vd) {
+        cacc[ob.db] = mfma32(a, pk[ob.t], cacc[ob.db], T());
+      } else {
+        oacc[ob.db] = mfma32(a, pk[ob.t], oacc[ob.db], T());
+        if constexpr (C::JVP) cacc[ob.db] = mfma32(a, hk[ob.t], cacc[ob.db], T());
+      }
+    }
+  };
+
+  // Online softmax of one tile in NMICRO micro-steps (log2 domain; lanes l and
+  // l^32 share a query and its running max). Value v of the score tile is key
+  // 16 (v >> 3) + 8 half + (v & 7); P~, H~ are packed as the B operands of the
+  // two 16-key chunks.
+  constexpr int NMICRO = 18;
+  float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
+  struct Soft {
+    float mx, alpha, neg_m, ls, rs, pv;
+    float hv;
+    bool moved;
+  };
+  auto soft_micro = [&](int u, Soft& sm, const f32x16_t& sc, const f32x16_t& tc, i32x4_t (&pk)[2],
+                        i32x4_t (&hk)[2]) {
+    if (u == 0) {
+      float a = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      float b2 = fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]));
+      float c2 = fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11]));
+      float d2 = fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]));
+      sm.mx = fmaxf(fmaxf(a, b2), fmaxf(c2, d2));
+      sm.ls = 0.f;
+      sm.rs = 0.f;
+    } else if (u == 1) {
+      sm.mx = fmaxf(sm.mx, other_half(sm.mx)) * p.scale_log2;
+      sm.moved = __builtin_amdgcn_ballot_w64(sm.mx > m_i + kSlack) != 0;
+      const float m_new = sm.moved ? fmaxf(m_i, sm.mx) : m_i;
+      sm.alpha = fast_exp2(m_i - m_new);
+      m_i = m_new;
+      sm.neg_m = -m_new;
+    } else {
+      const int v = u - 2;
+      const float pe = fast_exp2(fmaf(sc[v], p.scale_log2, sm.neg_m));
+      sm.ls += pe;
+      float he = 0.f;
+      if constexpr (C::JVP) {
+        he = pe * (tc[v] * p.scale);
+        sm.rs += he;
+      }
+      if (v & 1) {
+        pk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(sm.pv, pe);
+        if constexpr (C::JVP) hk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(sm.hv, he);
+      } else {
+        sm.pv = pe;
+        sm.hv = he;
+      }
+    }
+  };
+  auto rescale = [&](float alpha) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        oacc[d][v] *= alpha;
+        if constexpr (C::JVP) cacc[d][v] *= alpha;
+      }
+    }
+  };
+
+  // step i (i + 1 < ntiles, i % 4 == kk): phase A on tile i+1's K, softmax of
+  // tile i (sc, tc); phase B on tile i's V; requests tile i+3
+  auto step = [&](auto kk, int i, const f32x16_t& sc, const f32x16_t& tc, f32x16_t& sn, f32x16_t& tn) {
+    constexpr int k = decltype(kk)::value;
+    ring_sync<C::LOADS>();  // tile i+1 has landed (tile i+2 may be in flight)
+    pin_offsets();
+    const lds_char_t* s_next = stage(IC<k + 1>{});
+    const lds_char_t* s_cur = stage(IC<k>{});
+    lds_char_t* s_req = stage(IC<k + 3>{});
+    i32x4_t opr[PF];
+#pragma unroll
+    for (int o = 0; o < PF; ++o) opr[o] = load_op(s_next, s_cur, o);
+    Soft sm;
+    i32x4_t pk[2], hk[2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int o = 0; o < NOPA; ++o) {
+      mfma_op(o, opr[o % PF], sn, tn, pk, hk);
+      if (o + PF < NOP) opr[o % PF] = load_op(s_next, s_cur, o + PF);
+#pragma unroll
+      for (int u = o * NMICRO / NOPA; u < (o + 1) * NMICRO / NOPA; ++u) soft_micro(u, sm, sc, tc, pk, hk);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l_i = l_i * sm.alpha + sm.ls;
+    if constexpr (C::JVP) r_i = r_i * sm.alpha + sm.rs;
+    // keep the softmax in phase A: the values are used here, before the branch
+    asm volatile("" : "+v"(pk[0]), "+v"(pk[1]), "+v"(l_i));
+    if constexpr (C::JVP) asm volatile("" : "+v"(hk[0]), "+v"(hk[1]), "+v"(r_i));
+    if (sm.moved) rescale(sm.alpha);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int o = NOPA; o < NOP; ++o) {
+      mfma_op(o, opr[o % PF], sn, tn, pk, hk);
+      if (o + PF < NOP) opr[o % PF] = load_op(s_next, s_cur, o + PF);
+#pragma unroll
+      for (int li = 0; li < C::LOADS; ++li) {
+        if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, i + 3, li);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // last tile (may hold keys >= Lk): masked softmax, rescale, PV
+  auto last_step = [&](auto kk, int i, f32x16_t& sc, const f32x16_t& tc) {
+    const lds_char_t* s_cur = stage(kk);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      if (i * BN + 16 * (v >> 3) + 8 * half + (v & 7) >= p.Lk) sc[v] = -__builtin_inff();
+    }
+    Soft sm;
+    i32x4_t pk[2], hk[2];
+#pragma unroll
+    for (int u = 0; u < NMICRO; ++u) soft_micro(u, sm, sc, tc, pk, hk);
+    l_i = l_i * sm.alpha + sm.ls;
+    if constexpr (C::JVP) r_i = r_i * sm.alpha + sm.rs;
+    rescale(sm.alpha);
+    f32x16_t un_s, un_t;
+#pragma unroll
+    for (int o = NOPA; o < NOP; ++o) mfma_op(o, load_op(s_cur, s_cur, o), un_s, un_t, pk, hk);
+  };
+
+  // ---- prologue: tiles 0..2 requested, scores of tile 0
+#pragma unroll
+  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+#pragma unroll
+  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+#pragma unroll
+  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+  ring_sync<2 * C::LOADS>();  // Q slices and tile 0
+  f32x16_t sa, ta, sb, tb;
+  {
+    const lds_char_t* s0 = stage(IC<0>{});
+    const i32x4_t none[2] = {};
+#pragma unroll
+    for (int o = 0; o < NOPA; ++o) mfma_op(o, load_op(s0, s0, o), sa, ta, none, none);
+  }
+  int i = 0;
+  for (; i + 4 < ntiles; i += 4) {
+    step(IC<0>{}, i, sa, ta, sb, tb);
+    step(IC<1>{}, i + 1, sb, tb, sa, ta);
+    step(IC<2>{}, i + 2, sa, ta, sb, tb);
+    step(IC<3>{}, i + 3, sb, tb, sa, ta);
+  }
+  const int rest = ntiles - i;  // 1..4 tiles left
+  if (rest >= 2) step(IC<0>{}, i, sa, ta, sb, tb);
+  if (rest >= 3) step(IC<1>{}, i + 1, sb, tb, sa, ta);
+  if (rest >= 4) step(IC<2>{}, i + 2, sa, ta, sb, tb);
+  if (rest == 1) last_step(IC<0>{}, i, sa, ta);
+  else if (rest == 2) last_step(IC<1>{}, i + 1, sb, tb);
+  else if (rest == 3) last_step(IC<2>{}, i + 2, sa, ta);
+  else last_step(IC<3>{}, i + 3, sb, tb);
+  wait_vmem();  // no requests beyond the last tile stay in flight
+
+  // ---- epilogue: lane (query col, half) holds d = 32 db + 8 jj + 4 half + (0..3)
+  const float l = l_i + other_half(l_i);
+  const float inv_l = 1.0f / l;
+  float mu = 0.f;
+  if constexpr (C::JVP) mu = (r_i + other_half(r_i)) * inv_l;
+  const int64_t obase = b * p.o_sb + h * p.o_sh;
+  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + D) * 2);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
+  __amdgpu_buffer_rsrc_t rto = ro;
+  if constexpr (C::JVP) rto = make_rsrc((char*)p.to + obase * 2, o_bytes);
+  const uint32_t orow = (uint32_t)((int64_t)query * p.o_sl * 2);  // rows >= Lq fall outside the resource
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int dc = d * 32 + 8 * jj + 4 * half;
+      float ov[4], tv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ov[e] = oacc[d][4 * jj + e] * inv_l;
+        if constexpr (C::JVP) tv[e] = cacc[d][4 * jj + e] * inv_l - mu * ov[e];
+      }
+      const uint32_t off = orow + dc * 2;
+      buf_store8(ro, u32x2_t{Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])}, off);
+      if constexpr (C::JVP) buf_store8(rto, u32x2_t{Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])}, off);
+    }
+  }
+  if (half == 0 && query < p.Lq) {
+    const int64_t si = (int64_t)bh * p.Lq + query;
+    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    if constexpr (C::JVP) p.mu[si] = mu;
+  }
+}
+
+}  // namespace dmad

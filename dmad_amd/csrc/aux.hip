@@ -55,26 +55,43 @@ __device__ __forceinline__ float dot8(const uint16_t* a, const uint16_t* b) {
   return s;
 }
 
-template <typename T>
+// D/8 consecutive lanes share one query row, each lane reading 16 bytes of O,
+// dO (and Od, dOd): every load instruction reads whole rows, and the per-row
+// dot products finish with a butterfly over those lanes.
+template <typename T, int D>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepParams p) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)p.BH * p.LQP) return;
-  const int bh = (int)(gid / p.LQP), q = (int)(gid - (int64_t)bh * p.LQP);
+  constexpr int LPR = D / 8;        // lanes per row
+  constexpr int RPB = 256 / LPR;    // rows per workgroup
+  const int sub = threadIdx.x % LPR;
+  const int64_t gid = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const bool live = gid < (int64_t)p.BH * p.LQP;
+  const int bh = live ? (int)(gid / p.LQP) : 0, q = live ? (int)(gid - (int64_t)bh * p.LQP) : p.Lq;
   const int b = bh / p.H, h = bh - b * p.H;
-  float lse2 = __builtin_inff(), d_o = 0.f, d_to = 0.f, rho = 0.f, mu = 0.f;
+  const bool full = p.dto != nullptr;
+  float d_o = 0.f, d_to = 0.f, rho = 0.f;
   if (q < p.Lq) {
-    const uint16_t* o = (const uint16_t*)p.o + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_sl;
-    const uint16_t* dd = (const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh + (int64_t)q * p.do_sl;
-    const bool full = p.dto != nullptr;
-    const uint16_t* to = full ? (const uint16_t*)p.to + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_sl : nullptr;
-    const uint16_t* dt = full ? (const uint16_t*)p.dto + b * p.do_sb + h * p.do_sh + (int64_t)q * p.do_sl : nullptr;
-    for (int d = 0; d < p.D; d += 8) {
-      d_o += dot8<T>(dd + d, o + d);
-      if (full) {
-        d_to += dot8<T>(dt + d, to + d);
-        rho += dot8<T>(dt + d, o + d);
-      }
+    const int d = 8 * sub;
+    const uint16_t* o = (const uint16_t*)p.o + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_sl + d;
+    const uint16_t* dd = (const uint16_t*)p.dout + b * p.do_sb + h * p.do_sh + (int64_t)q * p.do_sl + d;
+    d_o = dot8<T>(dd, o);
+    if (full) {
+      const uint16_t* to = (const uint16_t*)p.to + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_sl + d;
+      const uint16_t* dt = (const uint16_t*)p.dto + b * p.do_sb + h * p.do_sh + (int64_t)q * p.do_sl + d;
+      d_to = dot8<T>(dt, to);
+      rho = dot8<T>(dt, o);
     }
+  }
+#pragma unroll
+  for (int m = 1; m < LPR; m <<= 1) {
+    d_o += __shfl_xor(d_o, m);
+    if (full) {
+      d_to += __shfl_xor(d_to, m);
+      rho += __shfl_xor(rho, m);
+    }
+  }
+  if (!live || sub != 0) return;
+  float lse2 = __builtin_inff(), mu = 0.f;
+  if (q < p.Lq) {
     lse2 = p.lse[(int64_t)bh * p.Lq + q] * 1.4426950408889634f;
     if (full) mu = p.mu[(int64_t)bh * p.Lq + q];
   }
@@ -97,14 +114,27 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepParams p) {
   }
 }
 
-static int64_t blocks_for(int64_t n) { return (n + 255) / 256; }
+template <typename T>
+static hipError_t launch_prep_t(const PrepParams& p, hipStream_t s) {
+  const int64_t rows = (int64_t)p.BH * p.LQP;
+  auto go = [&](auto kern, int lpr) {
+    const int64_t nb = (rows * lpr + 255) / 256;
+    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(256), 0, s, p);
+  };
+  switch (p.D) {
+    case 16: go(bwd_prep_kernel<T, 16>, 2); break;
+    case 32: go(bwd_prep_kernel<T, 32>, 4); break;
+    case 64: go(bwd_prep_kernel<T, 64>, 8); break;
+    case 128: go(bwd_prep_kernel<T, 128>, 16); break;
+    case 256: go(bwd_prep_kernel<T, 256>, 32); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s) {
-  const int64_t nb = blocks_for((int64_t)p.BH * p.LQP);
-  if (nb == 0) return hipSuccess;
-  if (dtype == 0) hipLaunchKernelGGL(bwd_prep_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(bwd_prep_kernel<_Float16>, dim3((unsigned)nb), dim3(256), 0, s, p);
-  return hipGetLastError();
+  if ((int64_t)p.BH * p.LQP == 0) return hipSuccess;
+  return dtype == 0 ? launch_prep_t<__bf16>(p, s) : launch_prep_t<_Float16>(p, s);
 }
 
 }  // namespace dmad

@@ -263,10 +263,14 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
   const int BH = (int)(B * H);
   char* ws = (char*)workspace;
   const int64_t vt_bytes = round_up(B * H * dvp * lkp * 2, 256);
+  // kernels for 128-wide heads transpose V on the LDS read; the others read a
+  // transposed, key-padded copy made here
+  const bool need_vt = !dmad::fwd32_supported((int)Dqk, (int)Dv);
+  hipError_t e = hipSuccess;
   dmad::TransposeParams tp{v, ws, v_strides[0], v_strides[1], v_strides[2], (int)H, (int)Lk, (int)Dv, (int)lkp, (int)dvp};
-  hipError_t e = dmad::launch_transpose_pad(tp, BH, s);
+  if (need_vt) e = dmad::launch_transpose_pad(tp, BH, s);
   if (e != hipSuccess) return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
-  if (kvt) {
+  if (kvt && need_vt) {
     dmad::TransposeParams tt = tp;
     tt.x = tv;
     tt.y = ws + vt_bytes;
@@ -281,6 +285,11 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
   p.tk = kvt ? tk : k;
   p.vt = ws;
   p.tvt = kvt ? (const void*)(ws + vt_bytes) : (const void*)ws;
+  p.v = v;
+  p.tv = kvt ? tv : v;
+  p.v_sb = v_strides[0];
+  p.v_sh = v_strides[1];
+  p.v_sl = v_strides[2];
   p.o = o;
   p.to = jvp ? to : o;
   p.lse = lse;
@@ -402,8 +411,11 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
     dmad::TransposeParams tp{x, y, st[0], st[1], st[2], (int)H, (int)L, (int)D, (int)LP, (int)dp};
     return dmad::launch_transpose_pad(tp, (int)BH, s);
   };
-  if ((e = tr(q, q_strides, trq, Lq, lqp)) != hipSuccess || (e = tr(dout, do_strides, trdo, Lq, lqp)) != hipSuccess ||
-      (e = tr(k, k_strides, trk, Lk, lkp)) != hipSuccess)
+  // the full-derivative kernels, and the dO-only ones for some head dims, read
+  // transposed copies of Q, dO (and Qd, dOd) and K (and Kd)
+  const bool need_tr = full || !dmad::dout_only_reads_rows((int)D);
+  if (need_tr && ((e = tr(q, q_strides, trq, Lq, lqp)) != hipSuccess ||
+                  (e = tr(dout, do_strides, trdo, Lq, lqp)) != hipSuccess || (e = tr(k, k_strides, trk, Lk, lkp)) != hipSuccess))
     return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
   if (full && ((e = tr(tq, q_strides, trtq, Lq, lqp)) != hipSuccess || (e = tr(dto, do_strides, trdto, Lq, lqp)) != hipSuccess ||
                (e = tr(tk, k_strides, trtk, Lk, lkp)) != hipSuccess))

@@ -4,6 +4,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include "attn_fwd.h"
+#include "attn_fwd32.h"
 #include "attn_bwd.h"
 #include "attn_bwd_dq.h"
 
@@ -14,6 +15,12 @@ typedef hipError_t (*FwdLaunchFn)(const FwdParams&, int grid, hipStream_t);
 // Launcher for attn_fwd_kernel<T, DQK, DV, MODE>, or nullptr if (DV, MODE) is unsupported.
 template <typename T, int DQK>
 FwdLaunchFn fwd_select(int dv, int mode);
+
+// Launcher for attn_fwd32_kernel<T, MODE> (128-wide heads; fwd32_inst.hip).
+template <typename T>
+FwdLaunchFn fwd32_select(int mode);
+template <> FwdLaunchFn fwd32_select<__bf16>(int);
+template <> FwdLaunchFn fwd32_select<_Float16>(int);
 
 typedef hipError_t (*BwdLaunchFn)(const BwdParams&, int grid, hipStream_t);
 
@@ -37,6 +44,18 @@ inline int bwd_bmq(int d, int mode) {
     case 64: return dout_only_kv_bmq<64>();
     case 128: return dout_only_kv_bmq<128>();
     default: return dout_only_kv_bmq<256>();
+  }
+}
+
+// True when the dO-only backward kernels for head dim d read Q, dO and K
+// row-major (transposing on the LDS read), so they need no transposed copies.
+inline bool dout_only_reads_rows(int d) {
+  switch (d) {
+    case 16: return KvTrCfg<16, kKvTrBmq>::FITS && DqTrCfg<16>::FITS;
+    case 32: return KvTrCfg<32, kKvTrBmq>::FITS && DqTrCfg<32>::FITS;
+    case 64: return KvTrCfg<64, kKvTrBmq>::FITS && DqTrCfg<64>::FITS;
+    case 128: return KvTrCfg<128, kKvTrBmq>::FITS && DqTrCfg<128>::FITS;
+    default: return KvTrCfg<256, kKvTrBmq>::FITS && DqTrCfg<256>::FITS;
   }
 }
 
