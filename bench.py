@@ -165,8 +165,8 @@ def main():
     # algorithmic flops of each main kernel (GEMM flops it must do, counting the
     # S and dP recomputation of the dQ pass)
     k_flops = {"fwd": f_fwd, "bwd_dkdv": 8.0 * H * L * L * D, "bwd_dq": 6.0 * H * L * L * D}
-    k_names = {"fwd": "attn_fwd_kernel<bf16,128,128,jvp>", "bwd_dkdv": "attn_bwd_kernel<bf16,128,dout_only>",
-               "bwd_dq": "attn_bwd_dq_kernel<bf16,128,dout_only>"}
+    k_names = {"fwd": "attn_fwd32_kernel<bf16,jvp>", "bwd_dkdv": "attn_bwd_kv_tr_kernel<bf16,128>",
+               "bwd_dq": "attn_bwd_dq_tr_kernel<bf16,128>"}
     dom = max(k_ms, key=k_ms.get)
     dom_flops, dom_name = k_flops[dom], k_names[dom]
     achieved = dom_flops / (k_ms[dom] * 1e-3) / 1e12

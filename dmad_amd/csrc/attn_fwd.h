@@ -13,15 +13,21 @@
 // epilogue (:216-223); they receive identical rescales, so one accumulator
 // C~ = A~ + B~ holds the same sum.
 //
-// Work decomposition (one workgroup = 4 waves = 128 query rows of one head):
-//   * wave w owns query rows [32w, 32w+32); its Q and Qd slices stay in
-//     registers as the B operand of S^T = K Q^T (lane l <-> query l%32);
+// Kernels in this file (128-wide Q/K and V heads use attn_fwd32_kernel in
+// attn_fwd32.h instead):
+//   attn_fwd_kernel / attn_fwd_stream_kernel: one workgroup = 8 waves (2 per
+//     SIMD) = 128 query rows of one head; wave w owns 16 query rows, whose Q
+//     and Qd slices stay in registers as the B operand of S^T = K Q^T on
+//     16x16x32 MFMAs (lane l <-> query l%16);
+//   attn_fwd_simple_kernel: 4 waves x 32 queries on 32x32x16 MFMAs, one
+//     tile per step, for head dims whose four-stage ring does not fit in LDS.
+// In all of them:
 //   * K, Kd tiles [BN keys][D] and V^T, Vd^T tiles [D][BN keys] are streamed
-//     through a double-buffered LDS ring by buffer->LDS DMA (16 B per lane);
-//   * the C layout of S^T (lane <-> query, 16 key values per lane) feeds the
-//     B operand of O^T = V^T P^T directly, because the K rows of every 32-key
-//     block are read in perm32 order (rows 8..15 of a lane's values then map
-//     to 8 consecutive keys);
+//     through an LDS ring by buffer->LDS DMA (16 B per lane);
+//   * the C layout of S^T (lane <-> query, key values per lane) feeds the
+//     B operand of O^T = V^T P^T directly, because the K rows of every key
+//     block are read in a permuted order that makes a lane's values cover
+//     consecutive keys;
 //   * O~^T and C~^T accumulate in registers with lane <-> query, so the
 //     per-row rescale is a per-lane scalar multiply.
 // V and Vd are read from a pre-transposed copy ([BH][DVP][LKP], zero padded),
