@@ -1,0 +1,31 @@
+// Instantiates the dO-only dQ pass for 128-wide heads (attn_bwd_dq_tr_kernel)
+// for one element type (-DDMAD_T=<0 bf16 | 1 f16>). This unit is compiled with
+// MFMAs in VGPR form: the kernel then fits 256 VGPRs with no AGPRs, the score
+// tiles need no AGPR->VGPR copies before the softmax, and two workgroups share
+// a CU (64 KiB of LDS each).
+#include "launch.h"
+
+#ifndef DMAD_T
+#error "DMAD_T must be defined"
+#endif
+
+namespace dmad {
+
+#if DMAD_T == 0
+using Elt = __bf16;
+#else
+using Elt = _Float16;
+#endif
+
+template <typename T>
+static hipError_t dq_tr_launch(const DqParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_dq_tr_kernel<T, 128>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <>
+DqLaunchFn dq_tr_select<Elt>() {
+  return &dq_tr_launch<Elt>;
+}
+
+}  // namespace dmad

@@ -31,9 +31,7 @@ static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
 
 template <typename T, int D, int MODE>
 static hipError_t dq_launch(const DqParams& p, int grid, hipStream_t s) {
-  if constexpr (MODE == kBwdDoutOnly && DqTrCfg<D>::FITS)
-    hipLaunchKernelGGL((attn_bwd_dq_tr_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
-  else if constexpr (MODE == kBwdDoutOnly && DqPipeCfg<D>::FITS)
+  if constexpr (MODE == kBwdDoutOnly && DqPipeCfg<D>::FITS)
     hipLaunchKernelGGL((attn_bwd_dq_pipe_kernel<T, D>), dim3(grid), dim3(512), 0, s, p);
   else
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);
@@ -42,6 +40,9 @@ static hipError_t dq_launch(const DqParams& p, int grid, hipStream_t s) {
 
 template <>
 DqLaunchFn dq_select<Elt, DMAD_D>(int mode) {
+  if constexpr (DqTrCfg<DMAD_D>::FITS) {
+    if (mode == kBwdDoutOnly) return dq_tr_select<Elt>();
+  }
   if (mode == kBwdDoutOnly) return &dq_launch<Elt, DMAD_D, kBwdDoutOnly>;
 #if DMAD_D <= 128
   if (mode == kBwdFull) return &dq_launch<Elt, DMAD_D, kBwdFull>;

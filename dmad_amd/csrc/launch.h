@@ -34,6 +34,12 @@ typedef hipError_t (*DqLaunchFn)(const DqParams&, int grid, hipStream_t);
 template <typename T, int D>
 DqLaunchFn dq_select(int mode);
 
+// Launcher for the dO-only attn_bwd_dq_tr_kernel<T, 128> (bwd_dq_inst.hip).
+template <typename T>
+DqLaunchFn dq_tr_select();
+template <> DqLaunchFn dq_tr_select<__bf16>();
+template <> DqLaunchFn dq_tr_select<_Float16>();
+
 // Query tile of the dK/dV kernel, which fixes the layout of the backward
 // statistics (the full-derivative kernel always uses 32-query tiles).
 inline int bwd_bmq(int d, int mode) {
