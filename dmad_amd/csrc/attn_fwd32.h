@@ -28,8 +28,6 @@
 //            the requests for tile i+3 spread between the MFMAs
 // Every MFMA's LDS operand is read four operands ahead.
 #pragma once
-#include <type_traits>
-
 #include "attn_fwd.h"
 
 namespace dmad {
@@ -245,67 +243,50 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
     }
   };
 
-  // Online softmax, split so that its VALU work spreads over both phases:
-  //   phase B of step i-1 (scores of tile i just computed): the row max of
-  //     tile i, the running max m and the rescale factor alpha of tile i;
-  //   phase A of step i: P~ = exp2(s log2(e) S - m), H~ = P~ * Sd, rounded and
-  //     packed as the B operands of the two 16-key chunks (value v of the score
-  //     tile is key 16 (v >> 3) + 8 half + (v & 7));
-  //   phase B of step i: the row sums of the rounded P~ and H~ (v_dot2 with
-  //     ones), so l and r sum exactly the weights the P V products use.
-  // Lanes l and l^32 share a query: the max is combined across them, the sums
-  // only in the epilogue.
+  // Online softmax of one tile in NMICRO micro-steps (log2 domain; lanes l and
+  // l^32 share a query and its running max). Value v of the score tile is key
+  // 16 (v >> 3) + 8 half + (v & 7); P~, H~ are packed as the B operands of the
+  // two 16-key chunks.
+  constexpr int NMICRO = 18;
   float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
-  struct TileSoft {
-    float alpha, neg_m;
+  struct Soft {
+    float mx, alpha, neg_m, ls, rs, pv;
+    float hv;
     bool moved;
   };
-  // row max of a score tile -> running max update (3 micro-steps, u = 0..2)
-  auto max_micro = [&](int u, float& mx, TileSoft& ts, const f32x16_t& sc) {
+  auto soft_micro = [&](int u, Soft& sm, const f32x16_t& sc, const f32x16_t& tc, i32x4_t (&pk)[2],
+                        i32x4_t (&hk)[2]) {
     if (u == 0) {
-      mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+      float a = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      float b2 = fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]));
+      float c2 = fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11]));
+      float d2 = fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]));
+      sm.mx = fmaxf(fmaxf(a, b2), fmaxf(c2, d2));
+      sm.ls = 0.f;
+      sm.rs = 0.f;
     } else if (u == 1) {
-      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11])),
-                           fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]))));
-    } else {
-      mx = fmaxf(mx, other_half(mx)) * p.scale_log2;
-      ts.moved = __builtin_amdgcn_ballot_w64(mx > m_i + kSlack) != 0;
-      const float m_new = ts.moved ? fmaxf(m_i, mx) : m_i;
-      ts.alpha = fast_exp2(m_i - m_new);
+      sm.mx = fmaxf(sm.mx, other_half(sm.mx)) * p.scale_log2;
+      sm.moved = __builtin_amdgcn_ballot_w64(sm.mx > m_i + kSlack) != 0;
+      const float m_new = sm.moved ? fmaxf(m_i, sm.mx) : m_i;
+      sm.alpha = fast_exp2(m_i - m_new);
       m_i = m_new;
-      ts.neg_m = -m_new;
-    }
-  };
-  // value v of a tile: P~, H~ packed in pairs (pv, hv hold the even value)
-  auto val_micro = [&](int v, const TileSoft& ts, float& pv, float& hv, const f32x16_t& sc, const f32x16_t& tc,
-                       i32x4_t (&pk)[2], i32x4_t (&hk)[2]) {
-    const float pe = fast_exp2(fmaf(sc[v], p.scale_log2, ts.neg_m));
-    float he = 0.f;
-    if constexpr (C::JVP) he = pe * (tc[v] * p.scale);
-    if (v & 1) {
-      pk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(pv, pe);
-      if constexpr (C::JVP) hk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(hv, he);
+      sm.neg_m = -m_new;
     } else {
-      pv = pe;
-      hv = he;
-    }
-  };
-  // row sums of the packed values (4 micro-steps, u = 0..3), then l and r
-  auto sum_micro = [&](int u, float& ls, float& rs, const TileSoft& ts, const i32x4_t (&pk)[2],
-                       const i32x4_t (&hk)[2]) {
-    if (u == 0) {
-      ls = 0.f;
-      rs = 0.f;
-    }
-    const int t = u >> 1, j0 = 2 * (u & 1);
-#pragma unroll
-    for (int j = j0; j < j0 + 2; ++j) {
-      ls = Elem<T>::dot2_ones(pk[t][j], ls);
-      if constexpr (C::JVP) rs = Elem<T>::dot2_ones(hk[t][j], rs);
-    }
-    if (u == 3) {
-      l_i = l_i * ts.alpha + ls;
-      if constexpr (C::JVP) r_i = r_i * ts.alpha + rs;
+      const int v = u - 2;
+      const float pe = fast_exp2(fmaf(sc[v], p.scale_log2, sm.neg_m));
+      sm.ls += pe;
+      float he = 0.f;
+      if constexpr (C::JVP) {
+        he = pe * (tc[v] * p.scale);
+        sm.rs += he;
+      }
+      if (v & 1) {
+        pk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(sm.pv, pe);
+        if constexpr (C::JVP) hk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(sm.hv, he);
+      } else {
+        sm.pv = pe;
+        sm.hv = he;
+      }
     }
   };
   auto rescale = [&](float alpha) {
@@ -318,22 +299,10 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
       }
     }
   };
-  // keys >= Lk of tile t score -inf (the last tile only)
-  auto mask_tile = [&](int t, f32x16_t& sc) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      if (t * BN + 16 * (v >> 3) + 8 * half + (v & 7) >= p.Lk) sc[v] = -__builtin_inff();
-    }
-  };
 
-  TileSoft cur;  // tile i's max state, computed one step ahead
-  // step i (i + 1 < ntiles, i % 4 == kk):
-  //   phase A: S^T, Sd^T of tile i+1 (K of stage i+1) || P~, H~ of tile i
-  //   phase B: O~^T, C~^T += ... of tile i (V of stage i) || row sums of tile i,
-  //            row max of tile i+1 (masked first if it is the last tile);
-  //            requests tile i+3
-  auto step = [&](auto kk, auto mask_next, int i, const f32x16_t& sc, const f32x16_t& tc, f32x16_t& sn,
-                  f32x16_t& tn) {
+  // step i (i + 1 < ntiles, i % 4 == kk): phase A on tile i+1's K, softmax of
+  // tile i (sc, tc); phase B on tile i's V; requests tile i+3
+  auto step = [&](auto kk, int i, const f32x16_t& sc, const f32x16_t& tc, f32x16_t& sn, f32x16_t& tn) {
     constexpr int k = decltype(kk)::value;
     ring_sync<C::LOADS>();  // tile i+1 has landed (tile i+2 may be in flight)
     pin_offsets();
@@ -343,22 +312,24 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
     i32x4_t opr[PF];
 #pragma unroll
     for (int o = 0; o < PF; ++o) opr[o] = load_op(s_next, s_cur, o);
+    Soft sm;
     i32x4_t pk[2], hk[2];
-    float pv = 0.f, hv = 0.f;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int o = 0; o < NOPA; ++o) {
       mfma_op(o, opr[o % PF], sn, tn, pk, hk);
       if (o + PF < NOP) opr[o % PF] = load_op(s_next, s_cur, o + PF);
 #pragma unroll
-      for (int v = o * 16 / NOPA; v < (o + 1) * 16 / NOPA; ++v) val_micro(v, cur, pv, hv, sc, tc, pk, hk);
+      for (int u = o * NMICRO / NOPA; u < (o + 1) * NMICRO / NOPA; ++u) soft_micro(u, sm, sc, tc, pk, hk);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (cur.moved) rescale(cur.alpha);
+    l_i = l_i * sm.alpha + sm.ls;
+    if constexpr (C::JVP) r_i = r_i * sm.alpha + sm.rs;
+    // keep the softmax in phase A: the values are used here, before the branch
+    asm volatile("" : "+v"(pk[0]), "+v"(pk[1]), "+v"(l_i));
+    if constexpr (C::JVP) asm volatile("" : "+v"(hk[0]), "+v"(hk[1]), "+v"(r_i));
+    if (sm.moved) rescale(sm.alpha);
     __builtin_amdgcn_sched_barrier(0);
-    constexpr int SUM0 = 1, MAX0 = NOPB / 2;  // phase B operands where the sums and the max start
-    float ls, rs, mx;
-    TileSoft nxt;
 #pragma unroll
     for (int o = NOPA; o < NOP; ++o) {
       mfma_op(o, opr[o % PF], sn, tn, pk, hk);
@@ -367,32 +338,29 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
       for (int li = 0; li < C::LOADS; ++li) {
         if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, i + 3, li);
       }
-      const int ob = o - NOPA;
-      if (ob >= SUM0 && ob < SUM0 + 4) sum_micro(ob - SUM0, ls, rs, cur, pk, hk);
-      if (ob == MAX0) {
-        if constexpr (decltype(mask_next)::value) mask_tile(i + 1, sn);
-      }
-      if (ob >= MAX0 && ob < MAX0 + 3) max_micro(ob - MAX0, mx, nxt, sn);
       __builtin_amdgcn_sched_barrier(0);
     }
-    cur = nxt;
   };
-  // last tile: P~, H~, rescale, PV, sums
-  auto last_step = [&](auto kk, const f32x16_t& sc, const f32x16_t& tc) {
+  // last tile (may hold keys >= Lk): masked softmax, rescale, PV
+  auto last_step = [&](auto kk, int i, f32x16_t& sc, const f32x16_t& tc) {
     const lds_char_t* s_cur = stage(kk);
-    i32x4_t pk[2], hk[2];
-    float pv = 0.f, hv = 0.f, ls, rs;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) val_micro(v, cur, pv, hv, sc, tc, pk, hk);
-    rescale(cur.alpha);
+    for (int v = 0; v < 16; ++v) {
+      if (i * BN + 16 * (v >> 3) + 8 * half + (v & 7) >= p.Lk) sc[v] = -__builtin_inff();
+    }
+    Soft sm;
+    i32x4_t pk[2], hk[2];
+#pragma unroll
+    for (int u = 0; u < NMICRO; ++u) soft_micro(u, sm, sc, tc, pk, hk);
+    l_i = l_i * sm.alpha + sm.ls;
+    if constexpr (C::JVP) r_i = r_i * sm.alpha + sm.rs;
+    rescale(sm.alpha);
     f32x16_t un_s, un_t;
 #pragma unroll
     for (int o = NOPA; o < NOP; ++o) mfma_op(o, load_op(s_cur, s_cur, o), un_s, un_t, pk, hk);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) sum_micro(u, ls, rs, cur, pk, hk);
   };
 
-  // ---- prologue: tiles 0..2 requested, scores and row max of tile 0
+  // ---- prologue: tiles 0..2 requested, scores of tile 0
 #pragma unroll
   for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
 #pragma unroll
@@ -406,43 +374,22 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
     const i32x4_t none[2] = {};
 #pragma unroll
     for (int o = 0; o < NOPA; ++o) mfma_op(o, load_op(s0, s0, o), sa, ta, none, none);
-    if (ntiles == 1) mask_tile(0, sa);
-    float mx;
-#pragma unroll
-    for (int u = 0; u < 3; ++u) max_micro(u, mx, cur, sa);
   }
-  using NoMask = std::false_type;
-  using Mask = std::true_type;
   int i = 0;
-  for (; i + 5 < ntiles; i += 4) {
-    step(IC<0>{}, NoMask{}, i, sa, ta, sb, tb);
-    step(IC<1>{}, NoMask{}, i + 1, sb, tb, sa, ta);
-    step(IC<2>{}, NoMask{}, i + 2, sa, ta, sb, tb);
-    step(IC<3>{}, NoMask{}, i + 3, sb, tb, sa, ta);
+  for (; i + 4 < ntiles; i += 4) {
+    step(IC<0>{}, i, sa, ta, sb, tb);
+    step(IC<1>{}, i + 1, sb, tb, sa, ta);
+    step(IC<2>{}, i + 2, sa, ta, sb, tb);
+    step(IC<3>{}, i + 3, sb, tb, sa, ta);
   }
-  // 1..5 tiles left; the step before the last tile masks that tile's scores
-  const int rest = ntiles - i;
-  if (rest == 1) {
-    last_step(IC<0>{}, sa, ta);
-  } else if (rest == 2) {
-    step(IC<0>{}, Mask{}, i, sa, ta, sb, tb);
-    last_step(IC<1>{}, sb, tb);
-  } else if (rest == 3) {
-    step(IC<0>{}, NoMask{}, i, sa, ta, sb, tb);
-    step(IC<1>{}, Mask{}, i + 1, sb, tb, sa, ta);
-    last_step(IC<2>{}, sa, ta);
-  } else if (rest == 4) {
-    step(IC<0>{}, NoMask{}, i, sa, ta, sb, tb);
-    step(IC<1>{}, NoMask{}, i + 1, sb, tb, sa, ta);
-    step(IC<2>{}, Mask{}, i + 2, sa, ta, sb, tb);
-    last_step(IC<3>{}, sb, tb);
-  } else {
-    step(IC<0>{}, NoMask{}, i, sa, ta, sb, tb);
-    step(IC<1>{}, NoMask{}, i + 1, sb, tb, sa, ta);
-    step(IC<2>{}, NoMask{}, i + 2, sa, ta, sb, tb);
-    step(IC<3>{}, Mask{}, i + 3, sb, tb, sa, ta);
-    last_step(IC<4>{}, sa, ta);
-  }
+  const int rest = ntiles - i;  // 1..4 tiles left
+  if (rest >= 2) step(IC<0>{}, i, sa, ta, sb, tb);
+  if (rest >= 3) step(IC<1>{}, i + 1, sb, tb, sa, ta);
+  if (rest >= 4) step(IC<2>{}, i + 2, sa, ta, sb, tb);
+  if (rest == 1) last_step(IC<0>{}, i, sa, ta);
+  else if (rest == 2) last_step(IC<1>{}, i + 1, sb, tb);
+  else if (rest == 3) last_step(IC<2>{}, i + 2, sa, ta);
+  else last_step(IC<3>{}, i + 3, sb, tb);
   wait_vmem();  // no requests beyond the last tile stay in flight
 
   // ---- epilogue: lane (query col, half) holds d = 32 db + 8 jj + 4 half + (0..3)

@@ -93,12 +93,6 @@ template <> struct Elem<__bf16> {
   __device__ __forceinline__ static float to_f32(uint16_t bits) {
     return __uint_as_float(((uint32_t)bits) << 16);
   }
-  // acc + lo + hi of a packed pair (v_dot2 with ones)
-  __device__ __forceinline__ static float dot2_ones(int pair, float acc) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), __builtin_bit_cast(bf16x2_t, 0x3f803f80u),
-                                           acc, false);
-  }
 };
 template <> struct Elem<_Float16> {
   using vec8 = f16x8_t;
@@ -111,10 +105,6 @@ template <> struct Elem<_Float16> {
   }
   __device__ __forceinline__ static float to_f32(uint16_t bits) {
     return (float)__builtin_bit_cast(_Float16, bits);
-  }
-  __device__ __forceinline__ static float dot2_ones(int pair, float acc) {
-    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
   }
 };
 
