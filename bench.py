@@ -37,6 +37,8 @@ def _args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--full-bwd", action="store_true", help="also time the full-derivative backward (extra field)")
+    ap.add_argument("--no-prologue", dest="prologue", action="store_false",
+                    help="skip timing the fused RMSNorm+RoPE prologue (extra field)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one elementwise kernel that reads and writes this many MiB "
                          "(a known-size reference for HBM byte counters under a profiler)")
@@ -93,6 +95,38 @@ def cpu_baseline(L, D, H, seconds):
                   f"(fwd+JVP+dO-only bwd) in {t:.1f} s; extrapolates to "
                   f"{H * L / done * t / 60:.0f} min for the 14B layer",
     }
+
+
+def prologue_timing(H, L, D, grid, dev):
+    """q and k prologues of one layer: [1, L, H*D] Linear outputs and tangents -> rotated BSHD pairs."""
+    import torch
+
+    from dmad_amd import _native, rmsnorm_rope_with_tangent
+    from dmad_amd.workload import rope_freqs_3d
+
+    C = H * D
+    g = torch.Generator(device=dev).manual_seed(3)
+    ys = [torch.randn(1, L, C, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    w = torch.ones(C, device=dev, dtype=torch.bfloat16)
+    freqs = rope_freqs_3d(*grid, D, device=dev) if grid is not None else None
+    for _ in range(2):
+        rmsnorm_rope_with_tangent((ys[0], ys[1]), w, 1e-6, freqs, H)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(5):
+        tq, tk = _native.KernelTimer(1), _native.KernelTimer(1)
+        with tq:
+            rmsnorm_rope_with_tangent((ys[0], ys[1]), w, 1e-6, freqs, H)
+        with tk:
+            rmsnorm_rope_with_tangent((ys[2], ys[3]), w, 1e-6, freqs, H)
+        torch.cuda.synchronize()
+        best = min(best, tq.elapsed()[0] + tk.elapsed()[0])
+    # algorithmic bytes per call: y, ty read and q, q_dot written (bf16), weight and angles
+    per_call = 4 * L * C * 2 + C * 2 + (L * D // 2 * 4 if grid is not None else 0)
+    gbs = 2 * per_call / (best * 1e-3) / 1e9
+    return {"kernel": "rmsnorm_rope_kernel<bf16,jvp,rope>", "ms_q_and_k": round(best, 4),
+            "bytes_per_call": per_call, "achieved_GBps": round(gbs, 1), "hbm_peak_GBps": 8000.0,
+            "frac": round(gbs / 8000.0, 4)}
 
 
 def main():
@@ -216,6 +250,10 @@ def main():
         b.record()
         torch.cuda.synchronize()
         out["ms_self_bwd_full"] = round(a.elapsed_time(b), 3)
+    # fused RMSNorm(+JVP) + RoPE prologue that produces q and k for this layer,
+    # timed after the step (HBM-bound; not part of the step or its flops)
+    if args.prologue:
+        out["prologue_rmsnorm_rope_jvp"] = prologue_timing(H, L, D, grid, dev)
     if args.calibration_copy_mib:
         n = args.calibration_copy_mib * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)

@@ -7,6 +7,8 @@ and the attention helpers of train/wan/rcm/utils/jvp_helper.py):
 * ``torch_attention_op_withT``      -- BSHD (x, x_dot) pairs in, (o, o_dot.detach()) out
 * ``torch_attention_op``            -- plain BSHD attention on the same kernels
 * ``plain_attention``               -- plain BHSD attention with backward
+* ``rmsnorm_rope_with_tangent``     -- fused RMSNorm(+JVP) and RoPE-with-tangent producing the op's q/k inputs
 """
 from .jvp_attention import _attention, attention, plain_attention, set_reference_backward  # noqa: F401
 from .jvp_helper import torch_attention_op, torch_attention_op_withT  # noqa: F401
+from .prologue import rmsnorm_rope_with_tangent  # noqa: F401

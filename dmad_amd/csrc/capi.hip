@@ -540,4 +540,49 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
   return ok();
 }
 
+int dmad_rmsnorm_rope_jvp(int dtype, int64_t rows, int64_t L, int64_t H, int64_t D, const void* y, const void* ty,
+                          int64_t y_stride, const void* weight, const float* freqs, float eps, void* out, void* tout,
+                          int64_t out_stride, void* stream) {
+  if (dtype != DMAD_BF16 && dtype != DMAD_F16) return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+  if (rows < 0 || H <= 0 || D <= 0) return fail(DMAD_ERR_INVALID, "bad sizes rows=%lld H=%lld D=%lld", (long long)rows,
+                                                (long long)H, (long long)D);
+  if (D % 8 != 0 || D > 512) return fail(DMAD_ERR_UNSUPPORTED, "head dim must be a multiple of 8 up to 512, got %lld",
+                                         (long long)D);
+  const int64_t C = H * D;
+  if (C > 64 * 8 * dmad::kPrologueMaxChunks)
+    return fail(DMAD_ERR_UNSUPPORTED, "model dim H*D = %lld exceeds %d", (long long)C, 64 * 8 * dmad::kPrologueMaxChunks);
+  if ((ty == nullptr) != (tout == nullptr)) return fail(DMAD_ERR_INVALID, "ty and tout must be both set or both null");
+  if (!(eps >= 0.f)) return fail(DMAD_ERR_INVALID, "eps must be non-negative");
+  if (rows == 0) return ok();
+  if (y == nullptr || weight == nullptr || out == nullptr) return fail(DMAD_ERR_INVALID, "null pointer");
+  for (const void* ptr : {y, ty, weight, (const void*)out, (const void*)tout})
+    if (ptr != nullptr && ((uintptr_t)ptr & 15) != 0) return fail(DMAD_ERR_INVALID, "pointers must be 16-byte aligned");
+  if (y_stride < C || out_stride < C || y_stride % 8 != 0 || out_stride % 8 != 0)
+    return fail(DMAD_ERR_INVALID, "row strides must be multiples of 8 and at least H*D");
+  if (freqs != nullptr && (L <= 0 || rows % L != 0))
+    return fail(DMAD_ERR_INVALID, "rows (%lld) must be a multiple of L (%lld)", (long long)rows, (long long)L);
+  if (rows > ((int64_t)1 << 34)) return fail(DMAD_ERR_UNSUPPORTED, "too many rows");
+  dmad::PrologueParams p{};
+  p.y = y;
+  p.ty = ty;
+  p.w = weight;
+  p.freqs = freqs;
+  p.out = out;
+  p.tout = tout;
+  p.rows = rows;
+  p.y_stride = y_stride;
+  p.o_stride = out_stride;
+  p.L = freqs != nullptr ? (int)L : 1;
+  p.C = (int)C;
+  p.D = (int)D;
+  p.eps = eps;
+  p.inv_c = 1.0f / (float)C;
+  hipStream_t s = (hipStream_t)stream;
+  mark(0, false, s);
+  const hipError_t e = dmad::launch_rmsnorm_rope(p, dtype, s);
+  mark(0, true, s);
+  if (e != hipSuccess) return fail(DMAD_ERR_HIP, "prologue launch: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

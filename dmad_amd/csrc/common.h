@@ -93,6 +93,8 @@ template <> struct Elem<__bf16> {
   __device__ __forceinline__ static float to_f32(uint16_t bits) {
     return __uint_as_float(((uint32_t)bits) << 16);
   }
+  // x rounded to bf16 (nearest even) and widened back
+  __device__ __forceinline__ static float round(float x) { return (float)(__bf16)x; }
 };
 template <> struct Elem<_Float16> {
   using vec8 = f16x8_t;
@@ -106,6 +108,7 @@ template <> struct Elem<_Float16> {
   __device__ __forceinline__ static float to_f32(uint16_t bits) {
     return (float)__builtin_bit_cast(_Float16, bits);
   }
+  __device__ __forceinline__ static float round(float x) { return (float)(_Float16)x; }
 };
 
 __device__ __forceinline__ f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c, __bf16) {

@@ -65,6 +65,21 @@ inline bool dout_only_reads_rows(int d) {
   }
 }
 
+// Fused RMSNorm(+tangent) + interleaved RoPE prologue (prologue.hip).
+constexpr int kPrologueMaxChunks = 20;  // 16-byte chunks per lane: C <= 64 * 8 * 20
+struct PrologueParams {
+  const void* y;      // [rows, C] (row stride y_stride elements)
+  const void* ty;     // tangent, same strides; null for the primal only
+  const void* w;      // [C] weight
+  const float* freqs;  // [L, D/2] angles; null skips the rotation
+  void* out;          // [rows, C] (row stride o_stride)
+  void* tout;         // tangent output; null iff ty is null
+  int64_t rows, y_stride, o_stride;
+  int L, C, D;
+  float eps, inv_c;
+};
+hipError_t launch_rmsnorm_rope(const PrologueParams& p, int dtype, hipStream_t s);
+
 hipError_t launch_transpose_pad(const TransposeParams& p, int BH, hipStream_t s);
 hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s);
 

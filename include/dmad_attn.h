@@ -105,6 +105,28 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
                       void* stream);
 
 /*
+ * Fused attention-input prologue: RMSNorm over the model dim C = H*D, then the
+ * interleaved rotary embedding, for a Linear output and its tangent in one HBM
+ * pass. Replaces WanRMSNorm._forward under torch.func.jvp
+ * (train/wan/rcm/networks/wan2pt1_jvp.py:207-216, applied to q and k at
+ * :312-317) followed by apply_rope_with_tangent (train/wan/rcm/utils/rope.py:
+ * 56-70, 106-114) as MinimalA2AAttnOpWithT.forward applies it
+ * (train/wan/rcm/utils/jvp_helper.py:180-196); the rounding points are the
+ * reference's (norm in float32, cast to the input type, times the weight in
+ * the input type; rotation in float32, cast back).
+ *   y, ty     : [rows, C] inputs (rows = B*L), row stride y_stride elements;
+ *               ty == NULL computes the primal only (then tout must be NULL)
+ *   weight    : [C] RMSNorm weight, same dtype
+ *   freqs     : [L, D/2] float32 angles, token l = row mod L; NULL: no rotation
+ *   out, tout : [rows, C] = [B, L, H, D] outputs, row stride out_stride
+ * D a multiple of 8 and <= 512, C = H*D <= 10240, pointers 16-byte aligned,
+ * strides multiples of 8 and >= C, rows a multiple of L when freqs is given.
+ */
+int dmad_rmsnorm_rope_jvp(int dtype, int64_t rows, int64_t L, int64_t H, int64_t D, const void* y, const void* ty,
+                          int64_t y_stride, const void* weight, const float* freqs, float eps, void* out, void* tout,
+                          int64_t out_stride, void* stream);
+
+/*
  * Timing hook (no counterpart in the reference; for benchmarks and profilers
  * that time kernels live). `events` points to `count` hipEvent_t handles; while
  * set, every dmad_attn_jvp_fwd / dmad_attn_fwd / dmad_attn_jvp_bwd call on

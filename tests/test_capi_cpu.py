@@ -106,3 +106,38 @@ def test_kernel_event_hook_validates(nat):
     arr = (ctypes.c_void_p * 10)()
     assert lib.dmad_set_kernel_events(arr, 10) == 1
     assert lib.dmad_set_kernel_events(None, 0) == 0
+
+
+def _pro(nat, **over):
+    a = dict(dtype=0, rows=64, L=32, H=2, D=64, y=256, ty=256, ys=128, w=256, freqs=256, eps=1e-6, out=256, tout=256,
+             os=128, stream=0)
+    a.update(over)
+    return nat.lib().dmad_rmsnorm_rope_jvp(
+        a["dtype"], a["rows"], a["L"], a["H"], a["D"], ctypes.c_void_p(a["y"]), ctypes.c_void_p(a["ty"]), a["ys"],
+        ctypes.c_void_p(a["w"]), ctypes.cast(ctypes.c_void_p(a["freqs"]), ctypes.POINTER(ctypes.c_float)), a["eps"],
+        ctypes.c_void_p(a["out"]), ctypes.c_void_p(a["tout"]), a["os"], ctypes.c_void_p(a["stream"]))
+
+
+@pytest.mark.parametrize(
+    "over,code,needle",
+    [
+        (dict(dtype=5), 2, "dtype"),
+        (dict(D=12), 2, "multiple of 8"),
+        (dict(D=1024), 2, "multiple of 8"),
+        (dict(H=100, D=128), 2, "exceeds"),
+        (dict(tout=0), 1, "both"),
+        (dict(y=0), 1, "null"),
+        (dict(out=264), 1, "aligned"),
+        (dict(ys=100), 1, "strides"),
+        (dict(os=64), 1, "strides"),
+        (dict(rows=48), 1, "multiple of L"),
+        (dict(eps=-1.0), 1, "eps"),
+    ],
+)
+def test_prologue_rejects_bad_arguments(nat, over, code, needle):
+    assert _pro(nat, **over) == code
+    assert needle in nat.lib().dmad_last_error().decode()
+
+
+def test_prologue_empty_is_a_no_op(nat):
+    assert _pro(nat, rows=0) == 0
