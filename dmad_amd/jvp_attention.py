@@ -24,6 +24,8 @@ Differences from the reference, all additive:
 """
 from __future__ import annotations
 
+from typing import Tuple
+
 import torch
 
 from . import _native as nat
@@ -232,34 +234,62 @@ class _attention(torch.autograd.Function):
 attention = _attention.apply
 
 
-class _plain_attention(torch.autograd.Function):
-    """Plain attention O = softmax(s Q K^T) V on the gfx950 forward kernel, with
-    the dO-only backward kernel (the same arithmetic the reference delegates to
-    flash-attn, flash_attention_jvp_triton.py:540-578)."""
+# Plain attention as registered torch ops, so that graph tools see one op per
+# pass: torch.compile traces it as a unit, and selective activation
+# checkpointing policies that keep attention outputs by name (the reference's
+# mm_only_policy saves any op whose name contains "flash_attn",
+# train/wan/rcm/utils/selective_activation_checkpoint.py:48-57) save its output
+# instead of recomputing the forward in the backward pass.
+@torch.library.custom_op("dmad::flash_attn_fwd", mutates_args=())
+def flash_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(O, LSE) of softmax(sm_scale Q K^T) V for [B, H, L, D] tensors (gfx950 forward kernel)."""
+    o, _, lse, _ = jvp_attention_forward(q, k, v, None, None, None, sm_scale)
+    return o, lse
 
-    @staticmethod
-    def forward(ctx, q, k, v, sm_scale=None):
-        assert q.shape[:-2] == k.shape[:-2] and k.shape[:-2] == v.shape[:-2]
-        assert k.shape[-2] == v.shape[-2] and q.shape[-1] == k.shape[-1]
-        assert q.shape[-1] in _HEAD_DIMS and v.shape[-1] in _HEAD_DIMS
-        if sm_scale is None:
-            sm_scale = q.shape[-1] ** (-0.5)
-        o, _, lse, _ = jvp_attention_forward(q, k, v, None, None, None, sm_scale)
-        if any(x.requires_grad for x in (q, k, v)):
-            ctx.save_for_backward(q, k, v, o, lse)
-            ctx.sm_scale = sm_scale
-        return o
 
-    @staticmethod
-    def backward(ctx, dout):
-        q, k, v, o, lse = ctx.saved_tensors
-        assert q.shape[-1] == v.shape[-1], "Backward not supported with different headdim."
-        dq, dk, dv, _, _, _ = jvp_attention_backward(
-            q, k, v, None, None, None, o, None, lse, None, dout, None, ctx.sm_scale, False
-        )
-        return dq, dk, dv, None
+@flash_attn_fwd.register_fake
+def _(q, k, v, sm_scale):
+    B, H, Lq, _ = q.shape
+    return q.new_empty((B, H, Lq, v.shape[-1])), q.new_empty((B, H, Lq), dtype=torch.float32)
+
+
+@torch.library.custom_op("dmad::flash_attn_bwd", mutates_args=())
+def flash_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                   lse: torch.Tensor, sm_scale: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """dO-only gradients (dQ, dK, dV) of flash_attn_fwd (the arithmetic the reference
+    delegates to flash-attn, flash_attention_jvp_triton.py:540-578)."""
+    dq, dk, dv, _, _, _ = jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, dout, None, sm_scale,
+                                                 False)
+    return dq, dk, dv
+
+
+@flash_attn_bwd.register_fake
+def _(dout, q, k, v, o, lse, sm_scale):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _fwd_setup_context(ctx, inputs, output):
+    q, k, v, sm_scale = inputs
+    o, lse = output
+    ctx.save_for_backward(q, k, v, o, lse)
+    ctx.sm_scale = sm_scale
+
+
+def _fwd_backward(ctx, dout, dlse):
+    q, k, v, o, lse = ctx.saved_tensors
+    assert q.shape[-1] == v.shape[-1], "Backward not supported with different headdim."
+    dq, dk, dv = torch.ops.dmad.flash_attn_bwd(dout, q, k, v, o, lse, ctx.sm_scale)
+    return dq, dk, dv, None
+
+
+flash_attn_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
 
 
 def plain_attention(q, k, v, sm_scale=None):
-    """softmax(sm_scale * q k^T) v for [B, H, L, D] tensors (gfx950 kernels)."""
-    return _plain_attention.apply(q, k, v, sm_scale)
+    """softmax(sm_scale * q k^T) v for [B, H, L, D] tensors (gfx950 kernels), with backward."""
+    assert q.shape[:-2] == k.shape[:-2] and k.shape[:-2] == v.shape[:-2]
+    assert k.shape[-2] == v.shape[-2] and q.shape[-1] == k.shape[-1]
+    assert q.shape[-1] in _HEAD_DIMS and v.shape[-1] in _HEAD_DIMS
+    if sm_scale is None:
+        sm_scale = q.shape[-1] ** (-0.5)
+    return torch.ops.dmad.flash_attn_fwd(q, k, v, float(sm_scale))[0]

@@ -1,0 +1,79 @@
+"""Plain attention as registered torch ops (dmad::flash_attn_fwd / flash_attn_bwd).
+
+The reference's selective-activation-checkpointing policy saves an op's output
+when its name contains "flash_attn" and recomputes everything else
+(train/wan/rcm/utils/selective_activation_checkpoint.py:48-57, restated below
+as `mm_only_policy`). Through the registered op the attention forward runs
+once per step under that policy, and its gradients are the oracle's.
+"""
+import pytest
+import torch
+from torch.utils.checkpoint import CheckpointPolicy, checkpoint, create_selective_checkpoint_contexts
+
+import dmad_amd  # noqa: F401  (registers the ops)
+from oracle import attention as orc
+
+SAVE = {torch.ops.aten.mm.default, torch.ops.aten.addmm.default}
+
+
+def mm_only_policy(ctx, func, *args, **kwargs):
+    name = str(func)
+    keep = func in SAVE or "flash_attn" in name or "magi" in name
+    return CheckpointPolicy.MUST_SAVE if keep else CheckpointPolicy.PREFER_RECOMPUTE
+
+
+def test_ops_are_registered_with_flash_attn_names():
+    assert "flash_attn" in str(torch.ops.dmad.flash_attn_fwd.default)
+    assert "flash_attn" in str(torch.ops.dmad.flash_attn_bwd.default)
+    assert mm_only_policy(None, torch.ops.dmad.flash_attn_fwd.default) == CheckpointPolicy.MUST_SAVE
+
+
+def test_fake_tensor_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(2, 3, 100, 64, dtype=torch.bfloat16)
+        k = torch.empty(2, 3, 70, 64, dtype=torch.bfloat16)
+        v = torch.empty(2, 3, 70, 32, dtype=torch.bfloat16)
+        o, lse = torch.ops.dmad.flash_attn_fwd(q, k, v, 0.125)
+        assert o.shape == (2, 3, 100, 32) and o.dtype == torch.bfloat16
+        assert lse.shape == (2, 3, 100) and lse.dtype == torch.float32
+
+
+@pytest.mark.gpu
+def test_selective_checkpointing_saves_the_attention_forward(gpu, monkeypatch):
+    from dmad_amd import jvp_attention, torch_attention_op
+
+    calls = {"fwd": 0}
+    real = jvp_attention.jvp_attention_forward
+
+    def counted(*a, **kw):
+        calls["fwd"] += 1
+        return real(*a, **kw)
+
+    monkeypatch.setattr(jvp_attention, "jvp_attention_forward", counted)
+    g = torch.Generator().manual_seed(11)
+    B, S, H, D = 1, 300, 2, 128
+    xs = [(torch.randn((B, S, H, D), generator=g) * 0.5).to(torch.bfloat16) for _ in range(4)]
+    w = torch.randn((D, D), generator=g) / D ** 0.5  # float32 projection (no bf16 batched products)
+    q, k, v, do = (x.to(gpu) for x in xs)
+    wq = w.to(gpu).requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+
+    def block(q, k, v):
+        return torch_attention_op((q.float() @ wq).to(torch.bfloat16), k, v)
+
+    out = checkpoint(block, q, k, v, use_reentrant=False,
+                     context_fn=lambda: create_selective_checkpoint_contexts(mm_only_policy))
+    out.backward(do)
+    torch.cuda.synchronize()
+    assert calls["fwd"] == 1, calls  # saved, not recomputed in the backward
+    # gradients against the oracle (through the projection of q)
+    qp = (q.float() @ wq.detach()).to(torch.bfloat16)
+    rq, rk, rv = orc.grads_dout_only(*(x.double().cpu().transpose(1, 2) for x in (qp, k.detach(), v.detach(), do)),
+                                     sm_scale=D ** -0.5)
+    assert orc.rel_l2(k.grad.transpose(1, 2), rk) <= 1e-2
+    assert orc.rel_l2(v.grad.transpose(1, 2), rv) <= 1e-2
+    ref_wq = torch.einsum("bshd,bshe->de", q.double().cpu(), rq.transpose(1, 2))
+    assert orc.rel_l2(wq.grad, ref_wq) <= 1e-2
