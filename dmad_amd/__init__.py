@@ -8,7 +8,10 @@ and the attention helpers of train/wan/rcm/utils/jvp_helper.py):
 * ``torch_attention_op``            -- plain BSHD attention on the same kernels
 * ``plain_attention``               -- plain BHSD attention with backward
 * ``rmsnorm_rope_with_tangent``     -- fused RMSNorm(+JVP) and RoPE-with-tangent producing the op's q/k inputs
+* ``magimask``                      -- block-sparse mask tables (MagiMask) for ``attention(..., magi_mask)``
 """
 from .jvp_attention import _attention, attention, plain_attention, set_reference_backward  # noqa: F401
 from .jvp_helper import torch_attention_op, torch_attention_op_withT  # noqa: F401
 from .prologue import rmsnorm_rope_with_tangent  # noqa: F401
+from . import magimask  # noqa: F401
+from .magimask import MagiMask, prepare_magi_csr_and_tasks  # noqa: F401

@@ -44,6 +44,10 @@ SIGNATURES = {
     "dmad_attn_jvp_fwd": (_INT, [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _I64,
                                  _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
                                  _P, _P, _I64P, _P, _P, _F, _P, _SZ, _P]),
+    "dmad_attn_jvp_fwd_magi": (_INT, [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _I64,
+                                      _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
+                                      _P, _P, _I64P, _P, _P, _F,
+                                      _P, _P, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _SZ, _P]),
     "dmad_attn_fwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
                              _I64P, _I64P, _I64P, _P, _I64P, _P, _F, _P, _SZ, _P]),
     "dmad_set_kernel_events": (_INT, [ctypes.POINTER(ctypes.c_void_p), _INT]),

@@ -62,7 +62,98 @@ struct FwdParams {
   int B, H, Lq, Lk, LKP;
   float scale;       // softmax scale s
   float scale_log2;  // s * log2(e)
+  // block-sparse (MagiMask) mode of attn_fwd32_kernel: query groups partition
+  // [0, Lq); group g attends to the sorted, disjoint key ranges
+  // k_ranges[qk_map[g] .. qk_map[g+1]); a task is a (group, 128-query tile) pair
+  const int* q_ranges;    // [G][2]
+  const int* k_ranges;    // [R][2]
+  const int* qk_map;      // [G+1]
+  const int* task_group;  // [T]
+  const int* task_qtile;  // [T]
+  int G, R, T;
 };
+
+// One (query group, 128-query tile) task of the block-sparse forward: group
+// and key-range indices clamped into the arrays, the query range and the key
+// ranges clipped to the sequences, so malformed tables read nothing outside
+// them. The query tile is 128 rows from row0.
+struct MagiTask {
+  int row0, q_lo, q_hi, r_beg, r_end;
+};
+__device__ __forceinline__ MagiTask magi_task(const FwdParams& p, int task, int bm) {
+  MagiTask t;
+  const int g = min(max(__builtin_amdgcn_readfirstlane(p.task_group[task]), 0), p.G - 1);
+  t.row0 = __builtin_amdgcn_readfirstlane(p.task_qtile[task]) * bm;
+  t.q_lo = max(__builtin_amdgcn_readfirstlane(p.q_ranges[2 * g]), 0);
+  t.q_hi = min(__builtin_amdgcn_readfirstlane(p.q_ranges[2 * g + 1]), p.Lq);
+  t.r_beg = min(max(__builtin_amdgcn_readfirstlane(p.qk_map[g]), 0), p.R);
+  t.r_end = min(max(__builtin_amdgcn_readfirstlane(p.qk_map[g + 1]), t.r_beg), p.R);
+  return t;
+}
+// Key range r clipped to [0, Lk) (empty when k1 <= k0).
+__device__ __forceinline__ void magi_range(const FwdParams& p, int r, int& k0, int& k1) {
+  k0 = max(__builtin_amdgcn_readfirstlane(p.k_ranges[2 * r]), 0);
+  k1 = min(__builtin_amdgcn_readfirstlane(p.k_ranges[2 * r + 1]), p.Lk);
+}
+// 32-key (BN-key) tiles the task walks: per range, from the tile holding its
+// first key to the one holding its last.
+__device__ __forceinline__ int magi_ntiles(const FwdParams& p, const MagiTask& t, int bn) {
+  int n = 0;
+  for (int r = t.r_beg; r < t.r_end; ++r) {
+    int k0, k1;
+    magi_range(p, r, k0, k1);
+    if (k1 > k0) n += (k1 + bn - 1) / bn - k0 / bn;
+  }
+  return n;
+}
+// Walks the key tiles of a task: current range r (clipped to [k0, k1)) and
+// the first key row of the current BN-key tile; past the last range it
+// points at row Lk and beyond (tiles of zeros, never used).
+struct MagiCursor {
+  int r, r_end, start, k0, k1;
+  __device__ __forceinline__ void seek(const FwdParams& p, int bn) {  // first non-empty range from r on
+    for (; r < r_end; ++r) {
+      magi_range(p, r, k0, k1);
+      if (k1 > k0) {
+        start = k0 / bn * bn;
+        return;
+      }
+    }
+    start = k0 = k1 = p.Lk;
+  }
+  __device__ __forceinline__ void next(const FwdParams& p, int bn) {
+    start += bn;
+    if (start >= k1 && r < r_end) {
+      ++r;
+      seek(p, bn);
+    }
+  }
+  // key lies outside the current range (the reference's n_mask, :338-343)
+  __device__ __forceinline__ bool masked(int key) const { return (unsigned)(key - k0) >= (unsigned)(k1 - k0); }
+  // the current tile has keys outside the range
+  __device__ __forceinline__ bool partial(int bn) const { return start < k0 || start + bn > k1; }
+};
+
+// Rows of a task whose group has no key in [0, Lk): O = Od = 0 and LSE = -inf,
+// what the reference's epilogue gives for l_i == 0 (:386-400); mu = 0. The
+// whole workgroup (any size) writes 16-byte chunks.
+template <typename T, int DV, bool JVP>
+__device__ void magi_store_empty(const FwdParams& p, int bh, const MagiTask& t, int bm) {
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int lo = max(t.row0, t.q_lo), hi = min(t.row0 + bm, t.q_hi);
+  constexpr int CH = DV / 8;
+  const int64_t obase = b * p.o_sb + h * p.o_sh;
+  for (int idx = threadIdx.x; idx < (hi - lo) * CH; idx += blockDim.x) {
+    const int r = lo + idx / CH, c = idx - (idx / CH) * CH;
+    const int64_t off = (obase + (int64_t)r * p.o_sl + 8 * c) * 2;
+    *(i32x4_t*)((char*)p.o + off) = i32x4_t{0, 0, 0, 0};
+    if constexpr (JVP) *(i32x4_t*)((char*)p.to + off) = i32x4_t{0, 0, 0, 0};
+  }
+  for (int r = lo + (int)threadIdx.x; r < hi; r += blockDim.x) {
+    p.lse[(int64_t)bh * p.Lq + r] = -__builtin_inff();
+    if constexpr (JVP) p.mu[(int64_t)bh * p.Lq + r] = 0.f;
+  }
+}
 
 // Rescale threshold (log2 units): the running max used for exp2 only moves when
 // a row's tile max exceeds it by more than this, so the accumulators are
@@ -803,7 +894,11 @@ struct FwdSimpleCfg {
   static constexpr int VPW = (NVI + NW - 1) / NW;
 };
 
-template <typename T, int DQK, int DV, int MODE>
+// MAGI: the block-sparse variant for every head shape (the reference's
+// `_attn_fwd_magi`, flash_attention_jvp_triton.py:242-409): one (query group,
+// 128-query tile) task per workgroup, key tiles walking the group's ranges,
+// keys outside the current range at -inf, only the group's rows stored.
+template <typename T, int DQK, int DV, int MODE, bool MAGI = false>
 __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   using C = FwdSimpleCfg<DQK, DV, MODE>;
   constexpr int BN = C::BN, NB = C::NB, KS = C::KS, DB = C::DB, CK = C::CK, CV = C::CV;
@@ -813,9 +908,31 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 31, half = lane >> 5;
 
-  const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
-  const int bh = work / nqt, qt = work - bh * nqt;
+  int bh, qt, ntiles;
+  int q_lo = 0, q_hi = p.Lq;         // rows this workgroup stores
+  MagiCursor cm{0, 0, 0, 0, 0};      // MAGI: tile in use
+  if constexpr (MAGI) {
+    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H);
+    bh = work / p.T;
+    const MagiTask t = magi_task(p, work - bh * p.T, C::BM);
+    qt = t.row0 / C::BM;
+    q_lo = t.q_lo;
+    q_hi = t.q_hi;
+    ntiles = magi_ntiles(p, t, BN);
+    if (ntiles == 0) {  // uniform over the workgroup: nothing requested yet
+      magi_store_empty<T, DV, C::JVP>(p, bh, t, C::BM);
+      return;
+    }
+    cm = MagiCursor{t.r_beg, t.r_end, 0, 0, 0};
+    cm.seek(p, BN);
+  } else {
+    const int nqt = (p.Lq + C::BM - 1) / C::BM;
+    const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+    bh = work / nqt;
+    qt = work - bh * nqt;
+    ntiles = (p.Lk + BN - 1) / BN;
+  }
+  MagiCursor ci = cm;  // MAGI: tile requested next
   const int b = bh / p.H, h = bh - b * p.H;
 
   const char* qbase = (const char*)p.q + (b * p.q_sb + h * p.q_sh) * 2;
@@ -861,10 +978,17 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   }
   const uint32_t k_tile_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
 
+  // tile kt (MAGI: the tile whose first key row is kt) into stage `stage`
   auto issue_tile = [&](int kt, int stage) {
     char* st = smem + stage * C::STAGE;
-    const uint32_t ks = (uint32_t)kt * k_tile_step;
-    const uint32_t vs = (uint32_t)kt * BN * 2;
+    uint32_t ks, vs;
+    if constexpr (MAGI) {
+      ks = (uint32_t)kt * (uint32_t)(p.k_sl * 2);
+      vs = (uint32_t)kt * 2;
+    } else {
+      ks = (uint32_t)kt * k_tile_step;
+      vs = (uint32_t)kt * BN * 2;
+    }
 #pragma unroll
     for (int j = 0; j < C::KPW; ++j) {
       const int i = wave + j * C::NW;
@@ -899,12 +1023,12 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   }
   float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
 
-  const int ntiles = (p.Lk + BN - 1) / BN;
-  issue_tile(0, 0);
+  issue_tile(MAGI ? ci.start : 0, 0);
   for (int kt = 0; kt < ntiles; ++kt) {
     wait_vmem();
     __syncthreads();
-    if (kt + 1 < ntiles) issue_tile(kt + 1, (kt + 1) & 1);
+    if constexpr (MAGI) ci.next(p, BN);
+    if (kt + 1 < ntiles) issue_tile(MAGI ? ci.start : kt + 1, (kt + 1) & 1);
     const char* st = smem + (kt & 1) * C::STAGE;
 
     // ---- S^T and Sd^T for BN keys x 32 queries
@@ -932,8 +1056,21 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
       }
     }
 
-    // ---- tail keys -> -inf
-    if ((kt + 1) * BN > p.Lk) {
+    // ---- tail keys (MAGI: keys outside the current range) -> -inf
+    if constexpr (MAGI) {
+      if (cm.partial(BN)) {
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int j = v >> 2;
+            const int key = cm.start + kb * 32 + ((j >> 1) << 4) + (half << 3) + ((j & 1) << 2) + (v & 3);
+            if (cm.masked(key)) sacc[kb][v] = -__builtin_inff();
+          }
+        }
+      }
+      cm.next(p, BN);
+    } else if ((kt + 1) * BN > p.Lk) {
 #pragma unroll
       for (int kb = 0; kb < NB; ++kb) {
 #pragma unroll
@@ -1021,7 +1158,9 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
   __amdgpu_buffer_rsrc_t rto = ro;
   if constexpr (C::JVP) rto = make_rsrc((char*)p.to + obase * 2, o_bytes);
-  const uint32_t orow = (uint32_t)((int64_t)qrow * p.o_sl * 2);
+  // rows >= Lq fall outside the resource; MAGI stores only the group's rows
+  const bool keep = !MAGI || (qrow >= q_lo && qrow < q_hi);
+  const uint32_t orow = keep ? (uint32_t)((int64_t)qrow * p.o_sl * 2) : o_bytes;
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -1044,7 +1183,7 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
       }
     }
   }
-  if (half == 0 && qrow < p.Lq) {
+  if (half == 0 && qrow < p.Lq && keep) {
     const int64_t si = (int64_t)bh * p.Lq + qrow;
     p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
     if constexpr (C::JVP) p.mu[si] = mu;

@@ -61,7 +61,13 @@ struct Fwd32Cfg {
 // its variants, which read a transposed copy of V).
 constexpr bool fwd32_supported(int dqk, int dv) { return dqk == 128 && dv == 128; }
 
-template <typename T, int MODE>
+// MAGI: the block-sparse variant (the reference's `_attn_fwd_magi`,
+// flash_attention_jvp_triton.py:242-409). The workgroup runs one (query group,
+// 128-query tile) task; its key tiles walk the group's key ranges in order, a
+// range starting at a 32-key boundary below its first key, and keys outside the
+// current range score -inf (the reference's n_mask, :338-343). Only the tile's
+// rows inside the group's query range are stored (:386-409).
+template <typename T, int MODE, bool MAGI = false>
 __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
   using C = Fwd32Cfg<MODE>;
   constexpr int D = C::D, BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
@@ -77,11 +83,31 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 31, half = lane >> 5;
 
-  const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
-  const int bh = work / nqt, qt = work - bh * nqt;
+  int bh, qt, ntiles;
+  int q_lo = 0, q_hi = p.Lq;  // rows this workgroup stores
+  int r_beg = 0, r_end = 0;   // key ranges of the group (MAGI)
+  if constexpr (MAGI) {
+    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H);
+    bh = work / p.T;
+    const MagiTask t = magi_task(p, work - bh * p.T, C::BM);
+    qt = t.row0 / C::BM;
+    q_lo = t.q_lo;
+    q_hi = t.q_hi;
+    r_beg = t.r_beg;
+    r_end = t.r_end;
+    ntiles = magi_ntiles(p, t, BN);
+    if (ntiles == 0) {  // uniform over the workgroup: nothing requested yet
+      magi_store_empty<T, D, C::JVP>(p, bh, t, C::BM);
+      return;
+    }
+  } else {
+    const int nqt = (p.Lq + C::BM - 1) / C::BM;
+    const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+    bh = work / nqt;
+    qt = work - bh * nqt;
+    ntiles = (p.Lk + BN - 1) / BN;
+  }
   const int b = bh / p.H, h = bh - b * p.H;
-  const int ntiles = (p.Lk + BN - 1) / BN;
 
   // ---- this lane's query: Q (and Qd) row slices, B operands of the score MFMAs
   const int query = qt * C::BM + wave * 32 + col;
@@ -139,11 +165,19 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
     else if constexpr (k == 2) return (lds_char_t*)stg2;
     else return (lds_char_t*)stg3;
   };
-  // request li (0 <= li < LOADS) of tile kt into stage st; tiles at or beyond
-  // the end read zeros or in-range rows into a stage nobody reads again
+  // request li (0 <= li < LOADS) of tile kt into stage st (MAGI: of the tile
+  // whose first key row is kt); tiles at or beyond the end read zeros or
+  // in-range rows into a stage nobody reads again
   auto issue_load = [&](lds_char_t* st, int kt, int li) {
     const int t = li % C::NTILE, jj = li / C::NTILE, i = wave + jj * C::NW;
-    const uint32_t ks = (uint32_t)kt * k_step, vs = (uint32_t)kt * v_step;
+    uint32_t ks, vs;
+    if constexpr (MAGI) {
+      ks = (uint32_t)kt * (uint32_t)(p.k_sl * 2);
+      vs = (uint32_t)kt * (uint32_t)(p.v_sl * 2);
+    } else {
+      ks = (uint32_t)kt * k_step;
+      vs = (uint32_t)kt * v_step;
+    }
     if (t == 0) buf_load16_lds(rk, st + C::OFF_K + i * 1024, roff_k[jj], ks);
     else if (t == 1) buf_load16_lds(rv, st + C::OFF_V + i * 1024, roff_v[jj], vs);
     else if (t == 2) buf_load16_lds(rtk, st + C::OFF_KT + i * 1024, roff_k[jj], ks);
@@ -300,6 +334,17 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
     }
   };
 
+  // keys of the cursor's tile outside its range score -inf
+  auto mask_range = [&](f32x16_t& sc, const MagiCursor& c) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      if (c.masked(c.start + 16 * (v >> 3) + 8 * half + (v & 7))) sc[v] = -__builtin_inff();
+    }
+  };
+  MagiCursor ci{r_beg, r_end, 0, 0, 0};  // MAGI: tile requested next
+  if constexpr (MAGI) ci.seek(p, BN);
+  MagiCursor cm = ci;  // MAGI: tile whose softmax runs next
+
   // step i (i + 1 < ntiles, i % 4 == kk): phase A on tile i+1's K, softmax of
   // tile i (sc, tc); phase B on tile i's V; requests tile i+3
   auto step = [&](auto kk, int i, const f32x16_t& sc, const f32x16_t& tc, f32x16_t& sn, f32x16_t& tn) {
@@ -314,6 +359,10 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
     for (int o = 0; o < PF; ++o) opr[o] = load_op(s_next, s_cur, o);
     Soft sm;
     i32x4_t pk[2], hk[2];
+    if constexpr (MAGI) {
+      if (cm.partial(BN)) mask_range(const_cast<f32x16_t&>(sc), cm);
+      cm.next(p, BN);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int o = 0; o < NOPA; ++o) {
@@ -336,17 +385,22 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
       if (o + PF < NOP) opr[o % PF] = load_op(s_next, s_cur, o + PF);
 #pragma unroll
       for (int li = 0; li < C::LOADS; ++li) {
-        if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, i + 3, li);
+        if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, MAGI ? ci.start : i + 3, li);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (MAGI) ci.next(p, BN);
   };
   // last tile (may hold keys >= Lk): masked softmax, rescale, PV
   auto last_step = [&](auto kk, int i, f32x16_t& sc, const f32x16_t& tc) {
     const lds_char_t* s_cur = stage(kk);
+    if constexpr (MAGI) {
+      mask_range(sc, cm);
+    } else {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      if (i * BN + 16 * (v >> 3) + 8 * half + (v & 7) >= p.Lk) sc[v] = -__builtin_inff();
+      for (int v = 0; v < 16; ++v) {
+        if (i * BN + 16 * (v >> 3) + 8 * half + (v & 7) >= p.Lk) sc[v] = -__builtin_inff();
+      }
     }
     Soft sm;
     i32x4_t pk[2], hk[2];
@@ -361,12 +415,24 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
   };
 
   // ---- prologue: tiles 0..2 requested, scores of tile 0
+  if constexpr (MAGI) {
 #pragma unroll
-  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), ci.start, li);
+    ci.next(p, BN);
 #pragma unroll
-  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), ci.start, li);
+    ci.next(p, BN);
 #pragma unroll
-  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), ci.start, li);
+    ci.next(p, BN);
+  } else {
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+#pragma unroll
+    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+  }
   ring_sync<2 * C::LOADS>();  // Q slices and tile 0
   f32x16_t sa, ta, sb, tb;
   {
@@ -402,7 +468,9 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
   const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
   __amdgpu_buffer_rsrc_t rto = ro;
   if constexpr (C::JVP) rto = make_rsrc((char*)p.to + obase * 2, o_bytes);
-  const uint32_t orow = (uint32_t)((int64_t)query * p.o_sl * 2);  // rows >= Lq fall outside the resource
+  // rows >= Lq fall outside the resource; MAGI stores only the group's rows
+  const bool keep = !MAGI || (query >= q_lo && query < q_hi);
+  const uint32_t orow = keep ? (uint32_t)((int64_t)query * p.o_sl * 2) : o_bytes;
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -419,7 +487,7 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
       if constexpr (C::JVP) buf_store8(rto, u32x2_t{Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])}, off);
     }
   }
-  if (half == 0 && query < p.Lq) {
+  if (half == 0 && query < p.Lq && keep) {
     const int64_t si = (int64_t)bh * p.Lq + query;
     p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
     if constexpr (C::JVP) p.mu[si] = mu;

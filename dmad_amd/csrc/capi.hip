@@ -39,6 +39,16 @@ template <> DqLaunchFn dq_select<_Float16, 32>(int);
 template <> DqLaunchFn dq_select<_Float16, 64>(int);
 template <> DqLaunchFn dq_select<_Float16, 128>(int);
 template <> DqLaunchFn dq_select<_Float16, 256>(int);
+template <> FwdLaunchFn fwd_magi_select<__bf16, 16>(int, int);
+template <> FwdLaunchFn fwd_magi_select<__bf16, 32>(int, int);
+template <> FwdLaunchFn fwd_magi_select<__bf16, 64>(int, int);
+template <> FwdLaunchFn fwd_magi_select<__bf16, 128>(int, int);
+template <> FwdLaunchFn fwd_magi_select<__bf16, 256>(int, int);
+template <> FwdLaunchFn fwd_magi_select<_Float16, 16>(int, int);
+template <> FwdLaunchFn fwd_magi_select<_Float16, 32>(int, int);
+template <> FwdLaunchFn fwd_magi_select<_Float16, 64>(int, int);
+template <> FwdLaunchFn fwd_magi_select<_Float16, 128>(int, int);
+template <> FwdLaunchFn fwd_magi_select<_Float16, 256>(int, int);
 }  // namespace dmad
 
 namespace {
@@ -124,6 +134,34 @@ dmad::FwdLaunchFn pick_fwd(int dtype, int64_t dqk, int64_t dv, int mode) {
   return nullptr;
 }
 
+dmad::FwdLaunchFn pick_fwd_magi(int dtype, int64_t dqk, int64_t dv, int mode) {
+  using namespace dmad;
+  if (dtype == DMAD_BF16) {
+    switch (dqk) {
+      case 16: return fwd_magi_select<__bf16, 16>((int)dv, mode);
+      case 32: return fwd_magi_select<__bf16, 32>((int)dv, mode);
+      case 64: return fwd_magi_select<__bf16, 64>((int)dv, mode);
+      case 128: return fwd_magi_select<__bf16, 128>((int)dv, mode);
+      case 256: return fwd_magi_select<__bf16, 256>((int)dv, mode);
+    }
+  } else if (dtype == DMAD_F16) {
+    switch (dqk) {
+      case 16: return fwd_magi_select<_Float16, 16>((int)dv, mode);
+      case 32: return fwd_magi_select<_Float16, 32>((int)dv, mode);
+      case 64: return fwd_magi_select<_Float16, 64>((int)dv, mode);
+      case 128: return fwd_magi_select<_Float16, 128>((int)dv, mode);
+      case 256: return fwd_magi_select<_Float16, 256>((int)dv, mode);
+    }
+  }
+  return nullptr;
+}
+
+// Block-sparse tables of dmad_attn_jvp_fwd_magi (device pointers).
+struct MagiArgs {
+  const int32_t *q_ranges, *k_ranges, *qk_map, *task_group, *task_qtile;
+  int64_t G, R, T;
+};
+
 dmad::BwdLaunchFn pick_bwd(int dtype, int64_t d, int mode) {
   using namespace dmad;
   if (dtype == DMAD_BF16) {
@@ -192,36 +230,12 @@ BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) 
   return w;
 }
 
-}  // namespace
-
-extern "C" {
-
-int dmad_abi_version(void) { return 1; }
-
-const char* dmad_last_error(void) { return g_last_error.c_str(); }
-
-int dmad_set_kernel_events(void* const* events, int count) {
-  if (count < 0 || count > kMaxEvents || (count % 2) != 0)
-    return fail(DMAD_ERR_INVALID, "count must be an even number in [0, %d]", kMaxEvents);
-  if (count > 0 && events == nullptr) return fail(DMAD_ERR_INVALID, "events: null pointer");
-  for (int i = 0; i < count; ++i) g_events[i] = (hipEvent_t)events[i];
-  g_nevents = count;
-  return ok();
-}
-
-int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dv, size_t* bytes) {
-  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
-  if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
-  if (B < 0 || H < 0 || Lk < 0 || !head_dim_ok(Dv)) return fail(DMAD_ERR_INVALID, "bad sizes");
-  *bytes = (size_t)fwd_ws_bytes(mode, B, H, Lk, Dv);
-  return ok();
-}
-
-int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
-                      const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
-                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4], void* o,
-                      void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale, void* workspace,
-                      size_t workspace_bytes, void* stream) {
+// Shared body of the dense and block-sparse forwards (mg == nullptr: dense).
+int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv, const void* q,
+             const void* k, const void* v, const void* tq, const void* tk, const void* tv, const int64_t q_strides[4],
+             const int64_t k_strides[4], const int64_t v_strides[4], void* o, void* to, const int64_t o_strides[4],
+             float* lse, float* mu, float sm_scale, void* workspace, size_t workspace_bytes, void* stream,
+             const MagiArgs* mg) {
   if (dtype != DMAD_BF16 && dtype != DMAD_F16) return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
   if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
   if (B < 0 || H < 0 || Lq < 0 || Lk < 0) return fail(DMAD_ERR_INVALID, "negative size");
@@ -229,7 +243,9 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
     return fail(DMAD_ERR_UNSUPPORTED, "head dims must be in {16,32,64,128,256}, got Dqk=%lld Dv=%lld", (long long)Dqk,
                 (long long)Dv);
   if (!(sm_scale > 0.f)) return fail(DMAD_ERR_UNSUPPORTED, "sm_scale must be positive");
-  if (B == 0 || H == 0 || Lq == 0) return ok();
+  if (mg != nullptr && mode == DMAD_FWD_PLAIN)
+    return fail(DMAD_ERR_UNSUPPORTED, "the block-sparse forward has JVP modes only");
+  if (B == 0 || H == 0 || Lq == 0 || (mg != nullptr && mg->T == 0)) return ok();
   if (Lk == 0) return fail(DMAD_ERR_INVALID, "Lk must be at least 1");
   if (B * H > ((int64_t)1 << 24) || Lq >= ((int64_t)1 << 26) || Lk >= ((int64_t)1 << 26))
     return fail(DMAD_ERR_UNSUPPORTED, "sizes too large");
@@ -256,7 +272,7 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
   const int64_t dvp = Dv < 32 ? 32 : Dv, lkp = round_up(Lk, kLkAlign);
   if (dvp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "Lk too large");
 
-  dmad::FwdLaunchFn fn = pick_fwd(dtype, Dqk, Dv, mode);
+  dmad::FwdLaunchFn fn = mg ? pick_fwd_magi(dtype, Dqk, Dv, mode) : pick_fwd(dtype, Dqk, Dv, mode);
   if (fn == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no kernel for Dqk=%lld Dv=%lld", (long long)Dqk, (long long)Dv);
 
   hipStream_t s = (hipStream_t)stream;
@@ -310,13 +326,78 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
   p.LKP = (int)lkp;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
-  const int64_t nqt = (Lq + 127) / 128;
-  if (nqt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  int64_t units = (Lq + 127) / 128;  // 128-query tiles (dense) or tasks (block-sparse)
+  if (mg != nullptr) {
+    p.q_ranges = mg->q_ranges;
+    p.k_ranges = mg->k_ranges;
+    p.qk_map = mg->qk_map;
+    p.task_group = mg->task_group;
+    p.task_qtile = mg->task_qtile;
+    p.G = (int)mg->G;
+    p.R = (int)mg->R;
+    p.T = (int)mg->T;
+    units = mg->T;
+  }
+  if (units * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
   mark(0, false, s);
-  e = fn(p, (int)(nqt * BH), s);
+  e = fn(p, (int)(units * BH), s);
   mark(0, true, s);
   if (e != hipSuccess) return fail(DMAD_ERR_HIP, "attention launch: %s", hipGetErrorString(e));
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int dmad_abi_version(void) { return 1; }
+
+const char* dmad_last_error(void) { return g_last_error.c_str(); }
+
+int dmad_set_kernel_events(void* const* events, int count) {
+  if (count < 0 || count > kMaxEvents || (count % 2) != 0)
+    return fail(DMAD_ERR_INVALID, "count must be an even number in [0, %d]", kMaxEvents);
+  if (count > 0 && events == nullptr) return fail(DMAD_ERR_INVALID, "events: null pointer");
+  for (int i = 0; i < count; ++i) g_events[i] = (hipEvent_t)events[i];
+  g_nevents = count;
+  return ok();
+}
+
+int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dv, size_t* bytes) {
+  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
+  if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
+  if (B < 0 || H < 0 || Lk < 0 || !head_dim_ok(Dv)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  *bytes = (size_t)fwd_ws_bytes(mode, B, H, Lk, Dv);
+  return ok();
+}
+
+int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
+                      const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4], void* o,
+                      void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  return fwd_impl(dtype, mode, B, H, Lq, Lk, Dqk, Dv, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to,
+                  o_strides, lse, mu, sm_scale, workspace, workspace_bytes, stream, nullptr);
+}
+
+int dmad_attn_jvp_fwd_magi(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
+                           const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                           const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                           void* o, void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale,
+                           const int32_t* q_ranges, const int32_t* k_ranges, const int32_t* qk_map, int64_t G,
+                           int64_t R, const int32_t* task_group, const int32_t* task_qtile, int64_t T,
+                           int64_t block_m, void* workspace, size_t workspace_bytes, void* stream) {
+  if (block_m != dmad::kMagiBlockM)
+    return fail(DMAD_ERR_UNSUPPORTED, "tasks must be built for %d-query tiles, got BLOCK_M=%lld", dmad::kMagiBlockM,
+                (long long)block_m);
+  if (G < 1 || R < 0 || T < 0 || G >= ((int64_t)1 << 30) || R >= ((int64_t)1 << 30) || T >= ((int64_t)1 << 30))
+    return fail(DMAD_ERR_INVALID, "bad table sizes G=%lld R=%lld T=%lld", (long long)G, (long long)R, (long long)T);
+  if (q_ranges == nullptr || qk_map == nullptr || (R > 0 && k_ranges == nullptr) ||
+      (T > 0 && (task_group == nullptr || task_qtile == nullptr)))
+    return fail(DMAD_ERR_INVALID, "block-sparse tables: null pointer");
+  const MagiArgs mg{q_ranges, k_ranges, qk_map, task_group, task_qtile, G, R, T};
+  return fwd_impl(dtype, mode, B, H, Lq, Lk, Dqk, Dv, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to,
+                  o_strides, lse, mu, sm_scale, workspace, workspace_bytes, stream, &mg);
 }
 
 int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv, const void* q,

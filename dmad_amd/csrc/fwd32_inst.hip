@@ -15,10 +15,27 @@ using Elt = __bf16;
 using Elt = _Float16;
 #endif
 
+static_assert(Fwd32Cfg<kFwdJvp>::BM == kMagiBlockM, "block-sparse tasks are 128-query tiles");
+
 template <typename T, int MODE>
 static hipError_t fwd32_launch(const FwdParams& p, int grid, hipStream_t s) {
   hipLaunchKernelGGL((attn_fwd32_kernel<T, MODE>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
+}
+
+template <typename T, int MODE>
+static hipError_t fwd32_magi_launch(const FwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_fwd32_kernel<T, MODE, true>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <>
+FwdLaunchFn fwd32_magi_select<Elt>(int mode) {
+  switch (mode) {
+    case kFwdJvp: return &fwd32_magi_launch<Elt, kFwdJvp>;
+    case kFwdJvpQOnly: return &fwd32_magi_launch<Elt, kFwdJvpQOnly>;
+    default: return nullptr;
+  }
 }
 
 template <>

@@ -17,6 +17,8 @@ using Elt = __bf16;
 using Elt = _Float16;
 #endif
 
+static_assert(FwdSimpleCfg<DMAD_D, 16, kFwdJvp>::BM == kMagiBlockM, "block-sparse tasks are 128-query tiles");
+
 template <typename T, int DQK, int DV, int MODE>
 static hipError_t fwd_launch(const FwdParams& p, int grid, hipStream_t s) {
   if constexpr (FwdStreamCfg<DQK, DV, MODE>::OK)
@@ -34,6 +36,35 @@ static FwdLaunchFn fwd_mode(int mode) {
     case kFwdPlain: return &fwd_launch<T, DQK, DV, kFwdPlain>;
     case kFwdJvp: return &fwd_launch<T, DQK, DV, kFwdJvp>;
     case kFwdJvpQOnly: return &fwd_launch<T, DQK, DV, kFwdJvpQOnly>;
+    default: return nullptr;
+  }
+}
+
+template <typename T, int DQK, int DV, int MODE>
+static hipError_t fwd_magi_launch(const FwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_fwd_simple_kernel<T, DQK, DV, MODE, true>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, int DQK, int DV>
+static FwdLaunchFn fwd_magi_mode(int mode) {
+  switch (mode) {
+    case kFwdJvp: return &fwd_magi_launch<T, DQK, DV, kFwdJvp>;
+    case kFwdJvpQOnly: return &fwd_magi_launch<T, DQK, DV, kFwdJvpQOnly>;
+    default: return nullptr;
+  }
+}
+
+template <>
+FwdLaunchFn fwd_magi_select<Elt, DMAD_D>(int dv, int mode) {
+  switch (dv) {
+    case 16: return fwd_magi_mode<Elt, DMAD_D, 16>(mode);
+    case 32: return fwd_magi_mode<Elt, DMAD_D, 32>(mode);
+    case 64: return fwd_magi_mode<Elt, DMAD_D, 64>(mode);
+    case 128:
+      if constexpr (fwd32_supported(DMAD_D, 128)) return fwd32_magi_select<Elt>(mode);
+      else return fwd_magi_mode<Elt, DMAD_D, 128>(mode);
+    case 256: return fwd_magi_mode<Elt, DMAD_D, 256>(mode);
     default: return nullptr;
   }
 }

@@ -22,6 +22,17 @@ FwdLaunchFn fwd32_select(int mode);
 template <> FwdLaunchFn fwd32_select<__bf16>(int);
 template <> FwdLaunchFn fwd32_select<_Float16>(int);
 
+// Block-sparse (MagiMask) forward launchers, JVP modes only; the grid is
+// tasks * B * H workgroups of 256 threads, each task a 128-query tile.
+template <typename T, int DQK>
+FwdLaunchFn fwd_magi_select(int dv, int mode);
+template <typename T>
+FwdLaunchFn fwd32_magi_select(int mode);
+template <> FwdLaunchFn fwd32_magi_select<__bf16>(int);
+template <> FwdLaunchFn fwd32_magi_select<_Float16>(int);
+// Query rows per task of the block-sparse kernels.
+constexpr int kMagiBlockM = 128;
+
 typedef hipError_t (*BwdLaunchFn)(const BwdParams&, int grid, hipStream_t);
 
 // Launcher for attn_bwd_kernel<T, D, MODE>, or nullptr if unsupported.

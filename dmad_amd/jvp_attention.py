@@ -20,7 +20,10 @@ Differences from the reference, all additive:
     tangents, :579). Without it the gradients are the reference's dO-only
     ones. ``set_reference_backward(True)`` restores the reference behaviour
     exactly in both cases.
-  * ``magi_mask`` (block-sparse masks, :504-531) raises NotImplementedError.
+  * ``magi_mask`` (block-sparse masks, :502-531) runs the block-sparse kernel
+    as the reference does (forward only: RuntimeError when q, k or v require
+    grad, :504-505, and likewise when a tangent does). Masks built with any
+    BLOCK_M are accepted (``dmad_amd.magimask.tasks_for_kernel``).
 """
 from __future__ import annotations
 
@@ -115,6 +118,61 @@ def jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale, need_mu=True):
     return o, to, lse, mu
 
 
+def jvp_attention_forward_magi(q, k, v, tq, tk, tv, sm_scale, magi_mask):
+    """Launch the block-sparse forward+JVP kernel; returns (o, to, lse, mu).
+
+    Rows that no task of the mask covers are left as allocated (uninitialised),
+    as in the reference. ``tk is None and tv is None`` skips their GEMMs.
+    """
+    from . import magimask as mm
+
+    B, H, Lq, Dqk = q.shape
+    Lk, Dv = v.shape[-2], v.shape[-1]
+    _check_device(q, k, v, tq, tk, tv)
+    if tq is None:
+        raise ValueError("the block-sparse forward needs the query tangent tq")
+    code = nat.dtype_code(q.dtype)
+    if tk is None and tv is None:
+        mode = nat.DMAD_FWD_JVP_KV_TANGENT_ZERO
+    else:
+        if tk is None:
+            tk = torch.zeros_like(k)
+        if tv is None:
+            tv = torch.zeros_like(v)
+        mode = nat.DMAD_FWD_JVP
+    q, tq = _pair(q, tq)
+    k, tk = _pair(k, tk)
+    v, tv = _pair(v, tv)
+    dev = q.device
+    q_unique = mm.as_int32(magi_mask.q_unique, dev)
+    k_flat = mm.as_int32(magi_mask.k_flat, dev)
+    qk_map = mm.as_int32(magi_mask.qk_map, dev)
+    G, R = q_unique.numel() // 2, k_flat.numel() // 2
+    if qk_map.numel() != G + 1:
+        raise ValueError(f"qk_map has {qk_map.numel()} entries for {G} query groups (expected {G + 1})")
+    task_group, task_qtile, T = mm.tasks_for_kernel(magi_mask, Lq, dev)
+    o = torch.empty((B, H, Lq, Dv), device=dev, dtype=q.dtype)
+    to = torch.empty_like(o)
+    lse = torch.empty((B, H, Lq), device=dev, dtype=torch.float32)
+    mu = torch.empty_like(lse)
+    lib = nat.lib()
+    ws_bytes = nat.ctypes.c_size_t(0)
+    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dv, nat.ctypes.byref(ws_bytes)))
+    ws = torch.empty(max(int(ws_bytes.value), 1), device=dev, dtype=torch.uint8)
+    nat.check(
+        lib.dmad_attn_jvp_fwd_magi(
+            code, mode, B, H, Lq, Lk, Dqk, Dv,
+            nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(tq), nat.ptr(tk), nat.ptr(tv),
+            nat.strides4(q), nat.strides4(k), nat.strides4(v),
+            nat.ptr(o), nat.ptr(to), nat.strides4(o), nat.ptr(lse), nat.ptr(mu), float(sm_scale),
+            nat.ptr(q_unique), nat.ptr(k_flat), nat.ptr(qk_map), G, R,
+            nat.ptr(task_group), nat.ptr(task_qtile), T, mm.KERNEL_BLOCK_M,
+            nat.ptr(ws), ws.numel(), nat.stream_ptr(dev),
+        )
+    )
+    return o, to, lse, mu
+
+
 def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_scale, want_tangent_grads):
     """Launch the backward kernels; returns (dq, dk, dv, dtq, dtk, dtv)."""
     B, H, Lq, D = q.shape
@@ -195,9 +253,10 @@ class _attention(torch.autograd.Function):
         if sm_scale is None:
             sm_scale = HEAD_DIM_QK ** (-0.5)
         if magi_mask is not None:
-            if is_grad:
+            if is_grad or any(x is not None and x.requires_grad for x in (tq, tk, tv)):
                 raise RuntimeError("Backward with MagiMask is not supported.")
-            raise NotImplementedError("block-sparse (MagiMask) JVP attention is not implemented by dmad_amd")
+            o, to, _, _ = jvp_attention_forward_magi(q, k, v, tq, tk, tv, sm_scale, magi_mask)
+            return o, to
         tangent_grad = any(x is not None and x.requires_grad for x in (tq, tk, tv))
         # an output that does not reach the loss arrives in backward as None
         # (not zeros), so an unused `to` keeps the dO-only kernel

@@ -69,6 +69,34 @@ int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int
                       size_t workspace_bytes, void* stream);
 
 /*
+ * Block-sparse forward (+JVP): replaces the `_attn_fwd_magi` launch of
+ * _attention.forward with a MagiMask (flash_attention_jvp_triton.py:502-531,
+ * kernel :242-409). The tables are the MagiMask fields
+ * (train/wan/rcm/utils/magimask.py:240-283), int32 in device memory:
+ *   q_ranges [G][2]  query range [q0, q1) of group g
+ *   k_ranges [R][2]  key ranges; group g uses k_ranges[qk_map[g] .. qk_map[g+1])
+ *   qk_map   [G+1]
+ *   task_group, task_qtile [T]  one task per (group, 128-query tile) that
+ *                    intersect; the tiles are block_m = 128 rows (the
+ *                    reference's BLOCK_M; other values are DMAD_ERR_UNSUPPORTED)
+ * Query row i of a task's tile attends to the keys of its group's ranges and
+ * is stored only if it lies in the group's query range; rows no task covers
+ * are left untouched (the reference allocates o, to, lse uninitialised). A
+ * group without keys in [0, Lk) gets o = to = 0, lse = -inf, mu = 0. Ranges
+ * are clipped to the sequences and table indices to the tables, so malformed
+ * tables cannot read outside them. mode: DMAD_FWD_JVP or
+ * DMAD_FWD_JVP_KV_TANGENT_ZERO (the reference has no plain masked forward).
+ * Workspace as dmad_attn_fwd_workspace_bytes.
+ */
+int dmad_attn_jvp_fwd_magi(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
+                           const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                           const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                           void* o, void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale,
+                           const int32_t* q_ranges, const int32_t* k_ranges, const int32_t* qk_map, int64_t G,
+                           int64_t R, const int32_t* task_group, const int32_t* task_qtile, int64_t T,
+                           int64_t block_m, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Plain forward (O and LSE), the attention used by the non-JVP Wan forward
  * (train/wan/rcm/utils/jvp_helper.py:305-308 and rcm/utils/attention.py:120-167).
  */

@@ -141,3 +141,45 @@ def test_prologue_rejects_bad_arguments(nat, over, code, needle):
 
 def test_prologue_empty_is_a_no_op(nat):
     assert _pro(nat, rows=0) == 0
+
+
+def _magi(nat, **over):
+    a = dict(dtype=0, mode=1, B=1, H=2, Lq=64, Lk=64, Dqk=128, Dv=128, q=256, k=256, v=256, tq=256, tk=256,
+             tv=256, qs=_strides(16384, 8192, 128, 1), ks=_strides(16384, 8192, 128, 1),
+             vs=_strides(16384, 8192, 128, 1), o=256, to=256, os=_strides(16384, 8192, 128, 1), lse=256, mu=256,
+             scale=0.125, qr=256, kr=256, qm=256, G=1, R=1, tg=256, tq_=256, T=1, bm=128, ws=256, wsb=1 << 30,
+             stream=0)
+    a.update(over)
+    P = ctypes.c_void_p
+    return nat.lib().dmad_attn_jvp_fwd_magi(
+        a["dtype"], a["mode"], a["B"], a["H"], a["Lq"], a["Lk"], a["Dqk"], a["Dv"],
+        P(a["q"]), P(a["k"]), P(a["v"]), P(a["tq"]), P(a["tk"]), P(a["tv"]), a["qs"], a["ks"], a["vs"],
+        P(a["o"]), P(a["to"]), a["os"], P(a["lse"]), P(a["mu"]), a["scale"],
+        P(a["qr"]), P(a["kr"]), P(a["qm"]), a["G"], a["R"], P(a["tg"]), P(a["tq_"]), a["T"], a["bm"],
+        P(a["ws"]), a["wsb"], P(a["stream"]))
+
+
+@pytest.mark.parametrize(
+    "over,code,needle",
+    [
+        (dict(bm=64), 2, "128-query tiles"),
+        (dict(G=0), 1, "table sizes"),
+        (dict(T=-1), 1, "table sizes"),
+        (dict(qr=0), 1, "null"),
+        (dict(qm=0), 1, "null"),
+        (dict(kr=0), 1, "null"),
+        (dict(tg=0), 1, "null"),
+        (dict(mode=0), 2, "JVP modes"),
+        (dict(Dqk=48), 2, "head dims"),
+        (dict(tk=0), 1, "tk: null"),
+        (dict(wsb=16, Dqk=64, Dv=64), 3, "workspace"),
+    ],
+)
+def test_magi_fwd_rejects_bad_arguments(nat, over, code, needle):
+    assert _magi(nat, **over) == code
+    assert needle in nat.lib().dmad_last_error().decode()
+
+
+def test_magi_fwd_without_tasks_is_a_no_op(nat):
+    assert _magi(nat, T=0, tg=0, tq_=0) == 0
+    assert _magi(nat, R=0, kr=0, T=0) == 0
