@@ -39,6 +39,8 @@ def _args():
     ap.add_argument("--full-bwd", action="store_true", help="also time the full-derivative backward (extra field)")
     ap.add_argument("--no-prologue", dest="prologue", action="store_false",
                     help="skip timing the fused RMSNorm+RoPE prologue (extra field)")
+    ap.add_argument("--no-magi", dest="magi", action="store_false",
+                    help="skip timing the block-sparse forward on the causal-student masks (extra field)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one elementwise kernel that reads and writes this many MiB "
                          "(a known-size reference for HBM byte counters under a profiler)")
@@ -127,6 +129,55 @@ def prologue_timing(H, L, D, grid, dev):
     return {"kernel": "rmsnorm_rope_kernel<bf16,jvp,rope>", "ms_q_and_k": round(best, 4),
             "bytes_per_call": per_call, "achieved_GBps": round(gbs, 1), "hbm_peak_GBps": 8000.0,
             "frac": round(gbs / 8000.0, 4)}
+
+
+def magi_timing(H, D, dev):
+    """Block-sparse forward+JVP on two Wan2.1-14B causal-student masks (1560-token
+    frames, a 1-frame first block, 4-frame blocks, window of 3 blocks, 1 sink
+    block): block-causal streaming with 16 query frames over 21 key frames
+    (query block offset 2), and teacher forcing on the packed 2 x 21-frame
+    sequence. Flops count only the allowed (query, key) pairs."""
+    import torch
+
+    from dmad_amd import _native
+    from dmad_amd import magimask as mm
+    from dmad_amd.jvp_attention import jvp_attention_forward_magi
+
+    pat = mm.BlockPattern(frame_tokens=1560, first_chunk_frames=1, chunk_frames=4)
+    cases = {
+        "block_causal": (mm.AttnMaskSpec(mode="block_causal", pattern=pat, q_block_offset=2, local_attn_blocks=3,
+                                         sink_blocks=1), 1560 * 16, 1560 * 21),
+        "teacher_forcing": (mm.AttnMaskSpec(mode="teacher_forcing", pattern=pat, clean_blocks=6,
+                                            local_attn_blocks=3, sink_blocks=1), 1560 * 42, 1560 * 42),
+    }
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(5)
+    for name, (spec, Q, KV) in cases.items():
+        qr, kr = mm.make_magi_ranges_full(spec, Q_real=Q, KV_real=KV, device=dev)
+        mask = mm.prepare_magi_csr_and_tasks(qr, kr, Q_real=Q, KV_real=KV)
+        qu, kf, qm = mask.q_unique.cpu().tolist(), mask.k_flat.cpu().tolist(), mask.qk_map.cpu().tolist()
+        pairs = sum((qu[i][1] - qu[i][0]) * sum(kf[r][1] - kf[r][0] for r in range(qm[i], qm[i + 1]))
+                    for i in range(len(qu)))
+        r = lambda L: torch.randn(1, L, H, D, generator=g, device=dev).to(torch.bfloat16).transpose(1, 2)  # noqa: E731
+        q, tq, k, tk, v, tv = r(Q), r(Q), r(KV), r(KV), r(KV), r(KV)
+        for _ in range(2):
+            jvp_attention_forward_magi(q, k, v, tq, tk, tv, D ** -0.5, mask)
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            t = _native.KernelTimer(1)
+            with t:
+                jvp_attention_forward_magi(q, k, v, tq, tk, tv, D ** -0.5, mask)
+            torch.cuda.synchronize()
+            best = min(best, t.elapsed()[0])
+        flops = 12.0 * H * D * pairs
+        tfs = flops / (best * 1e-3) / 1e12
+        res[name] = {"Q": Q, "KV": KV, "density": round(pairs / (Q * KV), 4), "tasks": mask.T,
+                     "ms": round(best, 3), "TFLOPs": round(tfs, 1),
+                     "pct_peak": round(100 * tfs / PEAK_BF16_TFLOPS, 2)}
+        del q, tq, k, tk, v, tv
+    res["kernel"] = "attn_fwd32_kernel<bf16,jvp,magi>"
+    return res
 
 
 def main():
@@ -254,6 +305,8 @@ def main():
     # timed after the step (HBM-bound; not part of the step or its flops)
     if args.prologue:
         out["prologue_rmsnorm_rope_jvp"] = prologue_timing(H, L, D, grid, dev)
+    if args.magi:
+        out["magi_fwd_jvp"] = magi_timing(H, D, dev)
     if args.calibration_copy_mib:
         n = args.calibration_copy_mib * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)
