@@ -875,9 +875,13 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
                    float (&dsv)[2]) {
     const int qb = v / 16, t = (v % 16) / 8, e = v % 8;
     const float l2 = sv.l[e >> 2][e & 3], dl = sv.d[e >> 2][e & 3];
-    const float pe = fast_exp2(fmaf(sc[qb][8 * t + e], p.scale_log2, -l2));
+    // re-define the inputs here (an empty asm) so the compiler cannot hoist the
+    // value's arithmetic out of its MFMA slot and bunch the VALU work together
+    float s_in = sc[qb][8 * t + e], d_in = dpc[qb][8 * t + e];
+    asm volatile("" : "+v"(s_in), "+v"(d_in));
+    const float pe = fast_exp2(fmaf(s_in, p.scale_log2, -l2));
     pv[v & 1] = pe;
-    dsv[v & 1] = pe * (dpc[qb][8 * t + e] - dl);
+    dsv[v & 1] = pe * (d_in - dl);
   };
   auto pack = [&](int v, const float (&pv)[2], const float (&dsv)[2], i32x4_t (&pb)[2 * NQB],
                   i32x4_t (&dsb)[2 * NQB]) {
@@ -925,7 +929,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
         if (3 * v / 2 == m) {
           if (v % 8 == 0 && v + 8 < NVAL) load_stats(s_cur, v / 8 + 1, sv[(v / 8 + 1) & 1]);
           value(v, sc, dpc, sv[(v / 8) & 1], pv, dsv);
-          if (v & 1) pack(v, pv, dsv, pb, dsb);
+          if (v & 1) {
+            pack(v, pv, dsv, pb, dsb);
+            asm volatile("" : "+v"(pb[v / 8][(v % 8) >> 1]), "+v"(dsb[v / 8][(v % 8) >> 1]));
+          }
         }
       }
 #pragma unroll
