@@ -27,6 +27,45 @@ PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 flop/clk/CU
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
+# Board power / clock sampler, run as a separate process started before this
+# process touches the GPU (amd-smi reads the driver, not HIP).
+_SAMPLER = r'''
+import re, subprocess, sys, time
+out = open(sys.argv[1], "w", buffering=1)
+while True:
+    t = time.time()
+    try:
+        txt = subprocess.run(["amd-smi", "metric", "-p", "-c"], capture_output=True, text=True, timeout=5).stdout
+    except Exception:
+        txt = ""
+    pw = re.search(r"SOCKET_POWER: (\d+)", txt)
+    clk = [int(c) for c in re.findall(r"GFX_\d+:\s*\n\s*CLK: (\d+) MHz", txt)]
+    if pw and clk:
+        out.write(f"{t:.3f} {pw.group(1)} {sum(clk) / len(clk):.0f}\n")
+    time.sleep(0.05)
+'''
+
+
+def _start_power_sampler(path):
+    import subprocess
+
+    return subprocess.Popen([sys.executable, "-c", _SAMPLER, path], stdout=subprocess.DEVNULL,
+                            stderr=subprocess.DEVNULL)
+
+
+def _power_summary(path, t0, t1):
+    rows = []
+    for line in open(path):
+        t, w, c = line.split()
+        if t0 <= float(t) <= t1:
+            rows.append((float(w), float(c)))
+    if not rows:
+        return {"samples": 0}
+    return {"samples": len(rows), "avg_W": round(sum(r[0] for r in rows) / len(rows), 1),
+            "max_W": max(r[0] for r in rows), "avg_gfx_MHz": round(sum(r[1] for r in rows) / len(rows)),
+            "source": "amd-smi metric -p -c (SOCKET_POWER, mean GFX CLK over the XCDs) during the timed steps"}
+
+
 def _args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -39,6 +78,8 @@ def _args():
     ap.add_argument("--full-bwd", action="store_true", help="also time the full-derivative backward (extra field)")
     ap.add_argument("--no-prologue", dest="prologue", action="store_false",
                     help="skip timing the fused RMSNorm+RoPE prologue (extra field)")
+    ap.add_argument("--power", action="store_true",
+                    help="sample board power and GFX clock with amd-smi during the timed steps (extra field)")
     ap.add_argument("--no-magi", dest="magi", action="store_false",
                     help="skip timing the block-sparse forward on the causal-student masks (extra field)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -188,6 +229,13 @@ def main():
               "(no collectives); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    sampler = None
+    if args.power:  # before any GPU use in this process
+        import tempfile
+
+        power_file = tempfile.NamedTemporaryFile(prefix="dmad_power_", suffix=".txt", delete=False).name
+        sampler = _start_power_sampler(power_file)
+
     import torch
 
     sys.path.insert(0, ROOT)
@@ -231,6 +279,7 @@ def main():
         step(False)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    w0 = time.time()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(args.steps):
@@ -238,6 +287,7 @@ def main():
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    w1 = time.time()
     ms_step = e0.elapsed_time(e1) / args.steps
     k_ms = {"fwd": 0.0, "bwd_dkdv": 0.0, "bwd_dq": 0.0}
     for tf, tb in timers:
@@ -290,6 +340,27 @@ def main():
         },
         "wall_s_timed": round(wall, 3),
     }
+    if sampler is not None:
+        # then each main pass alone for ~3 s, so each gets its own power/clock window
+        def phase(fn):
+            a = time.time()
+            while time.time() - a < 3.0:
+                for _ in range(4):
+                    fn()
+                torch.cuda.synchronize()
+            return a, time.time()
+
+        windows = {"step": (w0, w1)}
+        o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+        windows["fwd_jvp"] = phase(lambda: jvp_attention_forward(q, k, v, tq, tk, tv, s))
+        windows["bwd_dout_only"] = phase(
+            lambda: jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False))
+        time.sleep(0.3)
+        sampler.terminate()
+        sampler.wait()
+        # skip the first 0.5 s of each window: the clock settles after a change of load
+        out["power"] = {name: _power_summary(power_file, a + 0.5, b) for name, (a, b) in windows.items()}
+        os.unlink(power_file)
     if args.full_bwd:
         o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
         dto = x["dto"]
