@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
-  const int work = xcd_remap(blockIdx.x, nkt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nkt, kt = work - bh * nkt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
-  const int work = xcd_remap(blockIdx.x, nkt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nkt, kt = work - bh * nkt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
@@ -735,7 +735,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
-  const int work = xcd_remap(blockIdx.x, nkt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nkt, kt = work - bh * nkt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(DqParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_pipe_kernel(DqParams p) {
   const int col = lane & 15, grp = lane >> 4;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -555,7 +555,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int ntiles = (p.Lk + BN - 1) / BN;

@@ -236,7 +236,7 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
   const int col = lane & 15, grp = lane >> 4;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
   const int col = lane & 15, grp = lane >> 4;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+  const int work = blockIdx.x;  // head-major order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -927,7 +927,7 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
     cm.seek(p, BN);
   } else {
     const int nqt = (p.Lq + C::BM - 1) / C::BM;
-    const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+    const int work = blockIdx.x;  // head-major order (common.h)
     bh = work / nqt;
     qt = work - bh * nqt;
     ntiles = (p.Lk + BN - 1) / BN;

@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
     }
   } else {
     const int nqt = (p.Lq + C::BM - 1) / C::BM;
-    const int work = xcd_remap(blockIdx.x, nqt * p.B * p.H);
+    const int work = blockIdx.x;  // head-major order (common.h)
     bh = work / nqt;
     qt = work - bh * nqt;
     ntiles = (p.Lk + BN - 1) / BN;
