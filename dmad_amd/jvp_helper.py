@@ -6,14 +6,18 @@ Twins of train/wan/rcm/utils/jvp_helper.py:
     copy) and returns ``(o, o_dot.detach())`` in ``[B, S, H, D]``.
   * ``torch_attention_op`` (:305-308): plain attention in ``[B, S, H, D]``
     (the reference uses SDPA with its default scale D^-1/2).
+  * ``FlexOrSdpaLocalAttentionWithT`` (:213-269): the dense / block-sparse
+    dispatcher of the JVP students, with its per-shape MagiMask cache.
 """
 from __future__ import annotations
 
-from typing import Tuple
+from typing import Dict, Optional, Tuple
 
 import torch
+from torch import nn
 
 from .jvp_attention import _attention, plain_attention
+from .magimask import KERNEL_BLOCK_M, AttnMaskSpec, MagiMask, make_magi_ranges_full, prepare_magi_csr_and_tasks
 
 TensorWithT = Tuple[torch.Tensor, torch.Tensor]
 
@@ -39,3 +43,57 @@ def torch_attention_op_withT(q_B_S_H_D_withT: TensorWithT, k_B_S_H_D_withT: Tens
 def torch_attention_op(q_B_S_H_D, k_B_S_H_D, v_B_S_H_D):
     return plain_attention(q_B_S_H_D.transpose(1, 2), k_B_S_H_D.transpose(1, 2),
                            v_B_S_H_D.transpose(1, 2)).transpose(1, 2)
+
+
+def needs_block_mask(spec: Optional[AttnMaskSpec], Q: int, KV: int) -> bool:
+    """False when the spec reduces to dense attention (jvp_helper.py:251-263):
+    no mask, or a block-causal query block without sliding window whose keys all
+    lie in blocks <= its own."""
+    if spec is None or spec.mode == "none":
+        return False
+    if spec.mode == "block_causal" and int(spec.local_attn_blocks) == 0:
+        pat, q_blk = spec.pattern, int(spec.q_block_offset)
+        if Q == pat.get_block_tokens(q_blk) and KV <= pat.blocks_to_tokens(q_blk + 1):
+            return False
+    return True
+
+
+class FlexOrSdpaLocalAttentionWithT(nn.Module):
+    """Dense or block-sparse JVP attention on ``(x, x_dot)`` pairs in ``[B, S, H, D]``.
+
+    ``forward(q_withT, k_withT, v_withT, attn_meta=None)``: with no mask (or one
+    that covers every key, see ``needs_block_mask``) it calls the dense op;
+    otherwise it builds (once per spec and shape) the MagiMask of the spec with
+    the kernels' 128-query tiles and calls the block-sparse op. The block-sparse
+    op is forward only, as in the reference.
+    """
+
+    def __init__(self, attn_T=torch_attention_op_withT):
+        super().__init__()
+        self.attn_T = attn_T
+        self._cache: Dict[Tuple, MagiMask] = {}
+
+    def get_magi_mask(self, spec: AttnMaskSpec, Q_real: int, KV_real: int, device,
+                      BLOCK_M: int = KERNEL_BLOCK_M) -> MagiMask:
+        device = torch.device(device)
+        key = (spec.mode, spec.pattern, int(spec.local_attn_blocks), int(spec.sink_blocks), int(spec.q_block_offset),
+               int(spec.clean_blocks), int(Q_real), int(KV_real), int(BLOCK_M), device.type, device.index)
+        mask = self._cache.get(key)
+        if mask is None:
+            q_ranges, k_ranges = make_magi_ranges_full(spec, Q_real, KV_real, device)
+            mask = prepare_magi_csr_and_tasks(q_ranges, k_ranges, Q_real, KV_real, BLOCK_M)
+            self._cache[key] = mask
+        return mask
+
+    def clear_cache(self):
+        self._cache.clear()
+
+    def forward(self, q_withT, k_withT, v_withT, attn_meta: Optional[AttnMaskSpec] = None, **_ignored):
+        q, k, v = q_withT[0], k_withT[0], v_withT[0]
+        B, Q, H, D = q.shape
+        KV = k.shape[1]
+        assert k.shape == (B, KV, H, D) and v.shape == (B, KV, H, D)
+        if not needs_block_mask(attn_meta, Q, KV):
+            return self.attn_T(q_withT, k_withT, v_withT)
+        mask = self.get_magi_mask(attn_meta, Q_real=Q, KV_real=KV, device=q.device)
+        return self.attn_T(q_withT, k_withT, v_withT, mask)

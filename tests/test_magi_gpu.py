@@ -236,3 +236,24 @@ def test_wan_block_causal_full_width(gpu):
     idx = torch.tensor(rows)
     assert orc.rel_l2(o.cpu()[..., idx, :], ro) < 1e-2
     assert orc.rel_l2(to.cpu()[..., idx, :], rto) < 1e-2
+
+
+def test_dispatcher(gpu):
+    """FlexOrSdpaLocalAttentionWithT on BSHD pairs: no mask -> the dense op; a
+    block-causal spec -> the block-sparse op, equal to the oracle's masked JVP."""
+    from dmad_amd import FlexOrSdpaLocalAttentionWithT, torch_attention_op_withT
+
+    mod = FlexOrSdpaLocalAttentionWithT()
+    spec, Q, KV, allow = _spec("block_causal", 40, 4, chunk=2)
+    xs = _inputs(1, 2, Q, KV, 128, 128, torch.bfloat16, seed=17)
+    bshd = [x.to(gpu).transpose(1, 2) for x in xs]  # BSHD views, as the Wan callers pass
+    pairs = [(bshd[0], bshd[3]), (bshd[1], bshd[4]), (bshd[2], bshd[5])]
+    o_d, to_d = mod(*pairs)
+    o_r, to_r = torch_attention_op_withT(*pairs)
+    o_m, to_m = mod(*pairs, attn_meta=spec)
+    torch.cuda.synchronize()
+    assert torch.equal(o_d, o_r) and torch.equal(to_d, to_r)
+    ro, rto, _, _ = om.masked_jvp(*xs, allow, 128 ** -0.5)
+    assert orc.rel_l2(o_m.transpose(1, 2).cpu(), ro) < 1e-2
+    assert orc.rel_l2(to_m.transpose(1, 2).cpu(), rto) < 1e-2
+    assert not to_m.requires_grad

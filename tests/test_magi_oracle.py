@@ -221,3 +221,27 @@ def test_emulator_bf16_within_reference_tolerance():
     o, to, _, _ = om.masked_jvp(*xs, allow, 64 ** -0.5)
     torch.testing.assert_close(eo.to(torch.bfloat16).double(), o, atol=2e-2, rtol=1e-2)
     torch.testing.assert_close(eto.to(torch.bfloat16).double(), to, atol=2e-2, rtol=1e-2)
+
+
+def test_dispatcher_decision_and_cache():
+    """FlexOrSdpaLocalAttentionWithT's dense/masked decision (jvp_helper.py:251-263) and its mask cache."""
+    from dmad_amd.jvp_helper import FlexOrSdpaLocalAttentionWithT, needs_block_mask
+
+    pat = mm.BlockPattern(frame_tokens=16, first_chunk_frames=1, chunk_frames=2)
+    assert not needs_block_mask(None, 64, 64)
+    assert not needs_block_mask(mm.AttnMaskSpec(mode="none"), 64, 64)
+    # one query block (block 1 = 32 tokens) over keys of blocks 0..1 (48 tokens): dense
+    one = mm.AttnMaskSpec(mode="block_causal", pattern=pat, q_block_offset=1)
+    assert not needs_block_mask(one, 32, 48)
+    assert needs_block_mask(one, 32, 49) and needs_block_mask(one, 64, 48)
+    # a sliding window always needs the mask
+    assert needs_block_mask(mm.AttnMaskSpec(mode="block_causal", pattern=pat, q_block_offset=1, local_attn_blocks=1),
+                            32, 48)
+    assert needs_block_mask(mm.AttnMaskSpec(mode="teacher_forcing", pattern=pat, clean_blocks=2), 96, 96)
+    mod = FlexOrSdpaLocalAttentionWithT()
+    spec = mm.AttnMaskSpec(mode="block_causal", pattern=pat)
+    a = mod.get_magi_mask(spec, 80, 80, "cpu")
+    assert mod.get_magi_mask(spec, 80, 80, "cpu") is a and a.BLOCK_M == 128
+    assert mod.get_magi_mask(spec, 48, 48, "cpu") is not a
+    mod.clear_cache()
+    assert mod.get_magi_mask(spec, 80, 80, "cpu") is not a
