@@ -24,6 +24,9 @@ computes on this path:
   kernel's own error floor.
 * ``naive_attention_in_dtype`` -- the reference tests' oracle: matmul in the input
   dtype, softmax in fp32 cast back to the dtype (:596-605, :637-645).
+* ``fa2_bwd_emulator``        -- the numerics of the standard FA2 backward the reference
+  calls (P and dS rounded to the input type before the gradient products), used to
+  measure the reference backward's own error floor.
 
 How each function is pinned (tests/test_oracle.py):
   math_attention            brute-force loops on tiny inputs; LSE >= max S;
@@ -39,6 +42,8 @@ How each function is pinned (tests/test_oracle.py):
                             for every BLOCK_N; bf16 error within the reference
                             tests' tolerances.
   naive_attention_in_dtype  reduces to math_attention in float64.
+  fa2_bwd_emulator          equals grads_dout_only in float64 with no rounding;
+                            bf16 error within the reference tests' tolerances.
 Tensors are [B, H, L, D] (BHSD).
 """
 from __future__ import annotations
@@ -202,6 +207,35 @@ def triton_fwd_emulator(q, k, v, tq, tk, tv, sm_scale=None, block_n=64, round_dt
     to = a_i * inv_l[..., None] + b_i * inv_l[..., None] - mu[..., None] * o
     lse = (m_i + torch.log2(l_i)) * LN2
     return o, to, lse
+
+
+def fa2_bwd_emulator(q, k, v, do, sm_scale=None, round_dtype=torch.bfloat16):
+    """Numerics of the standard FlashAttention-2 backward the reference calls
+    (flash-attn, flash_attention_jvp_triton.py:540-578; the published FA2
+    backward: P recomputed from the forward's LSE, D = rowsum(dO * O) from the
+    stored O, dP = dO V^T and dS = P * (dP - D) in float32, P and dS rounded to
+    the input type before the dV = P^T dO, dK = s dS^T Q, dQ = s dS K products,
+    float32 accumulation). Inputs are the (already rounded) operands; returns
+    float32 (float64 for float64 inputs) dq, dk, dv before their final store
+    rounding. `round_dtype=None` rounds nothing, so float64 inputs give the
+    exact dO-only gradients.
+    """
+    f = torch.float64 if q.dtype == torch.float64 else torch.float32
+    q, k, v, do = (x.to(f) for x in (q, k, v, do))
+    s = _scale(q, sm_scale)
+    S = torch.matmul(q, k.transpose(-1, -2)) * s
+    lse = torch.logsumexp(S, dim=-1)
+    P = torch.exp(S - lse[..., None])
+    o = torch.matmul(_round(P, round_dtype), v)
+    o = _round(o, round_dtype)  # the forward stores O in the input type
+    Dr = (do * o).sum(-1)
+    dP = torch.matmul(do, v.transpose(-1, -2))
+    dS = P * (dP - Dr[..., None])
+    P_r, dS_r = _round(P, round_dtype), _round(dS, round_dtype)
+    dv = torch.matmul(P_r.transpose(-1, -2), do)
+    dk = s * torch.matmul(dS_r.transpose(-1, -2), q)
+    dq = s * torch.matmul(dS_r, k)
+    return dq, dk, dv
 
 
 def rel_l2(x, ref):

@@ -7,8 +7,10 @@ plus the tangent gradients) against oracle.grads_full, itself pinned against
 autograd through torch.func.jvp.
 
 Bar: relative L2 error <= 1e-2 on every gradient against the float64 oracle on
-the same rounded inputs, plus the reference tests' assert_close tolerances
-(atol 1e-2 / 2e-2, rtol 2e-2) against the in-dtype naive oracle.
+the same rounded inputs, no worse than 1.25x the reference backward's own error
+(oracle.fa2_bwd_emulator, the FA2 numerics it calls) + 1e-4 for the dO-only
+gradients, plus the reference tests' assert_close tolerances (atol 1e-2 / 2e-2,
+rtol 2e-2) against the in-dtype naive oracle.
 """
 import pytest
 import torch
@@ -60,8 +62,13 @@ def test_dout_only_backward(gpu, shape, dtype):
     q, k, v, _, _, _, do, _ = (x.double() for x in xs)
     rq, rk, rv = orc.grads_dout_only(q, k, v, do, 0.5)
     errs = [orc.rel_l2(a, b) for a, b in zip((dq, dk, dv), (rq, rk, rv))]
-    print("  rel-L2 dq %.2e dk %.2e dv %.2e" % tuple(errs))
+    # the reference backward's own error: FA2 numerics emulated on the same inputs
+    em = orc.fa2_bwd_emulator(xs[0], xs[1], xs[2], xs[6], 0.5, round_dtype=dtype)
+    floor = [orc.rel_l2(a.to(dtype), b) for a, b in zip(em, (rq, rk, rv))]
+    print("  rel-L2 dq %.2e dk %.2e dv %.2e" % tuple(errs), " FA2 floor dq %.2e dk %.2e dv %.2e" % tuple(floor))
     assert max(errs) <= 1e-2
+    for e, f in zip(errs, floor):
+        assert e <= 1.25 * f + 1e-4
     for a, b in zip((dq, dk, dv), (rq, rk, rv)):
         torch.testing.assert_close(a.double(), b, atol=2e-2, rtol=2e-2)
 

@@ -192,3 +192,25 @@ def test_rows_subset_matches_full():
     sub = orc.jvp_rows(*args, rows=rows, sm_scale=0.5)
     for x, y in zip(full, sub):
         assert torch.allclose(x[..., rows, :] if x.dim() == 4 else x[..., rows], y, atol=1e-13)
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 40, 40, 16), (2, 1, 33, 17, 32)])
+def test_fa2_bwd_emulator_exact_without_rounding(shape):
+    B, H, Lq, Lk, D = shape
+    g = torch.Generator().manual_seed(9)
+    q, k, v, do = (torch.randn(B, H, L, D, generator=g, dtype=torch.float64) for L in (Lq, Lk, Lk, Lq))
+    got = orc.fa2_bwd_emulator(q, k, v, do, 0.3, round_dtype=None)
+    ref = orc.grads_dout_only(q, k, v, do, 0.3)
+    for a, b in zip(got, ref):
+        assert torch.allclose(a, b, atol=1e-12, rtol=0)
+
+
+def test_fa2_bwd_emulator_bf16_within_reference_tolerance():
+    g = torch.Generator().manual_seed(20)
+    q, k, v, do = ((torch.randn(1, 2, 256, 64, generator=g, dtype=torch.float64) * sd).to(torch.bfloat16)
+                   for sd in (0.5, 0.5, 0.5, 1.0))
+    got = orc.fa2_bwd_emulator(q, k, v, do, 0.5)
+    ref = orc.grads_dout_only(*(x.double() for x in (q, k, v, do)), 0.5)
+    for a, b in zip(got, ref):
+        e = orc.rel_l2(a.to(torch.bfloat16), b)
+        assert 1e-4 < e < 1e-2  # rounding shows, and stays within the reference tests' bar
