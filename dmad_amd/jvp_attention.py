@@ -6,7 +6,8 @@ Reference: ``train/wan/rcm/utils/flash_attention_jvp_triton.py:450-582``.
 tangents ``(tq, tk, tv)``. Tensors are logical ``[B, H, L, D]`` with any
 strides (the Wan callers pass ``[B, L, H, D]`` storage viewed as BHSD).
 
-Device work is three hand-written HIP kernels reached through the C ABI of
+Device work is hand-written HIP (the forward+JVP kernel and its block-sparse
+variant, the dK/dV and dQ backward passes) reached through the C ABI of
 ``libdmad_attn.so`` (``include/dmad_attn.h``); this module only checks
 arguments, allocates outputs with the torch caching allocator and launches on
 torch's current stream. There is no CPU or PyTorch fallback.
