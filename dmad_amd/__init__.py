@@ -10,9 +10,17 @@ and the attention helpers of train/wan/rcm/utils/jvp_helper.py):
 * ``rmsnorm_rope_with_tangent``     -- fused RMSNorm(+JVP) and RoPE-with-tangent producing the op's q/k inputs
 * ``magimask``                      -- block-sparse mask tables (MagiMask) for ``attention(..., magi_mask)``
 * ``FlexOrSdpaLocalAttentionWithT`` -- dense / block-sparse dispatcher of the masked JVP students
+* ``MinimalA2AAttnOpWithT``, ``RopeCache`` -- RoPE-with-tangent then local attention (one-GPU branch)
+* ``apply_rope_with_tangent``       -- interleaved RoPE of a BSHD pair, differentiable
 """
 from .jvp_attention import _attention, attention, plain_attention, set_reference_backward  # noqa: F401
-from .jvp_helper import FlexOrSdpaLocalAttentionWithT, torch_attention_op, torch_attention_op_withT  # noqa: F401
-from .prologue import rmsnorm_rope_with_tangent  # noqa: F401
+from .jvp_helper import (  # noqa: F401
+    FlexOrSdpaLocalAttentionWithT,
+    MinimalA2AAttnOpWithT,
+    RopeCache,
+    torch_attention_op,
+    torch_attention_op_withT,
+)
+from .prologue import apply_rope_with_tangent, rmsnorm_rope_with_tangent  # noqa: F401
 from . import magimask  # noqa: F401
 from .magimask import MagiMask, prepare_magi_csr_and_tasks  # noqa: F401

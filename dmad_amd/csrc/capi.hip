@@ -635,7 +635,8 @@ int dmad_rmsnorm_rope_jvp(int dtype, int64_t rows, int64_t L, int64_t H, int64_t
   if ((ty == nullptr) != (tout == nullptr)) return fail(DMAD_ERR_INVALID, "ty and tout must be both set or both null");
   if (!(eps >= 0.f)) return fail(DMAD_ERR_INVALID, "eps must be non-negative");
   if (rows == 0) return ok();
-  if (y == nullptr || weight == nullptr || out == nullptr) return fail(DMAD_ERR_INVALID, "null pointer");
+  if (y == nullptr || out == nullptr) return fail(DMAD_ERR_INVALID, "null pointer");
+  if (weight == nullptr && freqs == nullptr) return fail(DMAD_ERR_INVALID, "weight and freqs are both null: nothing to do");
   for (const void* ptr : {y, ty, weight, (const void*)out, (const void*)tout})
     if (ptr != nullptr && ((uintptr_t)ptr & 15) != 0) return fail(DMAD_ERR_INVALID, "pointers must be 16-byte aligned");
   if (y_stride < C || out_stride < C || y_stride % 8 != 0 || out_stride % 8 != 0)

@@ -81,7 +81,7 @@ constexpr int kPrologueMaxChunks = 20;  // 16-byte chunks per lane: C <= 64 * 8 
 struct PrologueParams {
   const void* y;      // [rows, C] (row stride y_stride elements)
   const void* ty;     // tangent, same strides; null for the primal only
-  const void* w;      // [C] weight
+  const void* w;      // [C] weight; null skips the norm (rotation only)
   const float* freqs;  // [L, D/2] angles; null skips the rotation
   void* out;          // [rows, C] (row stride o_stride)
   void* tout;         // tangent output; null iff ty is null

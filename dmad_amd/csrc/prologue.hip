@@ -23,7 +23,9 @@
 
 namespace dmad {
 
-template <typename T, int MAXC, bool JVP, bool ROPE>
+// NORM = false (no weight): the rotation alone, RoPE-with-tangent of
+// train/wan/rcm/utils/rope.py:106-114 on its own.
+template <typename T, int MAXC, bool JVP, bool ROPE, bool NORM>
 __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -40,6 +42,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
     if (c < nch) {
       yv[j] = *(const i32x4_t*)(yrow + c * 16);
       if constexpr (JVP) tv[j] = *(const i32x4_t*)(tyrow + c * 16);
+      if constexpr (!NORM) continue;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t wy = (uint32_t)yv[j][e >> 1];
@@ -53,14 +56,17 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
       }
     }
   }
+  float r = 1.f, rd = 0.f;
+  if constexpr (NORM) {
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    s2 += __shfl_xor(s2, m);
-    if constexpr (JVP) sd += __shfl_xor(sd, m);
+    for (int m = 1; m < 64; m <<= 1) {
+      s2 += __shfl_xor(s2, m);
+      if constexpr (JVP) sd += __shfl_xor(sd, m);
+    }
+    const float mean = s2 * p.inv_c;
+    r = 1.0f / __builtin_sqrtf(mean + p.eps);
+    rd = -0.5f * (r * r * r) * (2.0f * sd * p.inv_c);
   }
-  const float mean = s2 * p.inv_c;
-  const float r = 1.0f / __builtin_sqrtf(mean + p.eps);
-  const float rd = -0.5f * (r * r * r) * (2.0f * sd * p.inv_c);
 
   // rotation angles of this lane's 4 pairs: i = 4 (lane mod D/8) + k
   float cs[4], sn[4];
@@ -78,17 +84,22 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
   for (int j = 0; j < MAXC; ++j) {
     const int c = lane + 64 * j;
     if (c >= nch) continue;
-    const i32x4_t wv = *(const i32x4_t*)((const char*)p.w + c * 16);
+    i32x4_t wv = {};
+    if constexpr (NORM) wv = *(const i32x4_t*)((const char*)p.w + c * 16);
     float q[8], tq[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int sh = (e & 1) ? 16 : 0;
       const float a = Elem<T>::to_f32((uint16_t)(((uint32_t)yv[j][e >> 1] >> sh) & 0xffff));
-      const float w = Elem<T>::to_f32((uint16_t)(((uint32_t)wv[e >> 1] >> sh) & 0xffff));
-      q[e] = Elem<T>::round(Elem<T>::round(__fmul_rn(a, r)) * w);
-      if constexpr (JVP) {
-        const float b = Elem<T>::to_f32((uint16_t)(((uint32_t)tv[j][e >> 1] >> sh) & 0xffff));
-        tq[e] = Elem<T>::round(Elem<T>::round(__fadd_rn(__fmul_rn(b, r), __fmul_rn(a, rd))) * w);
+      float b = 0.f;
+      if constexpr (JVP) b = Elem<T>::to_f32((uint16_t)(((uint32_t)tv[j][e >> 1] >> sh) & 0xffff));
+      if constexpr (NORM) {
+        const float w = Elem<T>::to_f32((uint16_t)(((uint32_t)wv[e >> 1] >> sh) & 0xffff));
+        q[e] = Elem<T>::round(Elem<T>::round(__fmul_rn(a, r)) * w);
+        if constexpr (JVP) tq[e] = Elem<T>::round(Elem<T>::round(__fadd_rn(__fmul_rn(b, r), __fmul_rn(a, rd))) * w);
+      } else {
+        q[e] = a;
+        tq[e] = b;
       }
     }
     if constexpr (ROPE) {
@@ -115,25 +126,30 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
   }
 }
 
-template <typename T, bool JVP, bool ROPE>
+template <typename T, bool JVP, bool ROPE, bool NORM>
 static hipError_t prologue_launch_t(const PrologueParams& p, hipStream_t s) {
   const unsigned grid = (unsigned)((p.rows + 3) / 4);
   if (p.C <= 64 * 8 * 4)
-    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 4, JVP, ROPE>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 4, JVP, ROPE, NORM>), dim3(grid), dim3(256), 0, s, p);
   else if (p.C <= 64 * 8 * 12)
-    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 12, JVP, ROPE>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 12, JVP, ROPE, NORM>), dim3(grid), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, kPrologueMaxChunks, JVP, ROPE>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, kPrologueMaxChunks, JVP, ROPE, NORM>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
+}
+
+template <typename T, bool NORM>
+static hipError_t prologue_launch_n(const PrologueParams& p, hipStream_t s) {
+  const bool jvp = p.ty != nullptr, rope = p.freqs != nullptr;
+  if (jvp && rope) return prologue_launch_t<T, true, true, NORM>(p, s);
+  if (jvp) return prologue_launch_t<T, true, false, NORM>(p, s);
+  if (rope) return prologue_launch_t<T, false, true, NORM>(p, s);
+  return prologue_launch_t<T, false, false, NORM>(p, s);
 }
 
 template <typename T>
 static hipError_t prologue_launch_d(const PrologueParams& p, hipStream_t s) {
-  const bool jvp = p.ty != nullptr, rope = p.freqs != nullptr;
-  if (jvp && rope) return prologue_launch_t<T, true, true>(p, s);
-  if (jvp) return prologue_launch_t<T, true, false>(p, s);
-  if (rope) return prologue_launch_t<T, false, true>(p, s);
-  return prologue_launch_t<T, false, false>(p, s);
+  return p.w != nullptr ? prologue_launch_n<T, true>(p, s) : prologue_launch_n<T, false>(p, s);
 }
 
 hipError_t launch_rmsnorm_rope(const PrologueParams& p, int dtype, hipStream_t s) {

@@ -8,15 +8,19 @@ Twins of train/wan/rcm/utils/jvp_helper.py:
     (the reference uses SDPA with its default scale D^-1/2).
   * ``FlexOrSdpaLocalAttentionWithT`` (:213-269): the dense / block-sparse
     dispatcher of the JVP students, with its per-shape MagiMask cache.
+  * ``MinimalA2AAttnOpWithT`` (:125-210): RoPE with tangent on q and k, then the
+    local attention; the one-GPU branch (no all-to-all, no KV cache).
 """
 from __future__ import annotations
 
-from typing import Dict, Optional, Tuple
+from dataclasses import dataclass
+from typing import Any, Dict, Optional, Tuple
 
 import torch
 from torch import nn
 
 from .jvp_attention import _attention, plain_attention
+from .prologue import apply_rope_with_tangent
 from .magimask import KERNEL_BLOCK_M, AttnMaskSpec, MagiMask, make_magi_ranges_full, prepare_magi_csr_and_tasks
 
 TensorWithT = Tuple[torch.Tensor, torch.Tensor]
@@ -97,3 +101,64 @@ class FlexOrSdpaLocalAttentionWithT(nn.Module):
             return self.attn_T(q_withT, k_withT, v_withT)
         mask = self.get_magi_mask(attn_meta, Q_real=Q, KV_real=KV, device=q.device)
         return self.attn_T(q_withT, k_withT, v_withT, mask)
+
+
+@dataclass
+class RopeCache:
+    """Per-layer RoPE angles (train/wan/rcm/utils/rope.py:13-32): ``query_freqs`` and
+    ``key_freqs`` [S, D/2]; with ``cached_k_rotated`` the keys arrive rotated except
+    the current block's, rotated by ``current_key_freqs``."""
+
+    query_freqs: Optional[torch.Tensor] = None
+    key_freqs: Optional[torch.Tensor] = None
+    current_key_freqs: Optional[torch.Tensor] = None
+    use_fused: bool = True
+    cached_k_rotated: bool = True
+
+
+def _rotate(x_withT, freqs):
+    x, tx = x_withT
+    x, tx = apply_rope_with_tangent(x, tx, freqs)
+    return x, (None if tx is None else tx.detach())
+
+
+class MinimalA2AAttnOpWithT(nn.Module):
+    """RoPE with tangent, then local JVP attention, on BSHD ``(x, x_dot)`` pairs
+    (train/wan/rcm/utils/jvp_helper.py:125-210, one-GPU branch).
+
+    ``forward(q_withT, k_withT, v_withT, *args, attn_ctx=None, **kwargs)``:
+    ``attn_ctx.rope`` (a ``RopeCache``) gives the angles, applied as the
+    reference does (:176-196): the current key block first when the cached keys
+    are already rotated, then the query, and the whole key otherwise; rotated
+    tangents are detached. The remaining arguments go to ``local_attn_T``
+    (``FlexOrSdpaLocalAttentionWithT`` takes ``attn_meta``). Context parallelism
+    (a process group of more than one rank) and the KV cache of streaming
+    inference are not part of this one-GPU build and raise.
+    """
+
+    def __init__(self, local_attn_T=torch_attention_op_withT):
+        super().__init__()
+        self.local_attn_T = local_attn_T
+        self.pg = None
+        self.stream = None
+
+    def set_context_parallel_group(self, process_group, ranks, stream):
+        del ranks
+        self.pg = process_group
+        self.stream = stream
+
+    def forward(self, query_withT, key_withT, value_withT, *args: Any, attn_ctx=None, **kwargs):
+        if self.pg is not None and torch.distributed.get_world_size(self.pg) > 1:
+            raise NotImplementedError("context parallelism (all-to-all over several GPUs) is not part of this build")
+        cache = getattr(attn_ctx, "kv_cache", None) if attn_ctx is not None else None
+        mode = getattr(attn_ctx, "mode", None)
+        if cache is not None and getattr(mode, "name", mode) != "DISABLED":
+            raise NotImplementedError("the KV cache of streaming inference is not part of this build")
+        rope = attn_ctx.rope if attn_ctx is not None else None
+        if rope is not None and rope.cached_k_rotated and rope.current_key_freqs is not None:
+            key_withT = _rotate(key_withT, rope.current_key_freqs)
+        if rope is not None and rope.query_freqs is not None:
+            query_withT = _rotate(query_withT, rope.query_freqs)
+            if not rope.cached_k_rotated:
+                key_withT = _rotate(key_withT, rope.key_freqs)
+        return self.local_attn_T(query_withT, key_withT, value_withT, *args, **kwargs)

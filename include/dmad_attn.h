@@ -144,8 +144,10 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
  * the input type; rotation in float32, cast back).
  *   y, ty     : [rows, C] inputs (rows = B*L), row stride y_stride elements;
  *               ty == NULL computes the primal only (then tout must be NULL)
- *   weight    : [C] RMSNorm weight, same dtype
+ *   weight    : [C] RMSNorm weight, same dtype; NULL: no norm, the rotation
+ *               alone (apply_rope_with_tangent, rope.py:106-114, by itself)
  *   freqs     : [L, D/2] float32 angles, token l = row mod L; NULL: no rotation
+ *               (weight and freqs may not both be NULL)
  *   out, tout : [rows, C] = [B, L, H, D] outputs, row stride out_stride
  * D a multiple of 8 and <= 512, C = H*D <= 10240, pointers 16-byte aligned,
  * strides multiples of 8 and >= C, rows a multiple of L when freqs is given.

@@ -127,6 +127,7 @@ def _pro(nat, **over):
         (dict(H=100, D=128), 2, "exceeds"),
         (dict(tout=0), 1, "both"),
         (dict(y=0), 1, "null"),
+        (dict(w=0, freqs=0), 1, "nothing to do"),
         (dict(out=264), 1, "aligned"),
         (dict(ys=100), 1, "strides"),
         (dict(os=64), 1, "strides"),

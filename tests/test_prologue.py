@@ -149,3 +149,89 @@ def test_kernel_primal_only_and_no_rope(gpu):
     assert tq is None
     rq = orp.rmsnorm(y.cpu(), w.cpu(), 1e-6).view(2, 100, 3, 64)
     assert _bf16_ulp_ratio(q.cpu(), rq) <= 2.0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(1, 32760, 12, 128), (2, 300, 3, 64)])
+def test_rope_only_matches_oracle_and_backward(gpu, shape):
+    """apply_rope_with_tangent (the rotation alone, rope.py:106-114): outputs against the
+    oracle's apply_rope / its jvp, and the backward against autograd of the oracle."""
+    from dmad_amd import apply_rope_with_tangent
+
+    B, S, H, D = shape
+    g = torch.Generator(device=gpu).manual_seed(2)
+    x = torch.randn(B, S, H, D, generator=g, device=gpu).to(torch.bfloat16)
+    tx = (torch.randn(B, S, H, D, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    freqs = rope_freqs_3d(21, 30, 52, D, device=gpu) if S == 32760 else torch.rand(S, D // 2, generator=g, device=gpu) * 40
+    out, tout = apply_rope_with_tangent(x, tx, freqs)
+    torch.cuda.synchronize()
+    rows = slice(0, min(S, 4096))
+    rx, rtx, rf = x[:, rows].cpu(), tx[:, rows].cpu(), freqs[rows].cpu()
+    ro, rto = orp.rope_jvp(rx, rtx, rf)
+    for got, ref, name in ((out[:, rows].cpu(), ro, "out"), (tout[:, rows].cpu(), rto, "t_out")):
+        ulps = _bf16_ulp_ratio(got, ref)
+        print(f"  {name}: max {ulps:.2f} ulp")
+        assert ulps <= 2.0, name
+    # backward: rotation by -freqs, against autograd through the oracle's apply_rope
+    xs = x[:, rows].detach().clone().requires_grad_(True)
+    txs = tx[:, rows].detach().clone().requires_grad_(True)
+    o2, to2 = apply_rope_with_tangent(xs, txs, freqs[rows])
+    go = torch.randn_like(o2)
+    gto = torch.randn_like(to2)
+    ((o2.float() * go.float()).sum() + (to2.float() * gto.float()).sum()).backward()
+    torch.cuda.synchronize()
+    cx = rx.clone().requires_grad_(True)
+    orp.apply_rope(cx, rf).float().mul(go.cpu().float()).sum().backward()
+    ctx_ = rtx.clone().requires_grad_(True)
+    orp.apply_rope(ctx_, rf).float().mul(gto.cpu().float()).sum().backward()
+    for got, ref, name in ((xs.grad.cpu(), cx.grad, "grad x"), (txs.grad.cpu(), ctx_.grad, "grad t_x")):
+        ulps = _bf16_ulp_ratio(got, ref)
+        print(f"  {name}: max {ulps:.2f} ulp")
+        assert ulps <= 2.0, name
+
+
+@pytest.mark.gpu
+def test_fused_prologue_refuses_gradients(gpu):
+    from dmad_amd import rmsnorm_rope_with_tangent
+
+    y = torch.randn(1, 8, 128, device=gpu, dtype=torch.bfloat16, requires_grad=True)
+    w = torch.ones(128, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no backward"):
+        rmsnorm_rope_with_tangent((y, None), w, 1e-6, None, 1)
+    with torch.no_grad():
+        rmsnorm_rope_with_tangent((y, None), w, 1e-6, None, 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cached_k_rotated", [False, True])
+def test_a2a_op_one_gpu_with_rope(gpu, cached_k_rotated):
+    """MinimalA2AAttnOpWithT (jvp_helper.py:125-210, one GPU): RoPE with tangent on q
+    (and k), then the JVP attention, against the oracle's rope_jvp followed by the
+    attention closed form."""
+    from types import SimpleNamespace
+
+    from dmad_amd import MinimalA2AAttnOpWithT, RopeCache
+    from oracle import attention as orc
+
+    B, S, H, D = 1, 700, 2, 128
+    g = torch.Generator(device=gpu).manual_seed(3)
+    r = lambda sd: (torch.randn(B, S, H, D, generator=g, device=gpu) * sd).to(torch.bfloat16)  # noqa: E731
+    q, k, v, tq, tk, tv = r(1.0), r(1.0), r(1.0), r(0.1), r(0.1), r(0.1)
+    fq = torch.rand(S, D // 2, generator=g, device=gpu) * 30
+    fk = torch.rand(S, D // 2, generator=g, device=gpu) * 30
+    if cached_k_rotated:
+        rope = RopeCache(query_freqs=fq, current_key_freqs=fk, cached_k_rotated=True)
+    else:
+        rope = RopeCache(query_freqs=fq, key_freqs=fk, cached_k_rotated=False)
+    op = MinimalA2AAttnOpWithT()
+    with torch.no_grad():
+        o, to = op((q, tq), (k, tk), (v, tv), attn_ctx=SimpleNamespace(rope=rope, kv_cache=None))
+    torch.cuda.synchronize()
+    qr, tqr = orp.rope_jvp(q.cpu(), tq.cpu(), fq.cpu())
+    kr, tkr = orp.rope_jvp(k.cpu(), tk.cpu(), fk.cpu())
+    bhsd = lambda t: t.transpose(1, 2).double()  # noqa: E731
+    ro, rto, _, _ = orc.jvp_closed_form(bhsd(qr), bhsd(kr), bhsd(v.cpu()), bhsd(tqr), bhsd(tkr), bhsd(tv.cpu()))
+    assert orc.rel_l2(o.transpose(1, 2).cpu(), ro) < 1e-2
+    assert orc.rel_l2(to.transpose(1, 2).cpu(), rto) < 1e-2
+    with pytest.raises(NotImplementedError):
+        op((q, tq), (k, tk), (v, tv), attn_ctx=SimpleNamespace(rope=rope, kv_cache=object(), mode="APPEND"))
