@@ -77,3 +77,41 @@ def test_selective_checkpointing_saves_the_attention_forward(gpu, monkeypatch):
     assert orc.rel_l2(v.grad.transpose(1, 2), rv) <= 1e-2
     ref_wq = torch.einsum("bshd,bshe->de", q.double().cpu(), rq.transpose(1, 2))
     assert orc.rel_l2(wq.grad, ref_wq) <= 1e-2
+
+
+def test_sdpa_twin_refuses_what_the_kernels_lack():
+    """dmad_amd.sdpa.attention (rcm/utils/attention.py:120-167): dropout, causal and
+    float32 raise before anything reaches the GPU."""
+    from dmad_amd.sdpa import attention
+
+    q = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="dropout"):
+        attention(q, q, q, dropout_p=0.1)
+    with pytest.raises(NotImplementedError, match="causal"):
+        attention(q, q, q, causal=True)
+    with pytest.raises(NotImplementedError, match="float32"):
+        attention(q.float(), q.float(), q.float())
+
+
+@pytest.mark.gpu
+def test_sdpa_twin_forward_and_backward(gpu):
+    """BSHD in, BSHD contiguous out; q_scale and softmax_scale as the reference applies
+    them; gradients through the registered op against the oracle."""
+    from dmad_amd.sdpa import attention
+
+    B, S, H, D = 2, 333, 3, 128
+    g = torch.Generator().manual_seed(8)
+    q, k, v, do = ((torch.randn(B, S, H, D, generator=g, dtype=torch.float64)).to(torch.bfloat16) for _ in range(4))
+    leaves = [x.to(gpu).requires_grad_(True) for x in (q, k, v)]
+    out = attention(*leaves, softmax_scale=0.1, q_scale=0.5, deterministic=True)
+    assert out.shape == (B, S, H, D) and out.is_contiguous()
+    out.backward(do.to(gpu))
+    torch.cuda.synchronize()
+    bhsd = lambda t: t.transpose(1, 2).double()  # noqa: E731
+    qs = bhsd(q) * 0.5
+    ref_o, _ = orc.math_attention(qs, bhsd(k), bhsd(v), 0.1)
+    assert orc.rel_l2(bhsd(out.detach().cpu()), ref_o) < 1e-2
+    rq, rk, rv = orc.grads_dout_only(qs, bhsd(k), bhsd(v), bhsd(do), 0.1)
+    assert orc.rel_l2(bhsd(leaves[0].grad.cpu()), rq * 0.5) < 1e-2  # through q * q_scale
+    assert orc.rel_l2(bhsd(leaves[1].grad.cpu()), rk) < 1e-2
+    assert orc.rel_l2(bhsd(leaves[2].grad.cpu()), rv) < 1e-2
