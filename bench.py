@@ -167,7 +167,7 @@ def prologue_timing(H, L, D, grid, dev):
     # algorithmic bytes per call: y, ty read and q, q_dot written (bf16), weight and angles
     per_call = 4 * L * C * 2 + C * 2 + (L * D // 2 * 4 if grid is not None else 0)
     gbs = 2 * per_call / (best * 1e-3) / 1e9
-    return {"kernel": "rmsnorm_rope_kernel<bf16,jvp,rope>", "ms_q_and_k": round(best, 4),
+    return {"kernel": "rmsnorm_rope_kernel<bf16,10,jvp,rope,norm>", "ms_q_and_k": round(best, 4),
             "bytes_per_call": per_call, "achieved_GBps": round(gbs, 1), "hbm_peak_GBps": 8000.0,
             "frac": round(gbs / 8000.0, 4)}
 

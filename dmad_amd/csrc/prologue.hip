@@ -40,8 +40,9 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
   for (int j = 0; j < MAXC; ++j) {
     const int c = lane + 64 * j;
     if (c < nch) {
-      yv[j] = *(const i32x4_t*)(yrow + c * 16);
-      if constexpr (JVP) tv[j] = *(const i32x4_t*)(tyrow + c * 16);
+      // streamed once: non-temporal loads and stores keep them from churning the caches
+      yv[j] = __builtin_nontemporal_load((const i32x4_t*)(yrow + c * 16));
+      if constexpr (JVP) tv[j] = __builtin_nontemporal_load((const i32x4_t*)(tyrow + c * 16));
       if constexpr (!NORM) continue;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -121,8 +122,8 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
       ov[k] = (int)Elem<T>::pack2(q[2 * k], q[2 * k + 1]);
       if constexpr (JVP) tov[k] = (int)Elem<T>::pack2(tq[2 * k], tq[2 * k + 1]);
     }
-    *(i32x4_t*)(orow + c * 16) = ov;
-    if constexpr (JVP) *(i32x4_t*)(torow + c * 16) = tov;
+    __builtin_nontemporal_store(ov, (i32x4_t*)(orow + c * 16));
+    if constexpr (JVP) __builtin_nontemporal_store(tov, (i32x4_t*)(torow + c * 16));
   }
 }
 
@@ -131,6 +132,8 @@ static hipError_t prologue_launch_t(const PrologueParams& p, hipStream_t s) {
   const unsigned grid = (unsigned)((p.rows + 3) / 4);
   if (p.C <= 64 * 8 * 4)
     hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 4, JVP, ROPE, NORM>), dim3(grid), dim3(256), 0, s, p);
+  else if (p.C <= 64 * 8 * 10)  // Wan2.1-14B, C = 5120: 126 VGPRs, four waves per SIMD
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 10, JVP, ROPE, NORM>), dim3(grid), dim3(256), 0, s, p);
   else if (p.C <= 64 * 8 * 12)
     hipLaunchKernelGGL((rmsnorm_rope_kernel<T, 12, JVP, ROPE, NORM>), dim3(grid), dim3(256), 0, s, p);
   else
