@@ -40,10 +40,10 @@ static hipError_t dq_launch(const DqParams& p, int grid, hipStream_t s) {
 
 template <>
 DqLaunchFn dq_select<Elt, DMAD_D>(int mode) {
-  if constexpr (DqTrCfg<DMAD_D>::FITS) {
-    if (mode == kBwdDoutOnly) return dq_tr_select<Elt>();
+  if (mode == kBwdDoutOnly) {
+    if constexpr (DqTrCfg<DMAD_D>::FITS) return dq_tr_select<Elt>();  // bwd_dq_inst.hip
+    else return &dq_launch<Elt, DMAD_D, kBwdDoutOnly>;
   }
-  if (mode == kBwdDoutOnly) return &dq_launch<Elt, DMAD_D, kBwdDoutOnly>;
 #if DMAD_D <= 128
   if (mode == kBwdFull) return &dq_launch<Elt, DMAD_D, kBwdFull>;
 #endif
