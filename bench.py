@@ -80,6 +80,8 @@ def _args():
                     help="skip timing the fused RMSNorm+RoPE prologue (extra field)")
     ap.add_argument("--power", action="store_true",
                     help="sample board power and GFX clock with amd-smi during the timed steps (extra field)")
+    ap.add_argument("--no-plain", dest="plain", action="store_false",
+                    help="skip timing plain attention forward + backward (extra field)")
     ap.add_argument("--no-magi", dest="magi", action="store_false",
                     help="skip timing the block-sparse forward on the causal-student masks (extra field)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -170,6 +172,38 @@ def prologue_timing(H, L, D, grid, dev):
     return {"kernel": "rmsnorm_rope_kernel<bf16,10,jvp,rope,norm>", "ms_q_and_k": round(best, 4),
             "bytes_per_call": per_call, "achieved_GBps": round(gbs, 1), "hbm_peak_GBps": 8000.0,
             "frac": round(gbs / 8000.0, 4)}
+
+
+def plain_timing(q, k, v, do, dev):
+    """Plain attention (no tangents) forward and dO-only backward at the step's
+    shape: the op DMAD's critics and student gradients train through
+    (dmad::flash_attn_fwd / flash_attn_bwd). Flops: 4 and 10 units of H*L^2*D."""
+    import torch
+
+    from dmad_amd import _native
+    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+
+    s = q.shape[-1] ** -0.5
+    o, _, lse, _ = jvp_attention_forward(q, k, v, None, None, None, s)
+    jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
+    torch.cuda.synchronize()
+    best_f = best_b = float("inf")
+    for _ in range(3):
+        tf, tb = _native.KernelTimer(1), _native.KernelTimer(2)
+        with tf:
+            o, _, lse, _ = jvp_attention_forward(q, k, v, None, None, None, s)
+        with tb:
+            jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
+        torch.cuda.synchronize()
+        best_f = min(best_f, tf.elapsed()[0])
+        best_b = min(best_b, sum(tb.elapsed()))
+    B, H, L, D = q.shape
+    unit = B * H * L * L * D
+    tfs = 14.0 * unit / ((best_f + best_b) * 1e-3) / 1e12
+    return {"kernels": "attn_fwd32_kernel<bf16,plain> + attn_bwd_kv_tr_kernel + attn_bwd_dq_tr_kernel",
+            "ms_fwd": round(best_f, 3), "ms_bwd": round(best_b, 3),
+            "fwd_pct_peak": round(100 * 4.0 * unit / (best_f * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+            "TFLOPs_fwd_bwd": round(tfs, 1), "pct_peak_fwd_bwd": round(100 * tfs / PEAK_BF16_TFLOPS, 2)}
 
 
 def magi_timing(H, D, dev):
@@ -376,6 +410,8 @@ def main():
     # timed after the step (HBM-bound; not part of the step or its flops)
     if args.prologue:
         out["prologue_rmsnorm_rope_jvp"] = prologue_timing(H, L, D, grid, dev)
+    if args.plain:
+        out["plain_attn_fwd_bwd"] = plain_timing(q, k, v, do, dev)
     if args.magi:
         out["magi_fwd_jvp"] = magi_timing(H, D, dev)
     if args.calibration_copy_mib:
