@@ -719,6 +719,9 @@ struct KvTrCfg {
 // Query tile of attn_bwd_kv_tr_kernel.
 constexpr int kKvTrBmq = 32;
 
+// Compiled with MFMAs in VGPR form (bwd_kv_inst.hip): the S, dP MFMAs write
+// VGPRs that the VALU reads directly, and the dK, dV accumulators stay in
+// AGPRs through inline MFMAs (mfma32_acc).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
   using C = KvTrCfg<D, kKvTrBmq>;
@@ -897,8 +900,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
       else sn[qb] = mfma32(op, kreg[s], s == 0 ? zero16 : sn[qb], T());
     } else {
       const int mm = m - NMA, u = mm / (2 * DB), r = mm % (2 * DB), db = r >> 1;
-      if (r & 1) dkacc[db] = mfma32(op, dsb[u], dkacc[db], T());
-      else dvacc[db] = mfma32(op, pb[u], dvacc[db], T());
+      // P~, dS~ of chunk u are packed at least one MFMA slot (and its LDS read)
+      // before their first use here; the LDS operand is waited for by the compiler
+      if (r & 1) mfma32_acc(dkacc[db], op, dsb[u], T());
+      else mfma32_acc(dvacc[db], op, pb[u], T());
     }
   };
 
@@ -991,6 +996,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
     else last_step(IC<3>{}, sb, pbb);
     wait_vmem();  // no requests beyond the last tile stay in flight
   }
+  mfma_acc_drain();  // the last dK, dV MFMAs have finished before their AGPRs are read
 
   // ---- store dK = s (dK^T)^T, dV = (dV^T)^T for this lane's key
   if (key < p.Lk) {

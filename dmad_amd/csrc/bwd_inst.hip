@@ -18,11 +18,11 @@ using Elt = _Float16;
 #endif
 
 // The launch choice below mirrors dout_only_kv_bmq<D>().
+// (the dO-only pass for 128-wide heads, attn_bwd_kv_tr_kernel, is compiled in
+// bwd_kv_inst.hip and selected in bwd_select)
 template <typename T, int D, int MODE>
 static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
-  if constexpr (MODE == kBwdDoutOnly && KvTrCfg<D, kKvTrBmq>::FITS)
-    hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
-  else if constexpr (MODE == kBwdDoutOnly && KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS)
+  if constexpr (MODE == kBwdDoutOnly && KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS)
     hipLaunchKernelGGL((attn_bwd_kv_pipe_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE>), dim3(grid), dim3(256), 0, s, p);
@@ -52,7 +52,10 @@ DqLaunchFn dq_select<Elt, DMAD_D>(int mode) {
 
 template <>
 BwdLaunchFn bwd_select<Elt, DMAD_D>(int mode) {
-  if (mode == kBwdDoutOnly) return &bwd_launch<Elt, DMAD_D, kBwdDoutOnly>;
+  if (mode == kBwdDoutOnly) {
+    if constexpr (KvTrCfg<DMAD_D, kKvTrBmq>::FITS) return kv_tr_select<Elt>();  // bwd_kv_inst.hip
+    else return &bwd_launch<Elt, DMAD_D, kBwdDoutOnly>;
+  }
 #if DMAD_D <= 128
   if (mode == kBwdFull) return &bwd_launch<Elt, DMAD_D, kBwdFull>;
 #endif

@@ -1,0 +1,30 @@
+// Instantiates the dO-only dK/dV pass for 128-wide heads (attn_bwd_kv_tr_kernel)
+// for one element type (-DDMAD_T=<0 bf16 | 1 f16>). This unit is compiled with
+// MFMAs in VGPR form, so the score tiles feed the softmax without AGPR->VGPR
+// copies; the dK, dV accumulators are kept in AGPRs by the kernel itself.
+#include "launch.h"
+
+#ifndef DMAD_T
+#error "DMAD_T must be defined"
+#endif
+
+namespace dmad {
+
+#if DMAD_T == 0
+using Elt = __bf16;
+#else
+using Elt = _Float16;
+#endif
+
+template <typename T>
+static hipError_t kv_tr_launch(const BwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, 128>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <>
+BwdLaunchFn kv_tr_select<Elt>() {
+  return &kv_tr_launch<Elt>;
+}
+
+}  // namespace dmad

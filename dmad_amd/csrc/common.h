@@ -120,6 +120,23 @@ __device__ __forceinline__ f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c, _Fl
                                                 c, 0, 0, 0);
 }
 
+// C += A B on a 32x32x16 MFMA whose accumulator C stays in AGPRs, for kernels
+// compiled with MFMAs in VGPR form: the compiler then keeps the score tiles its
+// own MFMAs produce in VGPRs (no AGPR->VGPR copies before the VALU uses them)
+// while these accumulators stay in AGPRs. The compiler does not insert hazard
+// wait states around an inline MFMA: its operands must be written at least two
+// instructions before it, and code that reads C afterwards must first wait for
+// it with mfma_acc_drain().
+__device__ __forceinline__ void mfma32_acc(f32x16_t& c, i32x4_t a, i32x4_t b, __bf16) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma32_acc(f32x16_t& c, i32x4_t a, i32x4_t b, _Float16) {
+  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+// 24 wait states: more than an in-flight 32x32x16 MFMA needs before its result
+// is read.
+__device__ __forceinline__ void mfma_acc_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+
 // 16x16x32 layouts: A (16 x 32): lane l holds row l%16, k = 8*(l/16) + e;
 // B (32 x 16): lane l holds col l%16, k = 8*(l/16) + e;
 // C (16 x 16): lane l holds col l%16, rows 4*(l/16) + v, v = 0..3.

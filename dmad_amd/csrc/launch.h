@@ -45,6 +45,12 @@ typedef hipError_t (*DqLaunchFn)(const DqParams&, int grid, hipStream_t);
 template <typename T, int D>
 DqLaunchFn dq_select(int mode);
 
+// Launcher for the dO-only attn_bwd_kv_tr_kernel<T, 128> (bwd_kv_inst.hip).
+template <typename T>
+BwdLaunchFn kv_tr_select();
+template <> BwdLaunchFn kv_tr_select<__bf16>();
+template <> BwdLaunchFn kv_tr_select<_Float16>();
+
 // Launcher for the dO-only attn_bwd_dq_tr_kernel<T, 128> (bwd_dq_inst.hip).
 template <typename T>
 DqLaunchFn dq_tr_select();
