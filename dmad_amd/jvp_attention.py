@@ -28,7 +28,7 @@ Differences from the reference, all additive:
 """
 from __future__ import annotations
 
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
 
@@ -262,10 +262,10 @@ class _attention(torch.autograd.Function):
         # an output that does not reach the loss arrives in backward as None
         # (not zeros), so an unused `to` keeps the dO-only kernel
         ctx.set_materialize_grads(False)
-        o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale)
+        o, to, lse, mu = torch.ops.dmad.flash_attn_jvp_fwd(q, k, v, tq, tk, tv, float(sm_scale))
         if is_grad or tangent_grad:
             ctx.save_for_backward(q, k, v, tq, tk, tv, o, to, lse, mu)
-            ctx.sm_scale = sm_scale
+            ctx.sm_scale = float(sm_scale)
             ctx.tangent_grad = tangent_grad
         return o, to
 
@@ -281,14 +281,61 @@ class _attention(torch.autograd.Function):
             return (None,) * 8
         if dout is None:
             dout = torch.zeros_like(o)
-        dq, dk, dv, dtq, dtk, dtv = jvp_attention_backward(
+        dq, dk, dv, dtq, dtk, dtv = torch.ops.dmad.flash_attn_jvp_bwd(
             q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, ctx.sm_scale, ctx.tangent_grad
         )
-        if dtk is not None and tk is None:
+        # absent gradients come back from the op as 0-element tensors
+        dtq, dtk, dtv = (None if g.numel() == 0 and x.numel() != 0 else g for g, x in ((dtq, q), (dtk, k), (dtv, v)))
+        if tk is None:
             dtk = None
-        if dtv is not None and tv is None:
+        if tv is None:
             dtv = None
         return dq, dk, dv, dtq, dtk, dtv, None, None
+
+
+# The forward+JVP and its backward as registered torch ops: torch.compile traces
+# each as one node (the autograd.Function above stays the differentiable
+# wrapper), and selective activation checkpointing policies that keep outputs of
+# ops whose name contains "flash_attn" (the reference's mm_only_policy,
+# train/wan/rcm/utils/selective_activation_checkpoint.py:48-57) keep O, Ȯ and
+# the row statistics instead of recomputing the forward.
+@torch.library.custom_op("dmad::flash_attn_jvp_fwd", mutates_args=())
+def flash_attn_jvp_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tq: torch.Tensor,
+                       tk: Optional[torch.Tensor], tv: Optional[torch.Tensor],
+                       sm_scale: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(O, Ȯ, LSE, mu) of the forward+JVP kernel; ``tk = tv = None`` means zero K, V tangents."""
+    return jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale)
+
+
+@flash_attn_jvp_fwd.register_fake
+def _(q, k, v, tq, tk, tv, sm_scale):
+    B, H, Lq, _ = q.shape
+    o = q.new_empty((B, H, Lq, v.shape[-1]))
+    lse = q.new_empty((B, H, Lq), dtype=torch.float32)
+    return o, torch.empty_like(o), lse, torch.empty_like(lse)
+
+
+@torch.library.custom_op("dmad::flash_attn_jvp_bwd", mutates_args=())
+def flash_attn_jvp_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tq: torch.Tensor,
+                       tk: Optional[torch.Tensor], tv: Optional[torch.Tensor], o: torch.Tensor, to: torch.Tensor,
+                       lse: torch.Tensor, mu: torch.Tensor, dout: torch.Tensor, dto: Optional[torch.Tensor],
+                       sm_scale: float, tangent_grads: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                                      torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dQ, dK, dV, dQ̇, dK̇, dV̇) of flash_attn_jvp_fwd. Without ``dto`` these are the dO-only
+    gradients; the tangent gradients are computed when ``dto`` is given and ``tangent_grads``
+    is set, else they are returned as 0-element tensors."""
+    dq, dk, dv, dtq, dtk, dtv = jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_scale,
+                                                       tangent_grads)
+    # one fresh 0-element tensor per absent gradient: outputs of a custom op may not alias
+    return dq, dk, dv, *(q.new_empty((0,)) if g is None else g for g in (dtq, dtk, dtv))
+
+
+@flash_attn_jvp_bwd.register_fake
+def _(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_scale, tangent_grads):
+    tg = dto is not None and tangent_grads
+    # the kernels write contiguous gradients whatever the input strides
+    grads = (q.new_empty(q.shape), q.new_empty(k.shape), q.new_empty(v.shape))
+    return (*grads, *(q.new_empty(g.shape) if tg else q.new_empty((0,)) for g in grads))
 
 
 attention = _attention.apply
@@ -325,7 +372,7 @@ def flash_attn_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torc
 
 @flash_attn_bwd.register_fake
 def _(dout, q, k, v, o, lse, sm_scale):
-    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    return q.new_empty(q.shape), q.new_empty(k.shape), q.new_empty(v.shape)
 
 
 def _fwd_setup_context(ctx, inputs, output):
