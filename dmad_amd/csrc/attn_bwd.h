@@ -688,10 +688,11 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
 
 // dO-only dK/dV pass reading the transposed operands Q^T, dO^T straight from
 // the row-major Q, dO tiles with lds_read_tr16 (no transposed copies in HBM or
-// LDS). 4 waves x 32 keys, 64-query steps through a four-stage ring, the same
-// fixed MFMA stream as attn_bwd_kv_pipe_kernel:
-//   S, dP of tile j+1 (P, dS of tile j on the VALU), then
-//   dV^T += dO^T P, dK^T += Q^T dS of tile j (tile j+3 requested meanwhile).
+// LDS). 4 waves x 32 keys, 32-query steps through a four-stage ring. Step j is
+// a fixed MFMA stream:
+//   S, dP of tile j+1 (the second half of tile j's P, dS on the VALU), then
+//   dV^T += dO^T P, dK^T += Q^T dS of tile j (the first half of tile j+1's P,
+//   dS on the VALU; tile j+3 requested meanwhile).
 template <int D, int BMQ_>
 struct KvTrCfg {
   static constexpr int NW = 4;
@@ -873,24 +874,44 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
     sv.d[0] = *(lds_f32x4_t*)(sst + 4 * (BMQ + q0));
     sv.d[1] = *(lds_f32x4_t*)(sst + 4 * (BMQ + q0 + 4));
   };
-  // value v: block qb = v / 16, C-tile value (v % 16) = query 32 qb + 16 t + 8 half + e
-  auto value = [&](int v, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], const Stats& sv, float (&pv)[2],
-                   float (&dsv)[2]) {
-    const int qb = v / 16, t = (v % 16) / 8, e = v % 8;
-    const float l2 = sv.l[e >> 2][e & 3], dl = sv.d[e >> 2][e & 3];
-    // re-define the inputs here (an empty asm) so the compiler cannot hoist the
-    // value's arithmetic out of its MFMA slot and bunch the VALU work together
-    float s_in = sc[qb][8 * t + e], d_in = dpc[qb][8 * t + e];
-    asm volatile("" : "+v"(s_in), "+v"(d_in));
-    const float pe = fast_exp2(fmaf(s_in, p.scale_log2, -l2));
-    pv[v & 1] = pe;
-    dsv[v & 1] = pe * (d_in - dl);
+  // Values of a tile: 16 per lane, value v = C-tile value v of S, dP (query 16 t + 8 half + e for
+  // v = 8 t + e). Chunk u = values 8u .. 8u + 7 feeds the update MFMAs of 16-query chunk u; pair i of
+  // a chunk = values 8u + 2i, 8u + 2i + 1, packed into component i of pb[u] (P~) and dsb[u] (dS~).
+  // A pair is computed in two halves placed in different MFMA slots, so that the exp latency is
+  // covered by an MFMA: half 1 = exp2(s c - lse2) and dP - Delta, half 2 = the product and packs.
+  struct Half {
+    float p[2], dd[2];
   };
-  auto pack = [&](int v, const float (&pv)[2], const float (&dsv)[2], i32x4_t (&pb)[2 * NQB],
-                  i32x4_t (&dsb)[2 * NQB]) {
-    const int u = v / 8, e2 = (v % 8) >> 1;
-    pb[u][e2] = (int)Elem<T>::pack2(pv[0], pv[1]);
-    dsb[u][e2] = (int)Elem<T>::pack2(dsv[0], dsv[1]);
+  auto pair_first = [&](int u, int i, const f32x16_t& sc, const f32x16_t& dpc, const Stats& sv, Half& hv) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const int v = 8 * u + 2 * i + w, e = v % 8;
+      const float l2 = sv.l[e >> 2][e & 3], dl = sv.d[e >> 2][e & 3];
+      // re-define the inputs here (an empty asm) so the compiler cannot hoist the
+      // arithmetic out of its MFMA slot and bunch the VALU work together
+      float s_in = sc[v], d_in = dpc[v];
+      asm volatile("" : "+v"(s_in), "+v"(d_in));
+      hv.p[w] = fast_exp2(fmaf(s_in, p.scale_log2, -l2));
+      hv.dd[w] = d_in - dl;
+    }
+  };
+  auto pair_second = [&](int i, Half& hv, i32x4_t& pbu, i32x4_t& dsbu) {
+    asm volatile("" : "+v"(hv.p[0]), "+v"(hv.p[1]), "+v"(hv.dd[0]), "+v"(hv.dd[1]));
+    pbu[i] = (int)Elem<T>::pack2(hv.p[0], hv.p[1]);
+    dsbu[i] = (int)Elem<T>::pack2(hv.p[0] * hv.dd[0], hv.p[1] * hv.dd[1]);
+    asm volatile("" : "+v"(pbu[i]), "+v"(dsbu[i]));
+  };
+  // all 16 values of a tile at once (prologue and last step)
+  auto chunk_now = [&](const lds_char_t* st, int u, const f32x16_t& sc, const f32x16_t& dpc, i32x4_t& pbu,
+                       i32x4_t& dsbu) {
+    Stats sv;
+    load_stats(st, u, sv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      Half hv;
+      pair_first(u, i, sc, dpc, sv, hv);
+      pair_second(i, hv, pbu, dsbu);
+    }
   };
   auto mfma_slot = [&](int m, i32x4_t op, f32x16_t (&sn)[NQB], f32x16_t (&dpn)[NQB], const i32x4_t (&pb)[2 * NQB],
                        const i32x4_t (&dsb)[2 * NQB]) {
@@ -900,46 +921,46 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
       else sn[qb] = mfma32(op, kreg[s], s == 0 ? zero16 : sn[qb], T());
     } else {
       const int mm = m - NMA, u = mm / (2 * DB), r = mm % (2 * DB), db = r >> 1;
-      // P~, dS~ of chunk u are packed at least one MFMA slot (and its LDS read)
-      // before their first use here; the LDS operand is waited for by the compiler
       if (r & 1) mfma32_acc(dkacc[db], op, dsb[u], T());
       else mfma32_acc(dvacc[db], op, pb[u], T());
     }
   };
-
-  // step j (j + 1 < nqt, j % 4 == kk)
+  static_assert(NQB == 1 && NMA == 16 && NS == 32, "slot plan below assumes one 32-query block per step");
+  // Slot plan of step j (P~, dS~ of chunk 0 of tile j arrive computed by the previous step):
+  //   slots  0..15  S, dP MFMAs of tile j + 1; chunk 1 of tile j: pair i halves at 2 + 3i, 4 + 3i
+  //   slots 16..23  dV, dK MFMAs of chunk 0; 24..31 of chunk 1
+  //   slots 17..31  chunk 0 of tile j + 1 (S, dP of tile j + 1 complete after slot 15): halves at 17 + 4i, 19 + 4i
+  constexpr int A1 = 2, B1 = 17;
   auto step = [&](auto kk, int j, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], f32x16_t (&sn)[NQB],
-                  f32x16_t (&dpn)[NQB]) {
+                  f32x16_t (&dpn)[NQB], const i32x4_t& pb0, const i32x4_t& ds0, i32x4_t& pb0n, i32x4_t& ds0n) {
     constexpr int k = decltype(kk)::value;
     ring_sync<C::LOADS>();  // tile j + 1 has landed (tile j + 2 may be in flight)
     pin_offsets();
     const lds_char_t* s_next = stage(IC<k + 1>{});
     const lds_char_t* s_cur = stage(IC<k>{});
     lds_char_t* s_req = stage(IC<k + 3>{});
-    Stats sv[2];  // chunks u (in use) and u + 1 (landing)
-    load_stats(s_cur, 0, sv[0]);
+    Stats sv1, svn;  // chunk 1 of tile j, chunk 0 of tile j + 1
+    load_stats(s_cur, 1, sv1);
     i32x4_t opr[PF];
 #pragma unroll
     for (int m = 0; m < PF; ++m) opr[m] = load_op(s_next, s_cur, m);
-    i32x4_t pb[2 * NQB], dsb[2 * NQB];
-    float pv[2], dsv[2];
+    i32x4_t pb[2], dsb[2];
+    pb[0] = pb0;
+    dsb[0] = ds0;
+    Half h1[4], hn[4];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int m = 0; m < NS; ++m) {
       mfma_slot(m, opr[m % PF], sn, dpn, pb, dsb);
       if (m + PF < NS) opr[m % PF] = load_op(s_next, s_cur, m + PF);
-      // values v at slot 3v/2: all of block u are packed before its first update MFMA
 #pragma unroll
-      for (int v = 0; v < NVAL; ++v) {
-        if (3 * v / 2 == m) {
-          if (v % 8 == 0 && v + 8 < NVAL) load_stats(s_cur, v / 8 + 1, sv[(v / 8 + 1) & 1]);
-          value(v, sc, dpc, sv[(v / 8) & 1], pv, dsv);
-          if (v & 1) {
-            pack(v, pv, dsv, pb, dsb);
-            asm volatile("" : "+v"(pb[v / 8][(v % 8) >> 1]), "+v"(dsb[v / 8][(v % 8) >> 1]));
-          }
-        }
+      for (int i = 0; i < 4; ++i) {
+        if (m == A1 + 3 * i) pair_first(1, i, sc[0], dpc[0], sv1, h1[i]);
+        if (m == A1 + 2 + 3 * i) pair_second(i, h1[i], pb[1], dsb[1]);
+        if (m == B1 + 4 * i) pair_first(0, i, sn[0], dpn[0], svn, hn[i]);
+        if (m == B1 + 2 + 4 * i) pair_second(i, hn[i], pb0n, ds0n);
       }
+      if (m == 12) load_stats(s_next, 0, svn);
 #pragma unroll
       for (int li = 0; li < C::LOADS; ++li) {
         if (li * NS / C::LOADS == m) issue_load(s_req, j + 3, li);
@@ -947,18 +968,16 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  static_assert(3 * (NVAL - 1) / 2 < NMA + 8 * NQB, "values of the last block must precede its updates");
-  auto last_step = [&](auto kk, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB]) {
+  static_assert(A1 + 2 + 3 * 3 < NMA + 8, "chunk 1 is packed before its first update MFMA");
+  static_assert(B1 + 2 + 4 * 3 < NS, "chunk 0 of the next tile is packed within the step");
+  // final tile: chunk 1 values then the update MFMAs
+  auto last_step = [&](auto kk, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], const i32x4_t& pb0,
+                       const i32x4_t& ds0) {
     const lds_char_t* s_cur = stage(kk);
-    i32x4_t pb[2 * NQB], dsb[2 * NQB];
-    float pv[2], dsv[2];
-    Stats sv;
-#pragma unroll
-    for (int v = 0; v < NVAL; ++v) {
-      if (v % 8 == 0) load_stats(s_cur, v / 8, sv);
-      value(v, sc, dpc, sv, pv, dsv);
-      if (v & 1) pack(v, pv, dsv, pb, dsb);
-    }
+    i32x4_t pb[2], dsb[2];
+    pb[0] = pb0;
+    dsb[0] = ds0;
+    chunk_now(s_cur, 1, sc[0], dpc[0], pb[1], dsb[1]);
     f32x16_t un_s[NQB], un_p[NQB];
 #pragma unroll
     for (int m = NMA; m < NS; ++m) mfma_slot(m, load_op(s_cur, s_cur, m), un_s, un_p, pb, dsb);
@@ -973,27 +992,29 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
     for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
     ring_sync<2 * C::LOADS>();  // K, V rows and tile 0
     f32x16_t sa[NQB], pa[NQB], sb[NQB], pbb[NQB];
+    i32x4_t ca_p, ca_d, cb_p, cb_d;  // chunk-0 packs carried between steps (alternating)
     {
       const lds_char_t* s0 = stage(IC<0>{});
       i32x4_t dummy_p[2 * NQB], dummy_d[2 * NQB];
 #pragma unroll
       for (int m = 0; m < NMA; ++m) mfma_slot(m, load_op(s0, s0, m), sa, pa, dummy_p, dummy_d);
+      chunk_now(s0, 0, sa[0], pa[0], ca_p, ca_d);
     }
     int j = 0;
     for (; j + 4 < nqt; j += 4) {
-      step(IC<0>{}, j, sa, pa, sb, pbb);
-      step(IC<1>{}, j + 1, sb, pbb, sa, pa);
-      step(IC<2>{}, j + 2, sa, pa, sb, pbb);
-      step(IC<3>{}, j + 3, sb, pbb, sa, pa);
+      step(IC<0>{}, j, sa, pa, sb, pbb, ca_p, ca_d, cb_p, cb_d);
+      step(IC<1>{}, j + 1, sb, pbb, sa, pa, cb_p, cb_d, ca_p, ca_d);
+      step(IC<2>{}, j + 2, sa, pa, sb, pbb, ca_p, ca_d, cb_p, cb_d);
+      step(IC<3>{}, j + 3, sb, pbb, sa, pa, cb_p, cb_d, ca_p, ca_d);
     }
     const int rest = nqt - j;  // 1..4 tiles left
-    if (rest >= 2) step(IC<0>{}, j, sa, pa, sb, pbb);
-    if (rest >= 3) step(IC<1>{}, j + 1, sb, pbb, sa, pa);
-    if (rest >= 4) step(IC<2>{}, j + 2, sa, pa, sb, pbb);
-    if (rest == 1) last_step(IC<0>{}, sa, pa);
-    else if (rest == 2) last_step(IC<1>{}, sb, pbb);
-    else if (rest == 3) last_step(IC<2>{}, sa, pa);
-    else last_step(IC<3>{}, sb, pbb);
+    if (rest >= 2) step(IC<0>{}, j, sa, pa, sb, pbb, ca_p, ca_d, cb_p, cb_d);
+    if (rest >= 3) step(IC<1>{}, j + 1, sb, pbb, sa, pa, cb_p, cb_d, ca_p, ca_d);
+    if (rest >= 4) step(IC<2>{}, j + 2, sa, pa, sb, pbb, ca_p, ca_d, cb_p, cb_d);
+    if (rest == 1) last_step(IC<0>{}, sa, pa, ca_p, ca_d);
+    else if (rest == 2) last_step(IC<1>{}, sb, pbb, cb_p, cb_d);
+    else if (rest == 3) last_step(IC<2>{}, sa, pa, ca_p, ca_d);
+    else last_step(IC<3>{}, sb, pbb, cb_p, cb_d);
     wait_vmem();  // no requests beyond the last tile stay in flight
   }
   mfma_acc_drain();  // the last dK, dV MFMAs have finished before their AGPRs are read
