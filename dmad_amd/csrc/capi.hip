@@ -436,6 +436,7 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
   if (full && D > 128) return fail(DMAD_ERR_UNSUPPORTED, "the full backward supports head dims up to 128");
   if (B == 0 || H == 0 || (Lq == 0 && Lk == 0)) return ok();
   if (Lk == 0) return fail(DMAD_ERR_INVALID, "Lk must be at least 1");
+  if (Lq == 0) return fail(DMAD_ERR_INVALID, "Lq must be at least 1 (with no query rows dK and dV are zero)");
   if (B * H > ((int64_t)1 << 24) || Lq >= ((int64_t)1 << 26) || Lk >= ((int64_t)1 << 26))
     return fail(DMAD_ERR_UNSUPPORTED, "sizes too large");
   int rc;

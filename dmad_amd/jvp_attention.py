@@ -181,6 +181,12 @@ def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_sc
     _check_device(q, k, v, o, dout)
     code = nat.dtype_code(q.dtype)
     full = dto is not None
+    if B * H * Lq == 0:
+        # no query rows: every gradient is zero (dQ, dQ̇ are empty)
+        tg = full and want_tangent_grads
+        zq, zk, zv = (torch.zeros(x.shape, device=q.device, dtype=q.dtype) for x in (q, k, v))
+        return zq, zk, zv, (torch.zeros_like(zq) if tg else None), (torch.zeros_like(zk) if tg else None), \
+            (torch.zeros_like(zv) if tg else None)
     if full:
         if tk is None:
             tk = torch.zeros_like(k)

@@ -121,7 +121,9 @@ int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, in
  * Requires Dqk == Dv == D (as asserted at :537). o, to, lse, mu are the
  * outputs of dmad_attn_jvp_fwd for the same inputs. Gradients have the
  * strides given in dq_strides (shared by dq, dtq), dk_strides (dk, dtk) and
- * dv_strides (dv, dtv); do/dto share do_strides.
+ * dv_strides (dv, dtv); do/dto share do_strides. B, H or Lq = Lk = 0 is a
+ * no-op; Lq = 0 with Lk > 0 (where dk, dv are zero) is DMAD_ERR_INVALID: the
+ * caller fills the zeros.
  */
 int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
                       const void* k, const void* v, const void* tq, const void* tk, const void* tv,

@@ -184,3 +184,57 @@ def test_magi_fwd_rejects_bad_arguments(nat, over, code, needle):
 def test_magi_fwd_without_tasks_is_a_no_op(nat):
     assert _magi(nat, T=0, tg=0, tq_=0) == 0
     assert _magi(nat, R=0, kr=0, T=0) == 0
+
+
+def _bwd(nat, **over):
+    st = _strides(8192, 4096, 64, 1)
+    args = dict(dtype=0, B=1, H=2, Lq=64, Lk=64, D=64, q=256, k=256, v=256, tq=0, tk=0, tv=0, qs=st, ks=st, vs=st,
+                o=256, to=0, os=st, lse=256, mu=0, do=256, dto=0, dos=st, dq=256, dk=256, dv=256, dtq=0, dtk=0,
+                dtv=0, dqs=st, dks=st, dvs=st, scale=0.125, ws=256, wsb=1 << 30, stream=0)
+    args.update(over)
+    a = args
+    p = ctypes.c_void_p
+    return nat.lib().dmad_attn_jvp_bwd(
+        a["dtype"], a["B"], a["H"], a["Lq"], a["Lk"], a["D"], p(a["q"]), p(a["k"]), p(a["v"]), p(a["tq"]),
+        p(a["tk"]), p(a["tv"]), a["qs"], a["ks"], a["vs"], p(a["o"]), p(a["to"]), a["os"], p(a["lse"]), p(a["mu"]),
+        p(a["do"]), p(a["dto"]), a["dos"], p(a["dq"]), p(a["dk"]), p(a["dv"]), p(a["dtq"]), p(a["dtk"]), p(a["dtv"]),
+        a["dqs"], a["dks"], a["dvs"], a["scale"], p(a["ws"]), a["wsb"], p(a["stream"]))
+
+
+_FULL = dict(tq=256, tk=256, tv=256, to=256, mu=256, dto=256)
+
+
+@pytest.mark.parametrize(
+    "over,code,needle",
+    [
+        (dict(dtype=7), 2, "dtype"),
+        (dict(D=48), 2, "head dim"),
+        (dict(scale=-1.0), 2, "sm_scale"),
+        (dict(Lq=-1), 1, "negative"),
+        (dict(dtq=256, dtk=256, dtv=256), 1, "need the cotangent dto"),
+        (dict(_FULL, dtq=256, dtk=256), 1, "all set or all null"),
+        (dict(_FULL, D=256), 2, "up to 128"),
+        (dict(Lk=0), 1, "Lk must be"),
+        (dict(Lq=0), 1, "Lq must be"),
+        (dict(q=0), 1, "q: null"),
+        (dict(dk=0), 1, "dk: null"),
+        (dict(dqs=_strides(8192, 4096, 64, 2)), 1, "stride of the head dim"),
+        (dict(lse=0), 1, "lse"),
+        (dict(_FULL, mu=0), 1, "mu"),
+        (dict(_FULL, tk=0), 1, "tk: null"),
+        (dict(_FULL, dtq=256, dtk=256, dtv=0), 1, "all set or all null"),
+        (dict(wsb=16), 3, "workspace"),
+        (dict(ws=272), 1, "256-byte"),
+    ],
+)
+def test_bwd_rejects_bad_arguments(nat, over, code, needle):
+    """dmad_attn_jvp_bwd checks its arguments before any launch; bad ones return the
+    documented status with a message naming the problem."""
+    assert _bwd(nat, **over) == code
+    assert needle in nat.lib().dmad_last_error().decode()
+
+
+def test_bwd_empty_problem_is_a_no_op(nat):
+    assert _bwd(nat, B=0) == 0
+    assert _bwd(nat, H=0) == 0
+    assert _bwd(nat, Lq=0, Lk=0) == 0
