@@ -84,6 +84,8 @@ def _args():
                     help="skip timing plain attention forward + backward (extra field)")
     ap.add_argument("--no-magi", dest="magi", action="store_false",
                     help="skip timing the block-sparse forward on the causal-student masks (extra field)")
+    ap.add_argument("--harness", action="store_true",
+                    help="also time the reference perf harness configuration (B=4, H=32, D=64 and 128, fp16)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one elementwise kernel that reads and writes this many MiB "
                          "(a known-size reference for HBM byte counters under a profiler)")
@@ -204,6 +206,45 @@ def plain_timing(q, k, v, do, dev):
             "ms_fwd": round(best_f, 3), "ms_bwd": round(best_b, 3),
             "fwd_pct_peak": round(100 * 4.0 * unit / (best_f * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
             "TFLOPs_fwd_bwd": round(tfs, 1), "pct_peak_fwd_bwd": round(100 * tfs / PEAK_BF16_TFLOPS, 2)}
+
+
+def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384)):
+    """The configuration of the reference's own perf_report harness
+    (flash_attention_jvp_triton.py:662-725): B=4, H=32, fp16, L = 1024..16384,
+    forward+JVP and its backward, with the harness's flop convention (12 and 10
+    units of B*H*L^2*D). The reference publishes no result for it."""
+    import torch
+
+    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+
+    B, H = 4, 32
+    rows = []
+    for L in lengths:
+        g = torch.Generator(device=dev).manual_seed(0)
+        q, k, v, tq, tk, tv, do = (torch.randn((B, H, L, D), device=dev, dtype=torch.float16, generator=g)
+                                   for _ in range(7))
+        s = D ** -0.5
+        o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+        jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, None, s, False)
+        torch.cuda.synchronize()
+        # whole library calls (statistics, transposed copies and kernels), as the harness times the op
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        best_f = best_b = float("inf")
+        for _ in range(3):
+            ev[0].record()
+            o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+            ev[1].record()
+            jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, None, s, False)
+            ev[2].record()
+            torch.cuda.synchronize()
+            best_f = min(best_f, ev[0].elapsed_time(ev[1]))
+            best_b = min(best_b, ev[1].elapsed_time(ev[2]))
+        unit = B * H * L * L * D
+        rows.append({"L": L, "ms_fwd_jvp": round(best_f, 3),
+                     "fwd_jvp_TFLOPs": round(12.0 * unit / (best_f * 1e-3) / 1e12, 1),
+                     "ms_bwd": round(best_b, 3), "bwd_TFLOPs": round(10.0 * unit / (best_b * 1e-3) / 1e12, 1)})
+        del q, k, v, tq, tk, tv, do, o, to, lse, mu
+    return {"B": 4, "H": 32, "D": D, "dtype": "fp16", "rows": rows}
 
 
 def magi_timing(H, D, dev):
@@ -414,6 +455,8 @@ def main():
         out["plain_attn_fwd_bwd"] = plain_timing(q, k, v, do, dev)
     if args.magi:
         out["magi_fwd_jvp"] = magi_timing(H, D, dev)
+    if args.harness:
+        out["reference_harness"] = [harness_timing(dev, D=d) for d in (64, 128)]
     if args.calibration_copy_mib:
         n = args.calibration_copy_mib * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)
