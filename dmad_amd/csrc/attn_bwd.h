@@ -713,7 +713,7 @@ struct KvTrCfg {
   static constexpr int NRI = BMQ * CR / 64;  // wave-wide 1 KiB loads per row tile
   static constexpr int RPW = NRI / NW;
   static constexpr int ST_LANES = STAT_BYTES / 16 / NW;
-  static constexpr bool FITS = D == 128 && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr bool FITS = (D == 128 || D == 64) && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
   static constexpr int LOADS = 2 * RPW + 1;
 };
 
@@ -724,11 +724,10 @@ constexpr int kKvTrBmq = 32;
 // VGPRs that the VALU reads directly, and the dK, dV accumulators stay in
 // AGPRs through inline MFMAs (mfma32_acc).
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(BwdParams p) {
   using C = KvTrCfg<D, kKvTrBmq>;
   constexpr int BMQ = C::BMQ, NQB = C::NQB, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
   static_assert(C::FITS, "configuration does not fit");
-  static_assert(CR == 16, "trswz16 assumes 16 chunks per row");
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
@@ -775,7 +774,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
   for (int j = 0; j < RPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int row = pch / CR, phys = pch % CR;
-    const int logical = phys ^ trswz16(row & 15);
+    const int logical = phys ^ trswz<CR>(row & 15);
     roff_q[j] = (uint32_t)((int64_t)row * p.q_sl * 2) + logical * 16;
     roff_do[j] = (uint32_t)((int64_t)row * p.do_sl * 2) + logical * 16;
   }
@@ -808,7 +807,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     const int r = perm32(col);
-    sx[s] = r * ROWB + (((2 * s + half) ^ trswz16(r & 15)) << 4);
+    sx[s] = r * ROWB + (((2 * s + half) ^ trswz<CR>(r & 15)) << 4);
   }
   // Transposed reads (dO^T, Q^T blocks): lane group g = lane / 16 covers d0 = 32 db + 16 (g & 1)
   // and queries 16 u + 8 (g >> 1) + (0..3 | 4..7); lane 4r + c of the group points at row r,
@@ -822,7 +821,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
       for (int hh = 0; hh < 2; ++hh) {
         const int row = 8 * (g >> 1) + 4 * hh + r;  // plus 16 u
         const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-        tx[db][hh] = row * ROWB + ((chunk ^ trswz16(row & 15)) << 4) + 8 * (c & 1);
+        tx[db][hh] = row * ROWB + ((chunk ^ trswz<CR>(row & 15)) << 4) + 8 * (c & 1);
       }
     }
   }
@@ -843,6 +842,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
     }
   }
 
+  // D = 128 keeps the dK, dV accumulators in AGPRs through inline MFMAs (462
+  // registers, one wave per SIMD); D = 64 keeps everything in VGPRs (no AGPRs,
+  // so the compiler can fit two waves per SIMD in 256 registers)
+  constexpr bool kAccAgpr = D == 128;
   constexpr int PF = 4;
   constexpr int NMA = 2 * KS * NQB;   // S, dP MFMAs
   constexpr int NMB = 4 * NQB * DB;   // dV^T, dK^T MFMAs
@@ -921,16 +924,25 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
       else sn[qb] = mfma32(op, kreg[s], s == 0 ? zero16 : sn[qb], T());
     } else {
       const int mm = m - NMA, u = mm / (2 * DB), r = mm % (2 * DB), db = r >> 1;
-      if (r & 1) mfma32_acc(dkacc[db], op, dsb[u], T());
-      else mfma32_acc(dvacc[db], op, pb[u], T());
+      if constexpr (kAccAgpr) {
+        if (r & 1) mfma32_acc(dkacc[db], op, dsb[u], T());
+        else mfma32_acc(dvacc[db], op, pb[u], T());
+      } else {
+        if (r & 1) dkacc[db] = mfma32(op, dsb[u], dkacc[db], T());
+        else dvacc[db] = mfma32(op, pb[u], dvacc[db], T());
+      }
     }
   };
-  static_assert(NQB == 1 && NMA == 16 && NS == 32, "slot plan below assumes one 32-query block per step");
-  // Slot plan of step j (P~, dS~ of chunk 0 of tile j arrive computed by the previous step):
+  static_assert(NQB == 1 && (NS == 32 || NS == 16), "slot plan below assumes one 32-query block per step");
+  // Slot plan of step j (P~, dS~ of chunk 0 of tile j arrive computed by the previous step), D = 128:
   //   slots  0..15  S, dP MFMAs of tile j + 1; chunk 1 of tile j: pair i halves at 2 + 3i, 4 + 3i
   //   slots 16..23  dV, dK MFMAs of chunk 0; 24..31 of chunk 1
   //   slots 17..31  chunk 0 of tile j + 1 (S, dP of tile j + 1 complete after slot 15): halves at 17 + 4i, 19 + 4i
-  constexpr int A1 = 2, B1 = 17;
+  // D = 64 (half the MFMAs, the same values): S, dP in slots 0..7, updates of chunk 0 in 8..11 and of chunk 1
+  // in 12..15; chunk 1 of tile j: halves at i, 2 + i; chunk 0 of tile j + 1: halves at 9 + i, 11 + i.
+  constexpr int A1 = NS == 32 ? 2 : 0, AS = NS == 32 ? 3 : 1;
+  constexpr int B1 = NMA + 1, BS = NS == 32 ? 4 : 1;
+  constexpr int STAT_SLOT = NS == 32 ? 12 : 6;  // statistics of tile j + 1 requested here
   auto step = [&](auto kk, int j, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], f32x16_t (&sn)[NQB],
                   f32x16_t (&dpn)[NQB], const i32x4_t& pb0, const i32x4_t& ds0, i32x4_t& pb0n, i32x4_t& ds0n) {
     constexpr int k = decltype(kk)::value;
@@ -955,12 +967,12 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
       if (m + PF < NS) opr[m % PF] = load_op(s_next, s_cur, m + PF);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (m == A1 + 3 * i) pair_first(1, i, sc[0], dpc[0], sv1, h1[i]);
-        if (m == A1 + 2 + 3 * i) pair_second(i, h1[i], pb[1], dsb[1]);
-        if (m == B1 + 4 * i) pair_first(0, i, sn[0], dpn[0], svn, hn[i]);
-        if (m == B1 + 2 + 4 * i) pair_second(i, hn[i], pb0n, ds0n);
+        if (m == A1 + AS * i) pair_first(1, i, sc[0], dpc[0], sv1, h1[i]);
+        if (m == A1 + 2 + AS * i) pair_second(i, h1[i], pb[1], dsb[1]);
+        if (m == B1 + BS * i) pair_first(0, i, sn[0], dpn[0], svn, hn[i]);
+        if (m == B1 + 2 + BS * i) pair_second(i, hn[i], pb0n, ds0n);
       }
-      if (m == 12) load_stats(s_next, 0, svn);
+      if (m == STAT_SLOT) load_stats(s_next, 0, svn);
 #pragma unroll
       for (int li = 0; li < C::LOADS; ++li) {
         if (li * NS / C::LOADS == m) issue_load(s_req, j + 3, li);
@@ -968,8 +980,9 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  static_assert(A1 + 2 + 3 * 3 < NMA + 8, "chunk 1 is packed before its first update MFMA");
-  static_assert(B1 + 2 + 4 * 3 < NS, "chunk 0 of the next tile is packed within the step");
+  static_assert(A1 + 2 + AS * 3 < NMA + 2 * DB, "chunk 1 is packed before its first update MFMA");
+  static_assert(B1 + 2 + BS * 3 < NS, "chunk 0 of the next tile is packed within the step");
+  static_assert(STAT_SLOT < B1, "statistics of the next tile are requested before their first use");
   // final tile: chunk 1 values then the update MFMAs
   auto last_step = [&](auto kk, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], const i32x4_t& pb0,
                        const i32x4_t& ds0) {
@@ -1017,7 +1030,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_tr_kernel(BwdParams p) {
     else last_step(IC<3>{}, sb, pbb, cb_p, cb_d);
     wait_vmem();  // no requests beyond the last tile stay in flight
   }
-  mfma_acc_drain();  // the last dK, dV MFMAs have finished before their AGPRs are read
+  if constexpr (kAccAgpr) mfma_acc_drain();  // the last dK, dV MFMAs have finished before their AGPRs are read
 
   // ---- store dK = s (dK^T)^T, dV = (dV^T)^T for this lane's key
   if (key < p.Lk) {

@@ -535,7 +535,7 @@ struct DqTrCfg {
   static constexpr int NSTAGE = 4;
   static constexpr int NRI = BN * CR / 64;
   static constexpr int RPW = NRI / NW;
-  static constexpr bool FITS = D == 128 && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr bool FITS = (D == 128 || D == 64) && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
   static constexpr int LOADS = 2 * RPW;
 };
 
@@ -544,7 +544,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
   using C = DqTrCfg<D>;
   constexpr int BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
   static_assert(C::FITS, "configuration does not fit");
-  static_assert(CR == 16, "trswz16 assumes 16 chunks per row");
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
@@ -595,7 +594,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
   for (int j = 0; j < RPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int row = pch / CR, phys = pch % CR;
-    const int logical = phys ^ trswz16(row & 15);
+    const int logical = phys ^ trswz<CR>(row & 15);
     roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
     roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
   }
@@ -623,7 +622,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     const int r = perm32(col);
-    sx[s] = r * ROWB + (((2 * s + half) ^ trswz16(r & 15)) << 4);
+    sx[s] = r * ROWB + (((2 * s + half) ^ trswz<CR>(r & 15)) << 4);
   }
   int tx[DB][2];
   {
@@ -634,7 +633,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
       for (int hh = 0; hh < 2; ++hh) {
         const int row = 8 * (g >> 1) + 4 * hh + r;  // plus 16 t
         const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-        tx[db][hh] = row * ROWB + ((chunk ^ trswz16(row & 15)) << 4) + 8 * (c & 1);
+        tx[db][hh] = row * ROWB + ((chunk ^ trswz<CR>(row & 15)) << 4) + 8 * (c & 1);
       }
     }
   }
@@ -657,7 +656,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
   constexpr int NMB = 2 * DB;  // dQ^T MFMAs (two 16-key chunks)
   constexpr int NS = NMA + NMB;
   constexpr int NVAL = 16;     // P, dS values per lane per tile
-  static_assert(NVAL <= NMA, "values ride in the score slots");
+  constexpr int VPS = (NVAL + NMA - 1) / NMA;  // values per score slot (1 for D = 128, 2 for D = 64)
+  static_assert(VPS * NMA >= NVAL && VPS <= 2, "values ride in the score slots");
   const f32x16_t zero16 = {};
   auto load_op = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int m) -> i32x4_t {
     if (m < NMA) return *(lds_i32x4_t*)(s_next + ((m & 1) ? C::OFF_V : C::OFF_K) + sx[m >> 1]);
@@ -701,9 +701,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
     for (int m = 0; m < NS; ++m) {
       mfma_slot(m, opr[m % PF], sn, dpn, dsb);
       if (m + PF < NS) opr[m % PF] = load_op(s_next, s_cur, m + PF);
-      if (m < NVAL) {
-        value(m, sc, dpc, dsv);
-        if (m & 1) dsb[m >> 3][(m & 7) >> 1] = (int)Elem<T>::pack2(dsv[0], dsv[1]);
+#pragma unroll
+      for (int w = 0; w < VPS; ++w) {
+        const int v = VPS * m + w;
+        if (m < NMA && v < NVAL) {
+          value(v, sc, dpc, dsv);
+          if (v & 1) dsb[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(dsv[0], dsv[1]);
+        }
       }
 #pragma unroll
       for (int li = 0; li < C::LOADS; ++li) {

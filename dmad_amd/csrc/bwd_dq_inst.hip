@@ -1,4 +1,4 @@
-// Instantiates the dO-only dQ pass for 128-wide heads (attn_bwd_dq_tr_kernel)
+// Instantiates the dO-only dQ pass for 64- and 128-wide heads (attn_bwd_dq_tr_kernel)
 // for one element type (-DDMAD_T=<0 bf16 | 1 f16>). This unit is compiled with
 // MFMAs in VGPR form: the kernel then fits 256 VGPRs with no AGPRs, the score
 // tiles need no AGPR->VGPR copies before the softmax, and two workgroups share
@@ -17,15 +17,19 @@ using Elt = __bf16;
 using Elt = _Float16;
 #endif
 
-template <typename T>
+template <typename T, int D>
 static hipError_t dq_tr_launch(const DqParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_bwd_dq_tr_kernel<T, 128>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_bwd_dq_tr_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
 template <>
-DqLaunchFn dq_tr_select<Elt>() {
-  return &dq_tr_launch<Elt>;
+DqLaunchFn dq_tr_select<Elt, 64>() {
+  return &dq_tr_launch<Elt, 64>;
+}
+template <>
+DqLaunchFn dq_tr_select<Elt, 128>() {
+  return &dq_tr_launch<Elt, 128>;
 }
 
 }  // namespace dmad

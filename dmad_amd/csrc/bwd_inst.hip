@@ -18,8 +18,9 @@ using Elt = _Float16;
 #endif
 
 // The launch choice below mirrors dout_only_kv_bmq<D>().
-// (the dO-only pass for 128-wide heads, attn_bwd_kv_tr_kernel, is compiled in
-// bwd_kv_inst.hip and selected in bwd_select)
+// (the dO-only passes for 64- and 128-wide heads, attn_bwd_kv_tr_kernel and
+// attn_bwd_dq_tr_kernel, are compiled in bwd_kv_inst.hip and bwd_dq_inst.hip
+// and selected in bwd_select / dq_select)
 template <typename T, int D, int MODE>
 static hipError_t bwd_launch(const BwdParams& p, int grid, hipStream_t s) {
   if constexpr (MODE == kBwdDoutOnly && KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS)
@@ -41,7 +42,7 @@ static hipError_t dq_launch(const DqParams& p, int grid, hipStream_t s) {
 template <>
 DqLaunchFn dq_select<Elt, DMAD_D>(int mode) {
   if (mode == kBwdDoutOnly) {
-    if constexpr (DqTrCfg<DMAD_D>::FITS) return dq_tr_select<Elt>();  // bwd_dq_inst.hip
+    if constexpr (DqTrCfg<DMAD_D>::FITS) return dq_tr_select<Elt, DMAD_D>();  // bwd_dq_inst.hip
     else return &dq_launch<Elt, DMAD_D, kBwdDoutOnly>;
   }
 #if DMAD_D <= 128
@@ -53,7 +54,7 @@ DqLaunchFn dq_select<Elt, DMAD_D>(int mode) {
 template <>
 BwdLaunchFn bwd_select<Elt, DMAD_D>(int mode) {
   if (mode == kBwdDoutOnly) {
-    if constexpr (KvTrCfg<DMAD_D, kKvTrBmq>::FITS) return kv_tr_select<Elt>();  // bwd_kv_inst.hip
+    if constexpr (KvTrCfg<DMAD_D, kKvTrBmq>::FITS) return kv_tr_select<Elt, DMAD_D>();  // bwd_kv_inst.hip
     else return &bwd_launch<Elt, DMAD_D, kBwdDoutOnly>;
   }
 #if DMAD_D <= 128

@@ -1,4 +1,4 @@
-// Instantiates the dO-only dK/dV pass for 128-wide heads (attn_bwd_kv_tr_kernel)
+// Instantiates the dO-only dK/dV pass for 64- and 128-wide heads (attn_bwd_kv_tr_kernel)
 // for one element type (-DDMAD_T=<0 bf16 | 1 f16>). This unit is compiled with
 // MFMAs in VGPR form, so the score tiles feed the softmax without AGPR->VGPR
 // copies; the dK, dV accumulators are kept in AGPRs by the kernel itself.
@@ -16,15 +16,19 @@ using Elt = __bf16;
 using Elt = _Float16;
 #endif
 
-template <typename T>
+template <typename T, int D>
 static hipError_t kv_tr_launch(const BwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, 128>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, D>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
 template <>
-BwdLaunchFn kv_tr_select<Elt>() {
-  return &kv_tr_launch<Elt>;
+BwdLaunchFn kv_tr_select<Elt, 64>() {
+  return &kv_tr_launch<Elt, 64>;
+}
+template <>
+BwdLaunchFn kv_tr_select<Elt, 128>() {
+  return &kv_tr_launch<Elt, 128>;
 }
 
 }  // namespace dmad

@@ -206,6 +206,20 @@ __device__ __forceinline__ u32x2_t lds_read_tr16(const lds_char_t* p) {
 // slots of the 256-byte bank window.
 __device__ __forceinline__ int trswz16(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
+// The same for row tiles of 8 chunks per row (128-byte rows: 64-wide heads): a
+// map of the row index modulo 16 to [0, 8) under which 16 lanes reading rows
+// 0..15 at one logical chunk hit 16 distinct 16-byte slots of the 256-byte bank
+// window, and the 32 lanes of a transposed read (4 aligned consecutive rows x 4
+// aligned chunks) do too. Bits: r0 ^ r2, r3, r1 (found by exhaustive search
+// against both access patterns).
+__device__ __forceinline__ int trswz8(int r) { return ((r ^ (r >> 2)) & 1) | ((r >> 2) & 2) | ((r << 1) & 4); }
+template <int CR>
+__device__ __forceinline__ int trswz(int r) {
+  static_assert(CR == 16 || CR == 8, "row tiles of 16 or 8 chunks");
+  if constexpr (CR == 16) return trswz16(r);
+  else return trswz8(r);
+}
+
 // Compile-time integer as a value (for generic lambdas).
 template <int K>
 struct IC {

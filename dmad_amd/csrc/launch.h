@@ -45,17 +45,21 @@ typedef hipError_t (*DqLaunchFn)(const DqParams&, int grid, hipStream_t);
 template <typename T, int D>
 DqLaunchFn dq_select(int mode);
 
-// Launcher for the dO-only attn_bwd_kv_tr_kernel<T, 128> (bwd_kv_inst.hip).
-template <typename T>
+// Launcher for the dO-only attn_bwd_kv_tr_kernel<T, D>, D = 64 or 128 (bwd_kv_inst.hip).
+template <typename T, int D>
 BwdLaunchFn kv_tr_select();
-template <> BwdLaunchFn kv_tr_select<__bf16>();
-template <> BwdLaunchFn kv_tr_select<_Float16>();
+template <> BwdLaunchFn kv_tr_select<__bf16, 64>();
+template <> BwdLaunchFn kv_tr_select<__bf16, 128>();
+template <> BwdLaunchFn kv_tr_select<_Float16, 64>();
+template <> BwdLaunchFn kv_tr_select<_Float16, 128>();
 
-// Launcher for the dO-only attn_bwd_dq_tr_kernel<T, 128> (bwd_dq_inst.hip).
-template <typename T>
+// Launcher for the dO-only attn_bwd_dq_tr_kernel<T, D>, D = 64 or 128 (bwd_dq_inst.hip).
+template <typename T, int D>
 DqLaunchFn dq_tr_select();
-template <> DqLaunchFn dq_tr_select<__bf16>();
-template <> DqLaunchFn dq_tr_select<_Float16>();
+template <> DqLaunchFn dq_tr_select<__bf16, 64>();
+template <> DqLaunchFn dq_tr_select<__bf16, 128>();
+template <> DqLaunchFn dq_tr_select<_Float16, 64>();
+template <> DqLaunchFn dq_tr_select<_Float16, 128>();
 
 // Query tile of the dK/dV kernel, which fixes the layout of the backward
 // statistics (the full-derivative kernel always uses 32-query tiles).
