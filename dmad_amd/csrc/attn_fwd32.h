@@ -1,4 +1,4 @@
-// Forward(+JVP) kernel for 128-wide heads on 32x32x16 MFMAs.
+// Forward(+JVP) kernel for 128- and 64-wide heads on 32x32x16 MFMAs.
 //
 // Same semantics as attn_fwd_kernel (the reference kernel `_attn_fwd`,
 // train/wan/rcm/utils/flash_attention_jvp_triton.py:107-232): log2-domain
@@ -32,9 +32,9 @@
 
 namespace dmad {
 
-template <int MODE>
+template <int MODE, int DH = 128>
 struct Fwd32Cfg {
-  static constexpr int D = 128;
+  static constexpr int D = DH;
   static constexpr int NW = 4;        // waves per workgroup
   static constexpr int BM = 32 * NW;  // query rows per workgroup
   static constexpr int BN = 32;       // keys per pipeline step
@@ -59,7 +59,7 @@ struct Fwd32Cfg {
 
 // Head shapes served by attn_fwd32_kernel (the others use attn_fwd_kernel and
 // its variants, which read a transposed copy of V).
-constexpr bool fwd32_supported(int dqk, int dv) { return dqk == 128 && dv == 128; }
+constexpr bool fwd32_supported(int dqk, int dv) { return (dqk == 128 && dv == 128) || (dqk == 64 && dv == 64); }
 
 // MAGI: the block-sparse variant (the reference's `_attn_fwd_magi`,
 // flash_attention_jvp_triton.py:242-409). The workgroup runs one (query group,
@@ -67,13 +67,12 @@ constexpr bool fwd32_supported(int dqk, int dv) { return dqk == 128 && dv == 128
 // range starting at a 32-key boundary below its first key, and keys outside the
 // current range score -inf (the reference's n_mask, :338-343). Only the tile's
 // rows inside the group's query range are stored (:386-409).
-template <typename T, int MODE, bool MAGI = false>
-__global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
-  using C = Fwd32Cfg<MODE>;
+template <typename T, int MODE, bool MAGI = false, int DH = 128>
+__global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void attn_fwd32_kernel(FwdParams p) {
+  using C = Fwd32Cfg<MODE, DH>;
   constexpr int D = C::D, BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
   constexpr int NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
   constexpr float kSlack = RescaleSlack<T>::value;
-  static_assert(CR == 16, "trswz16 assumes 16 chunks per row");
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
@@ -125,13 +124,17 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
       if constexpr (C::JVP) tqreg[s] = buf_load16(rtq, qo + s * 32);
     }
   }
-  // Q and Qd live in AGPRs for the whole kernel (MFMA operands read them there):
-  // the VGPRs hold the accumulators, the score tiles and the softmax. This
-  // unit is compiled with MFMAs in VGPR form (-amdgpu-mfma-vgpr-form).
+  // 128-wide heads: Q and Qd live in AGPRs for the whole kernel (MFMA operands
+  // read them there); the VGPRs hold the accumulators, the score tiles and the
+  // softmax. This unit is compiled with MFMAs in VGPR form
+  // (-amdgpu-mfma-vgpr-form). 64-wide heads keep everything in VGPRs, two waves
+  // per SIMD.
+  if constexpr (DH == 128) {
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    asm volatile("" : "+a"(qreg[s]));
-    if constexpr (C::JVP) asm volatile("" : "+a"(tqreg[s]));
+    for (int s = 0; s < KS; ++s) {
+      asm volatile("" : "+a"(qreg[s]));
+      if constexpr (C::JVP) asm volatile("" : "+a"(tqreg[s]));
+    }
   }
 
   // ---- key-side resources and per-lane request offsets (tile independent)
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
   for (int j = 0; j < RPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int row = pch / CR, phys = pch % CR;
-    const int logical = phys ^ trswz16(row & 15);
+    const int logical = phys ^ trswz<CR>(row & 15);
     roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
     roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
   }
@@ -190,7 +193,7 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     const int r = perm32(col);
-    sx[s] = r * ROWB + (((2 * s + half) ^ trswz16(r & 15)) << 4);
+    sx[s] = r * ROWB + (((2 * s + half) ^ trswz<CR>(r & 15)) << 4);
   }
   int tx[DB][2];
   {
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
       for (int hh = 0; hh < 2; ++hh) {
         const int row = 8 * (g >> 1) + 4 * hh + r;  // plus 16 t
         const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-        tx[db][hh] = row * ROWB + ((chunk ^ trswz16(row & 15)) << 4) + 8 * (c & 1);
+        tx[db][hh] = row * ROWB + ((chunk ^ trswz<CR>(row & 15)) << 4) + 8 * (c & 1);
       }
     }
   }
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(256) void attn_fwd32_kernel(FwdParams p) {
   // and the plain forward keeps them in VGPRs, where it fits two waves per SIMD.
   // Code that touches AGPR accumulators with the VALU (the rescale, the
   // epilogue) waits for the MFMAs first.
-  constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI;
+  constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI && DH == 128;
   auto acc_mfma = [&](f32x16_t& c, i32x4_t a, i32x4_t b) {
     if constexpr (kAccAgpr) mfma32_acc(c, a, b, T());
     else c = mfma32(a, b, c, T());

@@ -1,4 +1,4 @@
-// Instantiates attn_fwd32_kernel for one element type: compiled once per type
+// Instantiates attn_fwd32_kernel (64- and 128-wide heads) for one element type: compiled once per type
 // with -DDMAD_T=<0 bf16 | 1 f16> and MFMAs in VGPR form, so that the
 // accumulators and score tiles take the VGPRs and Q, Qd the AGPRs.
 #include "launch.h"
@@ -15,37 +15,47 @@ using Elt = __bf16;
 using Elt = _Float16;
 #endif
 
-static_assert(Fwd32Cfg<kFwdJvp>::BM == kMagiBlockM, "block-sparse tasks are 128-query tiles");
+static_assert(Fwd32Cfg<kFwdJvp>::BM == kMagiBlockM && Fwd32Cfg<kFwdJvp, 64>::BM == kMagiBlockM, "block-sparse tasks are 128-query tiles");
 
-template <typename T, int MODE>
+template <typename T, int MODE, int D>
 static hipError_t fwd32_launch(const FwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_fwd32_kernel<T, MODE>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_fwd32_kernel<T, MODE, false, D>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
-template <typename T, int MODE>
+template <typename T, int MODE, int D>
 static hipError_t fwd32_magi_launch(const FwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_fwd32_kernel<T, MODE, true>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_fwd32_kernel<T, MODE, true, D>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
-template <>
-FwdLaunchFn fwd32_magi_select<Elt>(int mode) {
+template <int D>
+static FwdLaunchFn fwd32_magi_mode(int mode) {
   switch (mode) {
-    case kFwdJvp: return &fwd32_magi_launch<Elt, kFwdJvp>;
-    case kFwdJvpQOnly: return &fwd32_magi_launch<Elt, kFwdJvpQOnly>;
+    case kFwdJvp: return &fwd32_magi_launch<Elt, kFwdJvp, D>;
+    case kFwdJvpQOnly: return &fwd32_magi_launch<Elt, kFwdJvpQOnly, D>;
+    default: return nullptr;
+  }
+}
+
+template <int D>
+static FwdLaunchFn fwd32_mode(int mode) {
+  switch (mode) {
+    case kFwdPlain: return &fwd32_launch<Elt, kFwdPlain, D>;
+    case kFwdJvp: return &fwd32_launch<Elt, kFwdJvp, D>;
+    case kFwdJvpQOnly: return &fwd32_launch<Elt, kFwdJvpQOnly, D>;
     default: return nullptr;
   }
 }
 
 template <>
-FwdLaunchFn fwd32_select<Elt>(int mode) {
-  switch (mode) {
-    case kFwdPlain: return &fwd32_launch<Elt, kFwdPlain>;
-    case kFwdJvp: return &fwd32_launch<Elt, kFwdJvp>;
-    case kFwdJvpQOnly: return &fwd32_launch<Elt, kFwdJvpQOnly>;
-    default: return nullptr;
-  }
+FwdLaunchFn fwd32_magi_select<Elt>(int mode, int d) {
+  return d == 64 ? fwd32_magi_mode<64>(mode) : d == 128 ? fwd32_magi_mode<128>(mode) : nullptr;
+}
+
+template <>
+FwdLaunchFn fwd32_select<Elt>(int mode, int d) {
+  return d == 64 ? fwd32_mode<64>(mode) : d == 128 ? fwd32_mode<128>(mode) : nullptr;
 }
 
 }  // namespace dmad

@@ -60,9 +60,11 @@ FwdLaunchFn fwd_magi_select<Elt, DMAD_D>(int dv, int mode) {
   switch (dv) {
     case 16: return fwd_magi_mode<Elt, DMAD_D, 16>(mode);
     case 32: return fwd_magi_mode<Elt, DMAD_D, 32>(mode);
-    case 64: return fwd_magi_mode<Elt, DMAD_D, 64>(mode);
+    case 64:
+      if constexpr (fwd32_supported(DMAD_D, 64)) return fwd32_magi_select<Elt>(mode, 64);
+      else return fwd_magi_mode<Elt, DMAD_D, 64>(mode);
     case 128:
-      if constexpr (fwd32_supported(DMAD_D, 128)) return fwd32_magi_select<Elt>(mode);
+      if constexpr (fwd32_supported(DMAD_D, 128)) return fwd32_magi_select<Elt>(mode, 128);
       else return fwd_magi_mode<Elt, DMAD_D, 128>(mode);
     case 256: return fwd_magi_mode<Elt, DMAD_D, 256>(mode);
     default: return nullptr;
@@ -74,9 +76,11 @@ FwdLaunchFn fwd_select<Elt, DMAD_D>(int dv, int mode) {
   switch (dv) {
     case 16: return fwd_mode<Elt, DMAD_D, 16>(mode);
     case 32: return fwd_mode<Elt, DMAD_D, 32>(mode);
-    case 64: return fwd_mode<Elt, DMAD_D, 64>(mode);
+    case 64:
+      if constexpr (fwd32_supported(DMAD_D, 64)) return fwd32_select<Elt>(mode, 64);
+      else return fwd_mode<Elt, DMAD_D, 64>(mode);
     case 128:
-      if constexpr (fwd32_supported(DMAD_D, 128)) return fwd32_select<Elt>(mode);
+      if constexpr (fwd32_supported(DMAD_D, 128)) return fwd32_select<Elt>(mode, 128);
       else return fwd_mode<Elt, DMAD_D, 128>(mode);
     case 256: return fwd_mode<Elt, DMAD_D, 256>(mode);
     default: return nullptr;

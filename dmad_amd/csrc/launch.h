@@ -18,18 +18,18 @@ FwdLaunchFn fwd_select(int dv, int mode);
 
 // Launcher for attn_fwd32_kernel<T, MODE> (128-wide heads; fwd32_inst.hip).
 template <typename T>
-FwdLaunchFn fwd32_select(int mode);
-template <> FwdLaunchFn fwd32_select<__bf16>(int);
-template <> FwdLaunchFn fwd32_select<_Float16>(int);
+FwdLaunchFn fwd32_select(int mode, int d);
+template <> FwdLaunchFn fwd32_select<__bf16>(int, int);
+template <> FwdLaunchFn fwd32_select<_Float16>(int, int);
 
 // Block-sparse (MagiMask) forward launchers, JVP modes only; the grid is
 // tasks * B * H workgroups of 256 threads, each task a 128-query tile.
 template <typename T, int DQK>
 FwdLaunchFn fwd_magi_select(int dv, int mode);
 template <typename T>
-FwdLaunchFn fwd32_magi_select(int mode);
-template <> FwdLaunchFn fwd32_magi_select<__bf16>(int);
-template <> FwdLaunchFn fwd32_magi_select<_Float16>(int);
+FwdLaunchFn fwd32_magi_select(int mode, int d);
+template <> FwdLaunchFn fwd32_magi_select<__bf16>(int, int);
+template <> FwdLaunchFn fwd32_magi_select<_Float16>(int, int);
 // Query rows per task of the block-sparse kernels.
 constexpr int kMagiBlockM = 128;
 
