@@ -40,7 +40,7 @@ _F = ctypes.c_float
 SIGNATURES = {
     "dmad_abi_version": (_INT, []),
     "dmad_last_error": (ctypes.c_char_p, []),
-    "dmad_attn_fwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _SZP]),
+    "dmad_attn_fwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _SZP]),
     "dmad_attn_jvp_fwd": (_INT, [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _I64,
                                  _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
                                  _P, _P, _I64P, _P, _P, _F, _P, _SZ, _P]),

@@ -106,7 +106,10 @@ int check_operand(const char* name, const void* ptr, const int64_t* st, int64_t 
   return DMAD_OK;
 }
 
-int64_t fwd_ws_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dv) {
+// Bytes of the transposed, key-padded V (and Vd) copies the generic forward
+// kernels read; the kernels for 64- and 128-wide heads read V in place.
+int64_t fwd_ws_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv) {
+  if (dmad::fwd32_supported((int)Dqk, (int)Dv)) return 0;
   const int64_t dvp = Dv < 32 ? 32 : Dv;
   const int64_t one = B * H * dvp * round_up(Lk, kLkAlign) * 2;
   return round_up(one, 256) * (mode == DMAD_FWD_JVP ? 2 : 1);
@@ -265,8 +268,8 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
     if ((rc = check_operand("tv", tv, v_strides, Lk, Dv))) return rc;
   }
   if (lse == nullptr) return fail(DMAD_ERR_INVALID, "lse: null pointer");
-  const int64_t need = fwd_ws_bytes(mode, B, H, Lk, Dv);
-  if (workspace == nullptr || (int64_t)workspace_bytes < need)
+  const int64_t need = fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
+  if (need > 0 && (workspace == nullptr || (int64_t)workspace_bytes < need))
     return fail(DMAD_ERR_WORKSPACE, "workspace needs %lld bytes, got %lld", (long long)need, (long long)workspace_bytes);
   if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
   const int64_t dvp = Dv < 32 ? 32 : Dv, lkp = round_up(Lk, kLkAlign);
@@ -363,11 +366,12 @@ int dmad_set_kernel_events(void* const* events, int count) {
   return ok();
 }
 
-int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dv, size_t* bytes) {
+int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv,
+                                  size_t* bytes) {
   if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
   if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
-  if (B < 0 || H < 0 || Lk < 0 || !head_dim_ok(Dv)) return fail(DMAD_ERR_INVALID, "bad sizes");
-  *bytes = (size_t)fwd_ws_bytes(mode, B, H, Lk, Dv);
+  if (B < 0 || H < 0 || Lk < 0 || !head_dim_ok(Dqk) || !head_dim_ok(Dv)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  *bytes = (size_t)fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
   return ok();
 }
 

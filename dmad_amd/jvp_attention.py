@@ -105,7 +105,7 @@ def jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale, need_mu=True):
     mu = torch.empty_like(lse) if tq is not None else None
     lib = nat.lib()
     ws_bytes = nat.ctypes.c_size_t(0)
-    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dv, nat.ctypes.byref(ws_bytes)))
+    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv, nat.ctypes.byref(ws_bytes)))
     ws = torch.empty(max(int(ws_bytes.value), 1), device=dev, dtype=torch.uint8)
     nat.check(
         lib.dmad_attn_jvp_fwd(
@@ -158,7 +158,7 @@ def jvp_attention_forward_magi(q, k, v, tq, tk, tv, sm_scale, magi_mask):
     mu = torch.empty_like(lse)
     lib = nat.lib()
     ws_bytes = nat.ctypes.c_size_t(0)
-    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dv, nat.ctypes.byref(ws_bytes)))
+    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv, nat.ctypes.byref(ws_bytes)))
     ws = torch.empty(max(int(ws_bytes.value), 1), device=dev, dtype=torch.uint8)
     nat.check(
         lib.dmad_attn_jvp_fwd_magi(

@@ -50,8 +50,10 @@ int dmad_abi_version(void);
 /* Description of the last failure on this thread ("" if none). */
 const char* dmad_last_error(void);
 
-/* Bytes of workspace dmad_attn_jvp_fwd / dmad_attn_fwd need for these sizes. */
-int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dv, size_t* bytes);
+/* Bytes of workspace dmad_attn_jvp_fwd / dmad_attn_fwd / dmad_attn_jvp_fwd_magi need
+ * for these sizes: 0 for Dqk = Dv = 64 or 128 (V is read in place; the workspace
+ * pointer may then be NULL), else room for transposed copies of V (and Vd). */
+int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv, size_t* bytes);
 
 /*
  * Forward (+JVP): replaces the `_attn_fwd` launch of _attention.forward

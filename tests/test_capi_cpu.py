@@ -67,8 +67,8 @@ def _fwd(nat, **over):
         (dict(ks=_strides(8192, 4096, 60, 1)), 1, "multiples of 8"),
         (dict(v=258), 1, "aligned"),
         (dict(mu=0), 1, "mu"),
-        (dict(wsb=16), 3, "workspace"),
-        (dict(ws=0), 3, "workspace"),
+        (dict(wsb=16, Dqk=32, Dv=32), 3, "workspace"),  # 32-wide heads read a transposed copy of V
+        (dict(ws=0, Dqk=32, Dv=32), 3, "workspace"),
         (dict(Lq=1 << 22, qs=_strides(0, 0, 4096, 1)), 2, "2 GiB"),
     ],
 )
@@ -84,17 +84,24 @@ def test_fwd_empty_problem_is_a_no_op(nat):
 
 def test_kv_tangent_zero_mode_does_not_need_kv_tangents(nat):
     # mode 2 never reads tk/tv: null is accepted up to the workspace check
-    assert _fwd(nat, mode=2, tk=0, tv=0, wsb=16) == 3
+    assert _fwd(nat, mode=2, tk=0, tv=0, wsb=16, Dqk=32, Dv=32) == 3
 
 
 def test_workspace_query(nat):
     n = ctypes.c_size_t(0)
-    assert nat.lib().dmad_attn_fwd_workspace_bytes(1, 1, 40, 32760, 128, ctypes.byref(n)) == 0
+    q = nat.lib().dmad_attn_fwd_workspace_bytes
+    # 64- and 128-wide heads read V in place: no workspace
+    for d in (64, 128):
+        for mode in (0, 1, 2):
+            assert q(mode, 1, 40, 32760, d, d, ctypes.byref(n)) == 0 and n.value == 0
+    # other head dims (or Dqk != Dv): transposed, key-padded copies of V (and Vd in the full JVP mode)
+    assert q(1, 1, 40, 32760, 64, 128, ctypes.byref(n)) == 0
     assert n.value == 2 * 40 * 128 * 32768 * 2
-    assert nat.lib().dmad_attn_fwd_workspace_bytes(0, 1, 40, 32760, 128, ctypes.byref(n)) == 0
-    assert n.value == 40 * 128 * 32768 * 2
-    assert nat.lib().dmad_attn_fwd_workspace_bytes(0, 1, 1, 10, 16, ctypes.byref(n)) == 0
+    assert q(0, 1, 40, 32760, 256, 256, ctypes.byref(n)) == 0
+    assert n.value == 40 * 256 * 32768 * 2
+    assert q(0, 1, 1, 10, 16, 16, ctypes.byref(n)) == 0
     assert n.value == 32 * 64 * 2  # Dv < 32 pads to 32 rows, keys pad to 64
+    assert q(0, 1, 1, 10, 48, 64, ctypes.byref(n)) == 1  # bad head dim
 
 
 def test_kernel_event_hook_validates(nat):
@@ -173,7 +180,7 @@ def _magi(nat, **over):
         (dict(mode=0), 2, "JVP modes"),
         (dict(Dqk=48), 2, "head dims"),
         (dict(tk=0), 1, "tk: null"),
-        (dict(wsb=16, Dqk=64, Dv=64), 3, "workspace"),
+        (dict(wsb=16, Dqk=32, Dv=32), 3, "workspace"),
     ],
 )
 def test_magi_fwd_rejects_bad_arguments(nat, over, code, needle):
