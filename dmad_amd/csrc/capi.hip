@@ -222,8 +222,11 @@ struct BwdWs {
 BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) {
   const int64_t BH = B * H, dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign);
   BwdWs w{};
-  w.nq = full ? 4 : 2;
-  w.nk = full ? 2 : 1;
+  // transposed copies of Q, dO (and Qd, dOd) and K (and Kd): the full derivative
+  // and the dO-only passes of the head dims that read transposed copies
+  const bool copies = full != 0 || !dmad::dout_only_reads_rows((int)D);
+  w.nq = full ? 4 : (copies ? 2 : 0);
+  w.nk = full ? 2 : (copies ? 1 : 0);
   w.tgrad = full == 2;
   w.trq = round_up(BH * dp * lqp * 2, 256);
   w.trk = round_up(BH * dp * lkp * 2, 256);
@@ -483,11 +486,11 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
 
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  char* trq = ws;
-  char* trdo = ws + w.trq;
+  char* trq = w.nq ? ws : nullptr;
+  char* trdo = w.nq ? ws + w.trq : nullptr;
   char* trtq = full ? ws + 2 * w.trq : nullptr;
   char* trdto = full ? ws + 3 * w.trq : nullptr;
-  char* trk = ws + w.nq * w.trq;
+  char* trk = w.nk ? ws + w.nq * w.trq : nullptr;
   char* trtk = full ? trk + w.trk : nullptr;
   float* stats = (float*)(ws + w.nq * w.trq + w.nk * w.trk);
   float* stats_bt = w.tgrad ? (float*)((char*)stats + w.stats) : nullptr;

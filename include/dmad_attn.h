@@ -109,7 +109,9 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
 
 /* Bytes of workspace dmad_attn_jvp_bwd needs. full: 0 = dO-only gradients,
  * 1 = full derivative (dto given), 2 = full derivative plus tangent gradients
- * (dto, dtq, dtk, dtv given). */
+ * (dto, dtq, dtk, dtv given). The per-row statistics always; transposed copies
+ * of Q, dO, K (and the tangents) for the full derivative and for the dO-only
+ * gradients of head dims other than 64 and 128. */
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes);
 
 /*

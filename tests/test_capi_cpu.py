@@ -241,6 +241,21 @@ def test_bwd_rejects_bad_arguments(nat, over, code, needle):
     assert needle in nat.lib().dmad_last_error().decode()
 
 
+def test_bwd_workspace_query(nat):
+    n = ctypes.c_size_t(0)
+    q = nat.lib().dmad_attn_bwd_workspace_bytes
+    stats = 40 * 32768 * 2 * 4  # lse2 and D per (head, padded query row)
+    # dO-only, 64- and 128-wide heads: the kernels read rows, only the statistics
+    for d in (64, 128):
+        assert q(0, 1, 40, 32760, 32760, d, ctypes.byref(n)) == 0 and n.value == stats
+    # 32-wide heads read transposed copies of Q, dO and K
+    copy = 40 * 32 * 32768 * 2
+    assert q(0, 1, 40, 32760, 32760, 32, ctypes.byref(n)) == 0 and n.value == 3 * copy + stats
+    # the full derivative: Q, dO, Qd, dOd, K, Kd copies and four statistics per row
+    copy = 40 * 128 * 32768 * 2
+    assert q(1, 1, 40, 32760, 32760, 128, ctypes.byref(n)) == 0 and n.value == 6 * copy + 2 * stats
+
+
 def test_bwd_empty_problem_is_a_no_op(nat):
     assert _bwd(nat, B=0) == 0
     assert _bwd(nat, H=0) == 0
