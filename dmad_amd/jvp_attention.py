@@ -15,12 +15,12 @@ torch's current stream. There is no CPU or PyTorch fallback.
 Differences from the reference, all additive:
   * ``tk``/``tv`` may be ``None`` (tangents of K and V known to be zero, as in
     Wan cross-attention): the forward then skips the two GEMMs they feed.
-  * backward: when the cotangent of ``to`` is given, the gradients include its
-    contribution and, if the tangents require grad, gradients for them
-    (the reference discards that cotangent, :535, and returns None for the
-    tangents, :579). Without it the gradients are the reference's dO-only
-    ones. ``set_reference_backward(True)`` restores the reference behaviour
-    exactly in both cases.
+  * backward (``set_backward_mode``): by default the reference's dO-only
+    gradients, with the reference's saved tensors (q, k, v, o, LSE; the
+    cotangent of ``to`` is ignored, :535), unless a tangent requires grad: then
+    the full derivative, including the cotangent of ``to`` and gradients for
+    the tangents (the reference returns None for them, :579). Mode "full" gives
+    the full derivative whenever that cotangent arrives; mode "reference" never.
   * ``magi_mask`` (block-sparse masks, :502-531) runs the block-sparse kernel
     as the reference does (forward only: RuntimeError when q, k or v require
     grad, :504-505, and likewise when a tangent does). Masks built with any
@@ -34,13 +34,29 @@ import torch
 
 from . import _native as nat
 
-_REFERENCE_BACKWARD = False
+_BACKWARD_MODES = ("auto", "reference", "full")
+_BACKWARD_MODE = "auto"
+
+
+def set_backward_mode(mode: str) -> None:
+    """How ``attention``'s backward treats the cotangent of ``to``.
+
+    "auto" (default): as the reference (dO-only gradients; only q, k, v, o and
+        the LSE are kept for the backward) unless a tangent requires grad; then
+        the full derivative, with gradients for the tangents.
+    "reference": always as the reference (tangents get None).
+    "full": the full derivative whenever the cotangent of ``to`` reaches the op
+        (the tangents, ``to`` and mu are then kept for the backward too).
+    """
+    global _BACKWARD_MODE
+    if mode not in _BACKWARD_MODES:
+        raise ValueError(f"backward mode must be one of {_BACKWARD_MODES}, got {mode!r}")
+    _BACKWARD_MODE = mode
 
 
 def set_reference_backward(flag: bool) -> None:
-    """Ignore the cotangent of the tangent output in backward, as the reference does."""
-    global _REFERENCE_BACKWARD
-    _REFERENCE_BACKWARD = bool(flag)
+    """True: ``set_backward_mode("reference")``; False: ``set_backward_mode("full")``."""
+    set_backward_mode("reference" if flag else "full")
 
 
 _HEAD_DIMS = {16, 32, 64, 128, 256}
@@ -269,20 +285,36 @@ class _attention(torch.autograd.Function):
         # (not zeros), so an unused `to` keeps the dO-only kernel
         ctx.set_materialize_grads(False)
         o, to, lse, mu = torch.ops.dmad.flash_attn_jvp_fwd(q, k, v, tq, tk, tv, float(sm_scale))
+        # the full derivative needs the tangent side; otherwise keep only what the
+        # reference keeps (q, k, v, o, LSE: :500-502), so tangent activations and
+        # `to` are not held until the backward
+        full = _BACKWARD_MODE == "full" or (_BACKWARD_MODE == "auto" and tangent_grad)
         if is_grad or tangent_grad:
-            ctx.save_for_backward(q, k, v, tq, tk, tv, o, to, lse, mu)
+            if full:
+                ctx.save_for_backward(q, k, v, tq, tk, tv, o, to, lse, mu)
+            else:
+                ctx.save_for_backward(q, k, v, o, lse)
+            ctx.full = full
             ctx.sm_scale = float(sm_scale)
             ctx.tangent_grad = tangent_grad
         return o, to
 
     @staticmethod
     def backward(ctx, dout, dto):
+        if not ctx.full:
+            # the reference's backward: dO-only gradients, the cotangent of `to` ignored (:534-579)
+            q, k, v, o, lse = ctx.saved_tensors
+            assert q.shape[-1] == k.shape[-1] and k.shape[-1] == v.shape[-1], (
+                "Backward not supported with different headdim."
+            )
+            if dout is None:
+                return (None,) * 8
+            dq, dk, dv = torch.ops.dmad.flash_attn_bwd(dout, q, k, v, o, lse, ctx.sm_scale)
+            return dq, dk, dv, None, None, None, None, None
         q, k, v, tq, tk, tv, o, to, lse, mu = ctx.saved_tensors
         assert q.shape[-1] == k.shape[-1] and k.shape[-1] == v.shape[-1], (
             "Backward not supported with different headdim."
         )
-        if _REFERENCE_BACKWARD:
-            dto = None
         if dout is None and dto is None:
             return (None,) * 8
         if dout is None:

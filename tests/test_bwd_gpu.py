@@ -50,7 +50,7 @@ def _grad_run(dev, xs, sm_scale, use_dto, tangent_grad):
         loss = loss + (to.float() * dto.float()).sum()
     loss.backward()
     torch.cuda.synchronize()
-    return [x.grad.cpu() for x in leaves]
+    return [None if x.grad is None else x.grad.cpu() for x in leaves]
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -106,8 +106,19 @@ def test_full_backward_with_tangent_grads(gpu, shape, dtype):
     assert max(errs) <= 1e-2
 
 
+@pytest.fixture
+def backward_mode():
+    """Sets dmad_amd's backward mode for one test and restores the default."""
+    from dmad_amd import set_backward_mode
+
+    yield set_backward_mode
+    set_backward_mode("auto")
+
+
 @pytest.mark.parametrize("shape", [(1, 2, 999, 999, 128), (1, 3, 200, 130, 64)])
-def test_full_backward_without_tangent_grads(gpu, shape):
+def test_full_backward_without_tangent_grads(gpu, shape, backward_mode):
+    """Mode "full": the cotangent of `to` reaches q, k, v although no tangent requires grad."""
+    backward_mode("full")
     xs = _case(shape, torch.bfloat16, tstd=0.1)
     got = _grad_run(gpu, xs, None, use_dto=True, tangent_grad=False)
     ref = orc.grads_full(*(x.double() for x in xs), sm_scale=shape[-1] ** -0.5)[:3]
@@ -115,18 +126,17 @@ def test_full_backward_without_tangent_grads(gpu, shape):
     assert max(errs) <= 1e-2, errs
 
 
-def test_reference_backward_switch_ignores_dto(gpu):
-    from dmad_amd import set_reference_backward
-
+@pytest.mark.parametrize("mode,tangent_grad", [("auto", False), ("reference", False), ("reference", True)])
+def test_reference_backward_ignores_dto(gpu, backward_mode, mode, tangent_grad):
+    """The default without tangent grads, and mode "reference" always, give the reference's
+    dO-only gradients (the cotangent of `to` is ignored, tangents get no gradient)."""
+    backward_mode(mode)
     xs = _case((1, 2, 300, 300, 64), torch.bfloat16, tstd=0.1)
-    set_reference_backward(True)
-    try:
-        got = _grad_run(gpu, xs, 0.5, use_dto=True, tangent_grad=False)
-    finally:
-        set_reference_backward(False)
+    got = _grad_run(gpu, xs, 0.5, use_dto=True, tangent_grad=tangent_grad)
     q, k, v, _, _, _, do, _ = (x.double() for x in xs)
     ref = orc.grads_dout_only(q, k, v, do, 0.5)
-    assert max(orc.rel_l2(a, b) for a, b in zip(got, ref)) <= 1e-2
+    assert max(orc.rel_l2(a, b) for a, b in zip(got[:3], ref)) <= 1e-2
+    assert all(g is None for g in got[3:])  # tangents: no gradient, as the reference
 
 
 @pytest.mark.parametrize("D", [16, 32, 256])
