@@ -79,10 +79,12 @@ def test_fake_trace_has_one_node_per_pass(full):
 
 
 @pytest.mark.gpu
-def test_compiled_equals_eager(gpu):
+@pytest.mark.parametrize("tangent_grad", [True, False])
+def test_compiled_equals_eager(gpu, tangent_grad):
     """torch.compile (aot_eager: no generated kernels) traces the op without graph
     breaks and, the kernels being deterministic, reproduces eager bit for bit,
-    gradients included."""
+    gradients included: the full derivative when the tangents require grad, and
+    the reference's dO-only backward (DMAD's case: `to` detached) when not."""
     import torch._dynamo
 
     torch._dynamo.reset()
@@ -92,17 +94,24 @@ def test_compiled_equals_eager(gpu):
 
     def run(f):
         xs = _leaves((1, 2, 200, 128), 8, 3, device=gpu)
+        if not tangent_grad:
+            xs = [x.detach() if 3 <= i < 6 else x for i, x in enumerate(xs)]
         o, to = f(*xs[:6])
-        ((o.float() * xs[6].float()).sum() + (to.float() * xs[7].float()).sum()).backward()
+        loss = (o.float() * xs[6].float()).sum()
+        if tangent_grad:
+            loss = loss + (to.float() * xs[7].float()).sum()
+        loss.backward()
         torch.cuda.synchronize()
-        return xs, (o.detach(), to.detach(), *(x.grad for x in xs[:6]))
+        n = 6 if tangent_grad else 3
+        return xs, (o.detach(), to.detach(), *(x.grad for x in xs[:n]))
 
     _, eager = run(fwd)
     xs, compiled = run(torch.compile(fwd, backend="aot_eager", fullgraph=True))
     names = ("o", "to", "dq", "dk", "dv", "dtq", "dtk", "dtv")
     for name, a, b in zip(names, eager, compiled):
         assert torch.equal(a, b), name
-    ref = orc.grads_full(*(x.detach().double().cpu() for x in xs))
+    x64 = [x.detach().double().cpu() for x in xs]
+    ref = orc.grads_full(*x64) if tangent_grad else orc.grads_dout_only(x64[0], x64[1], x64[2], x64[6])
     for name, got, r in zip(names[2:], compiled[2:], ref):
         assert orc.rel_l2(got.cpu(), r) <= 1e-2, name
 
