@@ -258,13 +258,14 @@ __global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void attn_fwd32_kernel(FwdPa
     }
   }
   const f32x16_t zero16 = {};
-  // O~, C~ accumulation. In the dense JVP mode the accumulators stay in AGPRs
-  // through inline MFMAs, which frees the VGPRs for the score tiles and the
-  // softmax (0.6-1% faster); measured slower for the block-sparse variant (3%),
-  // and the plain forward keeps them in VGPRs, where it fits two waves per SIMD.
-  // Code that touches AGPR accumulators with the VALU (the rescale, the
-  // epilogue) waits for the MFMAs first.
-  constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI && DH == 128;
+  // O~, C~ accumulation. In the dense bf16 JVP mode for 128-wide heads the
+  // accumulators stay in AGPRs through inline MFMAs, which frees the VGPRs for
+  // the score tiles and the softmax (0.6-1% faster). Measured slower for the
+  // block-sparse variant (3%) and for fp16 (6%: 59.8 against 56.3 ms at the
+  // Wan2.1-14B shape); the plain forward keeps them in VGPRs, where it fits two
+  // waves per SIMD. Code that touches AGPR accumulators with the VALU (the
+  // rescale, the epilogue) waits for the MFMAs first.
+  constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI && DH == 128 && !__is_same(T, _Float16);
   auto acc_mfma = [&](f32x16_t& c, i32x4_t a, i32x4_t b) {
     if constexpr (kAccAgpr) mfma32_acc(c, a, b, T());
     else c = mfma32(a, b, c, T());
