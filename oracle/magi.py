@@ -9,13 +9,20 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
   (first block ``first_chunk_frames`` frames, the rest ``chunk_frames``),
   block-causal with an optional sliding window and sink, or teacher forcing on
   a packed [clean][noisy] sequence. It does not use the range tables, so it
-  checks them.
+  checks them. ``as_range_builder=True`` switches the one rule where the
+  reference's range builder differs from its test mask (teacher forcing,
+  1-block window, sink: noisy queries get no sink).
 * ``masked_jvp``        -- (O, Od, LSE, mu) of attention restricted to a boolean
   mask, closed form in float64: P = softmax over the allowed keys,
   Sd = s (Qd K^T + Q Kd^T), mu = rowsum(P Sd), Od = P Vd + (P (Sd - mu)) V.
   A row with no allowed key gets O = Od = 0, LSE = -inf, mu = 0 (what
   ``_attn_fwd_magi``'s epilogue gives for l_i == 0, :386-400).
 * ``masked_jvp_rows``   -- the same for a subset of query rows.
+* ``random_rectangles`` -- a seeded random mask as the reference's builder takes
+  it (``prepare_magi_csr_and_tasks``, train/wan/rcm/utils/magimask.py:265-283):
+  the query axis cut into groups, each with 1-4 key ranges that may overlap,
+  touch or reach outside [0, KV), rows shuffled; the [Q, KV] mask is the union
+  of the clipped rectangles, painted straight from the raw ranges.
 * ``magi_fwd_emulator`` -- the numerics of ``_attn_fwd_magi`` (:242-409): per
   query group, key tiles of BLOCK_N walking each range from the tile boundary
   below its start, keys outside the range at -inf (tangent scores at 0),
@@ -28,7 +35,8 @@ range tables describe for a sweep of schedules; ``masked_jvp`` by
 ``torch.func.jvp`` of masked math attention, by the dense closed form when
 everything is allowed, by per-row brute force and the empty-row case;
 ``magi_fwd_emulator`` by ``masked_jvp`` in float64 without rounding, for
-several BLOCK_N.
+several BLOCK_N; ``random_rectangles`` by hand-painted masks of small draws
+(every row's rectangle, and nothing else, is set).
 """
 from __future__ import annotations
 
@@ -50,8 +58,16 @@ def _block_of(tok: np.ndarray, ft: int, first: int, chunk: int, use_first: bool)
 
 def allowed_mask(mode: str, frame_tokens: int, Q: int, KV: int, first_chunk_frames: int = 1, chunk_frames: int = 1,
                  q_block_offset: int = 0, local_attn_blocks: int = 0, sink_blocks: int = 0,
-                 clean_blocks: int = 0) -> torch.Tensor:
-    """[Q, KV] bool: which keys each query may attend to."""
+                 clean_blocks: int = 0, as_range_builder: bool = False) -> torch.Tensor:
+    """[Q, KV] bool: which keys each query may attend to.
+
+    The reference states teacher forcing twice, and the two differ in one case:
+    with ``local_attn_blocks == 1`` and a sink, its boolean test mask
+    (flash_attention_jvp_triton.py:850-853) lets noisy queries see the sink
+    blocks, while its range builder (train/wan/rcm/utils/magimask.py:98-104)
+    adds a noisy block's sink only together with a non-empty window of earlier
+    clean blocks, which a 1-block window never has. The kernels run on the range
+    builder's tables, so ``as_range_builder=True`` gives that rule."""
     ft, first, chunk = frame_tokens, first_chunk_frames, chunk_frames
     q = np.arange(Q)[:, None]
     kv = np.arange(KV)[None, :]
@@ -80,7 +96,8 @@ def allowed_mask(mode: str, frame_tokens: int, Q: int, KV: int, first_chunk_fram
         noisy_own = ~q_clean & ~k_clean & (kb_n == qb_n)
         ok = clean_ok | noisy_prev | noisy_own
         if sink_blocks > 0:
-            ok |= ~q_clean & k_clean & (kb_c < sink_blocks) & (kb_c < qb_n)
+            if not (as_range_builder and window == 0):
+                ok |= ~q_clean & k_clean & (kb_c < sink_blocks) & (kb_c < qb_n)
             ok |= q_clean & k_clean & (kb_c < sink_blocks) & (kb_c < qb_c)
         ok = ok | (q == kv)
         return torch.from_numpy(np.broadcast_to(ok, (Q, KV)).copy())
@@ -108,6 +125,35 @@ def masked_jvp_rows(q, k, v, tq, tk, tv, allow, rows, sm_scale):
     """masked_jvp for the query rows `rows` only (float64)."""
     idx = torch.as_tensor(rows, dtype=torch.long)
     return masked_jvp(q[..., idx, :], k, v, tq[..., idx, :], tk, tv, allow[idx], sm_scale)
+
+
+def random_rectangles(seed: int, Q: int, KV: int, max_groups: int = 6):
+    """(q_ranges [R,2], k_ranges [R,2] int32, allow [Q,KV] bool) of a random mask
+    whose query groups partition [0, Q) and each have at least one key in range."""
+    rng = np.random.default_rng(seed)
+    n_groups = int(rng.integers(1, min(max_groups, Q) + 1))
+    cuts = np.sort(rng.choice(np.arange(1, Q), size=n_groups - 1, replace=False)) if n_groups > 1 else np.array([], int)
+    bounds = [0] + [int(c) for c in cuts] + [Q]
+    rows = []
+    allow = np.zeros((Q, KV), dtype=bool)
+    for q0, q1 in zip(bounds[:-1], bounds[1:]):
+        a = int(rng.integers(0, KV))
+        spans = [(a, int(rng.integers(a + 1, KV + 1)))]  # one range inside [0, KV)
+        for _ in range(int(rng.integers(0, 4))):
+            kind = int(rng.integers(0, 3))
+            if kind == 0 and spans:  # touching the previous range
+                b0 = spans[-1][1]
+                spans.append((b0, b0 + int(rng.integers(1, KV // 3 + 2))))
+            else:  # anywhere, possibly before 0 or past KV
+                a = int(rng.integers(-KV // 4 - 1, KV + KV // 4 + 1))
+                spans.append((a, a + int(rng.integers(1, KV // 2 + 2))))
+        for a, b in spans:
+            rows.append((q0, q1, a, b))
+            if max(a, 0) < min(b, KV):  # a range wholly outside [0, KV) adds nothing
+                allow[q0:q1, max(a, 0):min(b, KV)] = True
+    rows = [rows[i] for i in rng.permutation(len(rows))]
+    arr = torch.tensor(rows, dtype=torch.int32).reshape(-1, 4)
+    return arr[:, :2].contiguous(), arr[:, 2:].contiguous(), torch.from_numpy(allow)
 
 
 def _round(x, dtype):

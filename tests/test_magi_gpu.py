@@ -5,8 +5,10 @@ Cases: the reference's own test_jvp_magi grid (flash_attention_jvp_triton.py:
 and 64/128, fp16 and bf16, masks built with BLOCK_M = 64, plus the sliding
 window + sink case), 128-wide heads (the production kernel's block-sparse
 variant) with block edges off the 32-key and 128-query grids, batch and heads
-> 1, the zero-K/V-tangent mode, and hand-made tables: a group without keys,
-ranges reaching outside the sequences, and rows no task covers.
+> 1, the zero-K/V-tangent mode, hand-made tables (a group without keys, ranges
+reaching outside the sequences, rows no task covers), a seeded sweep of
+schedules (frame and block sizes, windows, sinks, query block offsets) and
+seeded masks given as raw overlapping rectangles.
 
 Bar: relative L2 <= 1e-2 against the float64 masked closed form, no worse than
 the reference kernel's numerics (oracle.magi.magi_fwd_emulator, BLOCK_N 64) plus
@@ -25,17 +27,19 @@ from oracle import magi as om
 pytestmark = pytest.mark.gpu
 
 
-def _spec(mode, ft, nb, first=1, chunk=1, local=0, sink=0):
+def _spec(mode, ft, nb, first=1, chunk=1, local=0, sink=0, q_bo=0):
     pat = mm.BlockPattern(frame_tokens=ft, first_chunk_frames=first, chunk_frames=chunk)
     if mode == "block_causal":
-        Q = KV = pat.blocks_to_tokens(nb)
-        spec = mm.AttnMaskSpec(mode=mode, pattern=pat, local_attn_blocks=local, sink_blocks=sink)
-        allow = om.allowed_mask(mode, ft, Q, KV, first, chunk, local_attn_blocks=local, sink_blocks=sink)
+        KV = pat.blocks_to_tokens(q_bo + nb)
+        Q = KV - pat.blocks_to_tokens(q_bo) if q_bo else KV
+        spec = mm.AttnMaskSpec(mode=mode, pattern=pat, q_block_offset=q_bo, local_attn_blocks=local, sink_blocks=sink)
+        allow = om.allowed_mask(mode, ft, Q, KV, first, chunk, q_block_offset=q_bo, local_attn_blocks=local,
+                                sink_blocks=sink)
     else:
         Q = KV = 2 * pat.blocks_to_tokens(nb)
         spec = mm.AttnMaskSpec(mode=mode, pattern=pat, clean_blocks=nb, local_attn_blocks=local, sink_blocks=sink)
         allow = om.allowed_mask(mode, ft, Q, KV, first, chunk, local_attn_blocks=local, sink_blocks=sink,
-                                clean_blocks=nb)
+                                clean_blocks=nb, as_range_builder=True)
     return spec, Q, KV, allow
 
 
@@ -114,6 +118,58 @@ def test_wide_heads(gpu, case, dtype):
     qr, kr = mm.make_magi_ranges_full(spec, Q_real=Q, KV_real=KV, device=gpu)
     mask = mm.prepare_magi_csr_and_tasks(qr, kr, Q_real=Q, KV_real=KV)
     _check(_inputs(B, H, Q, KV, 128, 128, dtype, seed=7), gpu, mask, allow, 128 ** -0.5, dtype)
+
+
+def _sweep(n, seed):
+    g = torch.Generator().manual_seed(seed)
+
+    def pick(xs):
+        return xs[int(torch.randint(len(xs), (1,), generator=g))]
+
+    def rint(lo, hi):
+        return int(torch.randint(lo, hi + 1, (1,), generator=g))
+
+    out = []
+    for i in range(n):
+        mode = pick(["block_causal", "teacher_forcing"])
+        out.append(dict(mode=mode, ft=rint(3, 48), nb=rint(2, 5), first=rint(1, 2), chunk=rint(1, 3),
+                        local=pick([0, 0, 1, 2, 3]), sink=rint(0, 2),
+                        q_bo=pick([0, 1, 2]) if mode == "block_causal" else 0, B=rint(1, 2), H=rint(1, 3),
+                        dims=pick([(128, 128), (64, 64), (64, 128)]), block_m=pick([64, 128]),
+                        dtype=pick([torch.bfloat16, torch.float16]), seed=300 + i))
+    return out
+
+
+@pytest.mark.parametrize("c", _sweep(12, 77), ids=lambda c: "{mode}-ft{ft}-nb{nb}-bo{q_bo}-d{dims[0]}".format(**c))
+def test_pattern_sweep(gpu, c):
+    """Seeded schedules: frame sizes off every tile grid, 1-2 frame first blocks,
+    1-3 frame blocks, windows and sinks, a query block offset (block-causal
+    queries that start past the first blocks), tables built at BLOCK_M 64 or 128.
+    The mask comes from the oracle's allowed_mask (with the range builder's rule
+    for a 1-block teacher-forcing window), not from the range tables."""
+    print(f"case {c}", flush=True)
+    dqk, dv = c["dims"]
+    spec, Q, KV, allow = _spec(c["mode"], c["ft"], c["nb"], c["first"], c["chunk"], c["local"], c["sink"], c["q_bo"])
+    qr, kr = mm.make_magi_ranges_full(spec, Q_real=Q, KV_real=KV, device=gpu)
+    mask = mm.prepare_magi_csr_and_tasks(qr, kr, Q_real=Q, KV_real=KV, BLOCK_M=c["block_m"])
+    xs = _inputs(c["B"], c["H"], Q, KV, dqk, dv, c["dtype"], seed=c["seed"])
+    _check(xs, gpu, mask, allow, dqk ** -0.5, c["dtype"])
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_rectangles(gpu, seed):
+    """Masks given as raw rectangles: query groups of random lengths, each with
+    1-4 key ranges that overlap, touch or reach outside [0, KV), rows shuffled;
+    the expected mask is painted from the raw rectangles."""
+    g = torch.Generator().manual_seed(500 + seed)
+    Q, KV = (int(x) for x in torch.randint(40, 600, (2,), generator=g))
+    D = (128, 64)[seed % 2]
+    dtype = (torch.bfloat16, torch.float16)[(seed // 2) % 2]
+    print(f"case seed={seed} Q={Q} KV={KV} D={D} dtype={dtype}", flush=True)
+    qr, kr, allow = om.random_rectangles(seed, Q, KV)
+    mask = mm.prepare_magi_csr_and_tasks(qr.to(gpu), kr.to(gpu), Q_real=Q, KV_real=KV)
+    xs = _inputs(1 + seed % 2, 2, Q, KV, D, D, dtype, seed=600 + seed)
+    _check(xs, gpu, mask, allow, D ** -0.5, dtype)
 
 
 @pytest.mark.parametrize("dims", [(128, 128), (64, 64), (128, 32)])

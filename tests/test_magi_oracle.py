@@ -14,6 +14,7 @@
 """
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -74,7 +75,7 @@ def _spec_mask(mode, ft, nb, first=1, chunk=1, local=0, sink=0, q_bo=0):
         Q = KV = 2 * pat.blocks_to_tokens(nb)
         spec = mm.AttnMaskSpec(mode=mode, pattern=pat, clean_blocks=nb, local_attn_blocks=local, sink_blocks=sink)
         ref = om.allowed_mask(mode, ft, Q, KV, first, chunk, local_attn_blocks=local, sink_blocks=sink,
-                              clean_blocks=nb)
+                              clean_blocks=nb, as_range_builder=True)
     return spec, Q, KV, ref
 
 
@@ -82,7 +83,7 @@ SWEEP = [
     (mode, ft, nb, first, chunk, local, sink)
     for mode in ("block_causal", "teacher_forcing")
     for ft, nb, first, chunk in ((1, 5, 1, 1), (3, 4, 1, 2), (5, 3, 2, 1), (16, 4, 1, 1), (7, 6, 1, 3))
-    for local, sink in ((0, 0), (3, 1), (2, 0), (2, 2))
+    for local, sink in ((0, 0), (3, 1), (2, 0), (2, 2), (1, 0), (1, 1), (1, 2))
 ]
 
 
@@ -120,6 +121,29 @@ def test_block_causal_with_query_offset():
     assert torch.equal(mm.csr_to_dense(mask.q_unique, mask.k_flat, mask.qk_map, Q, KV), ref)
 
 
+@pytest.mark.parametrize("first,chunk,sink", [(1, 1, 1), (2, 1, 2), (1, 2, 1), (1, 3, 3)])
+def test_one_block_window_noisy_sink(first, chunk, sink):
+    """Teacher forcing with a 1-block window and a sink: the reference's test mask
+    and its range builder differ by exactly the rectangles noisy block i (i >= 1)
+    x clean keys [0, end of block min(sink, i)), which only the test mask grants."""
+    ft, nb = 3, 4
+    pat = mm.BlockPattern(frame_tokens=ft, first_chunk_frames=first, chunk_frames=chunk)
+    clean = pat.blocks_to_tokens(nb)
+    Q = KV = 2 * clean
+    kw = dict(local_attn_blocks=1, sink_blocks=sink, clean_blocks=nb)
+    test_mask = om.allowed_mask("teacher_forcing", ft, Q, KV, first, chunk, **kw)
+    builder = om.allowed_mask("teacher_forcing", ft, Q, KV, first, chunk, as_range_builder=True, **kw)
+    expect = torch.zeros(Q, KV, dtype=torch.bool)
+    for i in range(1, nb):
+        q0, q1 = clean + pat.blocks_to_tokens(i), clean + pat.blocks_to_tokens(i + 1)
+        expect[q0:q1, :pat.blocks_to_tokens(min(sink, i))] = True
+    assert torch.equal(test_mask & ~builder, expect) and not (builder & ~test_mask).any()
+    spec = mm.AttnMaskSpec(mode="teacher_forcing", pattern=pat, **kw)
+    qr, kr = mm.make_magi_ranges_full(spec, Q_real=Q, KV_real=KV, device="cpu")
+    mask = mm.prepare_magi_csr_and_tasks(qr, kr, Q_real=Q, KV_real=KV)
+    assert torch.equal(mm.csr_to_dense(mask.q_unique, mask.k_flat, mask.qk_map, Q, KV), builder)
+
+
 def test_merge_clips_sorts_and_merges():
     qr = torch.tensor([[5, 9], [0, 5], [5, 9], [0, 5], [5, 9], [0, 5]], dtype=torch.int32)
     kr = torch.tensor([[8, 12], [-3, 2], [0, 3], [2, 4], [3, 5], [20, 30]], dtype=torch.int32)
@@ -132,6 +156,29 @@ def test_merge_clips_sorts_and_merges():
         mm.merge_k_ranges(torch.tensor([[0, 4]]), torch.tensor([[12, 14]]), KV_real=10)
     with pytest.raises(AssertionError):
         mm.prepare_magi_csr_and_tasks(torch.tensor([[0, 4], [5, 8]]), torch.tensor([[0, 1], [0, 1]]), 8, 8)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_rectangles_build_their_mask(seed):
+    """Random overlapping / touching / out-of-range key ranges: the generator's mask
+    is the element-wise union of the raw rectangles, and the CSR tables the builder
+    makes from the shuffled rows describe exactly that mask."""
+    g = np.random.default_rng(1000 + seed)
+    Q, KV = int(g.integers(1, 300)), int(g.integers(1, 300))
+    qr, kr, allow = om.random_rectangles(seed, Q, KV)
+    qi, kj = np.arange(Q)[None, :, None], np.arange(KV)[None, None, :]
+    q0, q1 = qr[:, 0].numpy()[:, None, None], qr[:, 1].numpy()[:, None, None]
+    k0, k1 = kr[:, 0].numpy()[:, None, None], kr[:, 1].numpy()[:, None, None]
+    member = ((qi >= q0) & (qi < q1) & (kj >= k0) & (kj < k1)).any(0)
+    assert np.array_equal(allow.numpy(), member)
+    assert allow.any(1).all()  # every query row has a key
+    for block_m in (64, 128):
+        mask = mm.prepare_magi_csr_and_tasks(qr, kr, Q_real=Q, KV_real=KV, BLOCK_M=block_m)
+        assert torch.equal(mm.csr_to_dense(mask.q_unique, mask.k_flat, mask.qk_map, Q, KV), allow)
+        qm, kf = mask.qk_map.numpy(), mask.k_flat.numpy()
+        for grp in range(mask.G):
+            segs = kf[qm[grp]:qm[grp + 1]]
+            assert (segs[:, 0] >= 0).all() and (segs[:, 1] <= KV).all() and (segs[1:, 0] > segs[:-1, 1]).all()
 
 
 def test_tasks_for_kernel_rebuilds_other_block_m():
