@@ -2,7 +2,8 @@
 queries and keys, lengths just off the 32/64/128 tile grids, logits large
 enough that the online softmax rescales on almost every tile, inputs with no
 query rows, and a seeded sweep of random shapes, head dims, dtypes and
-layouts (BHSD contiguous or BSHD views, as the Wan callers pass them).
+layouts (BHSD contiguous or BSHD views, as the Wan callers pass them), and
+bitwise-equal repeat runs (no atomics, fixed reduction order).
 
 Bar: rel-L2 <= 1e-2 on O, Ȯ and every gradient (the reference's own tests
 use atol/rtol 1e-2), with an absolute bound where the exact value is zero.
@@ -152,3 +153,27 @@ def test_random_shapes(gpu, c):
     print(f"case {c}", flush=True)
     xs = _case(c["B"], c["H"], c["Lq"], c["Lk"], c["D"], dtype=c["dtype"], seed=c["seed"], bshd=c["bshd"])
     _check(xs, _gpu_run(gpu, xs, c["full"]), c["full"])
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_repeat_runs_are_bitwise_equal(gpu, D):
+    """No kernel uses atomics and every reduction has a fixed order: two runs of the
+    forward and of both backward modes on the same inputs agree bit for bit, and
+    so does the block-sparse forward."""
+    from dmad_amd import attention
+    from dmad_amd import magimask as mm
+
+    print(f"case repeat D={D}", flush=True)
+    xs = _case(1, 4, 2100, 2100, D, seed=31)
+    for full in (False, True):
+        a, b = _gpu_run(gpu, xs, full), _gpu_run(gpu, xs, full)
+        for name, x, y in zip(("o", "to", "dq", "dk", "dv", "dtq", "dtk", "dtv"), a, b):
+            assert torch.equal(x, y), (full, name)
+    pat = mm.BlockPattern(frame_tokens=300, first_chunk_frames=1, chunk_frames=2)
+    spec = mm.AttnMaskSpec(mode="block_causal", pattern=pat, local_attn_blocks=2, sink_blocks=1)
+    qr, kr = mm.make_magi_ranges_full(spec, Q_real=2100, KV_real=2100, device=gpu)
+    mask = mm.prepare_magi_csr_and_tasks(qr, kr, Q_real=2100, KV_real=2100)
+    g = [x.to(gpu) for x in xs[:6]]
+    r1, r2 = attention(*g, None, mask), attention(*g, None, mask)
+    torch.cuda.synchronize()
+    assert torch.equal(r1[0], r2[0]) and torch.equal(r1[1], r2[1])
