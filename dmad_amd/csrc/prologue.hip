@@ -15,10 +15,12 @@
 //
 // One wave per row: lane l owns the 16-byte chunks l, l+64, l+128, ... of the
 // row, so every load and store instruction moves whole 1 KiB row segments.
-// A chunk's position inside its head is the same for all of a lane's chunks
-// (64 chunks span whole heads for D <= 512), so each lane computes the sine
-// and cosine of its 4 angles once per row. HBM-bound: per row 2C (or 4C with
-// the tangent) bytes in and out, the weight and angles from cache.
+// Chunk c sits at position c mod (D/8) inside its head. When D/8 divides 64
+// (D = 8, 16, 32, 64, 128, 256, 512) that position is the same for all of a
+// lane's chunks, so each lane computes the sine and cosine of its 4 angles
+// once per row; for other head dims (D = 24, 40, 96, ...) the angles are
+// recomputed per chunk. HBM-bound: per row 2C (or 4C with the tangent) bytes
+// in and out, the weight and angles from cache.
 #include "launch.h"
 
 namespace dmad {
@@ -69,14 +71,19 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
     rd = -0.5f * (r * r * r) * (2.0f * sd * p.inv_c);
   }
 
-  // rotation angles of this lane's 4 pairs: i = 4 (lane mod D/8) + k
+  // rotation angles of the 4 pairs of chunk c: i = 4 (c mod D/8) + k
   float cs[4], sn[4];
-  if constexpr (ROPE) {
-    const int l = (int)(row % p.L);
-    const int i0 = 4 * (lane % (p.D >> 3));
-    const float* f = p.freqs + (int64_t)l * (p.D >> 1) + i0;
+  const int cpd = p.D >> 3;                  // chunks per head
+  const bool same_pos = (64 % cpd) == 0;     // every chunk of a lane at one in-head position
+  const float* frow = nullptr;
+  auto angles = [&](int c) {
+    const float* f = frow + 4 * (c % cpd);
 #pragma unroll
     for (int k = 0; k < 4; ++k) sincosf(f[k], &sn[k], &cs[k]);
+  };
+  if constexpr (ROPE) {
+    frow = p.freqs + (int64_t)(row % p.L) * (p.D >> 1);
+    angles(lane);
   }
 
   char* orow = (char*)p.out + row * p.o_stride * 2;
@@ -104,6 +111,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
       }
     }
     if constexpr (ROPE) {
+      if (j > 0 && !same_pos) angles(c);  // wave-uniform branch
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float xe = q[2 * k], xo = q[2 * k + 1];

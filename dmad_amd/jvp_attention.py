@@ -61,6 +61,37 @@ def set_reference_backward(flag: bool) -> None:
 
 _HEAD_DIMS = {16, 32, 64, 128, 256}
 
+# Largest head dim the full-derivative backward kernels are built for.
+FULL_BWD_MAX_HEAD_DIM = 128
+_warned_full_fallback = False
+
+
+def _full_backward_unavailable(dqk: int, dv: int) -> bool:
+    """Backward mode for head dims the full derivative does not cover.
+
+    Mode "auto" falls back to the reference's backward (dO-only gradients, None
+    for the tangents, :534-579) with a one-time warning, so the op runs wherever
+    the reference runs; mode "full" asked for the full derivative explicitly and
+    raises here, in the forward, before any work is done.
+    """
+    global _warned_full_fallback
+    if _BACKWARD_MODE == "full":
+        raise NotImplementedError(
+            f"the full-derivative backward supports head dims up to {FULL_BWD_MAX_HEAD_DIM} "
+            f"(got Dqk={dqk}, Dv={dv}); use set_backward_mode('auto') or ('reference') for the "
+            "reference's dO-only gradients"
+        )
+    if not _warned_full_fallback:
+        import warnings
+
+        warnings.warn(
+            f"head dim {max(dqk, dv)} > {FULL_BWD_MAX_HEAD_DIM}: the tangents get no gradients and the "
+            "cotangent of `to` is ignored (the reference backward's behaviour)",
+            stacklevel=3,
+        )
+        _warned_full_fallback = True
+    return False
+
 
 def _kernel_ready(t: torch.Tensor) -> bool:
     """Unit inner stride, 16-byte aligned rows (what the kernels load from)."""
@@ -281,14 +312,16 @@ class _attention(torch.autograd.Function):
             o, to, _, _ = jvp_attention_forward_magi(q, k, v, tq, tk, tv, sm_scale, magi_mask)
             return o, to
         tangent_grad = any(x is not None and x.requires_grad for x in (tq, tk, tv))
-        # an output that does not reach the loss arrives in backward as None
-        # (not zeros), so an unused `to` keeps the dO-only kernel
-        ctx.set_materialize_grads(False)
-        o, to, lse, mu = torch.ops.dmad.flash_attn_jvp_fwd(q, k, v, tq, tk, tv, float(sm_scale))
         # the full derivative needs the tangent side; otherwise keep only what the
         # reference keeps (q, k, v, o, LSE: :500-502), so tangent activations and
         # `to` are not held until the backward
         full = _BACKWARD_MODE == "full" or (_BACKWARD_MODE == "auto" and tangent_grad)
+        if full and (is_grad or tangent_grad) and max(HEAD_DIM_QK, HEAD_DIM_V) > FULL_BWD_MAX_HEAD_DIM:
+            full = _full_backward_unavailable(HEAD_DIM_QK, HEAD_DIM_V)
+        # an output that does not reach the loss arrives in backward as None
+        # (not zeros), so an unused `to` keeps the dO-only kernel
+        ctx.set_materialize_grads(False)
+        o, to, lse, mu = torch.ops.dmad.flash_attn_jvp_fwd(q, k, v, tq, tk, tv, float(sm_scale))
         if is_grad or tangent_grad:
             if full:
                 ctx.save_for_backward(q, k, v, tq, tk, tv, o, to, lse, mu)

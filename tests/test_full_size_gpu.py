@@ -57,6 +57,28 @@ def oracle_bwd_head(q, k, v, do, h, sm_scale):
     return torch.cat(dqs, 0), dk, dv
 
 
+def oracle_full_bwd_head(x, h, sm_scale, tangents=True):
+    """Oracle full derivative (dQ, dK, dV, dQd, dKd, dVd) of head h (oracle.grads_full),
+    float32, query-chunked: every row statistic (LSE, mu, rho, D') is row-local,
+    dQ, dQd are row-local and dK, dV, dKd, dVd are sums over query rows."""
+    qh, kh, vh, tqh = (_head(x[n], h) for n in ("q", "k", "v", "tq"))
+    tkh = _head(x["tk"], h) if tangents else torch.zeros_like(kh)
+    tvh = _head(x["tv"], h) if tangents else torch.zeros_like(vh)
+    doh, dtoh = _head(x["do"], h), _head(x["dto"], h)
+    rows = [[], []]
+    cols = [torch.zeros_like(kh), torch.zeros_like(vh), torch.zeros_like(kh), torch.zeros_like(vh)]
+    for c in range(0, qh.shape[0], CHUNK):
+        sl = slice(c, c + CHUNK)
+        dq, dk, dv, dtq, dtk, dtv = orc.grads_full(qh[sl], kh, vh, tqh[sl], tkh, tvh, doh[sl], dtoh[sl],
+                                                   sm_scale=sm_scale)
+        rows[0].append(dq)
+        rows[1].append(dtq)
+        for acc, part in zip(cols, (dk, dv, dtk, dtv)):
+            acc += part
+    dq, dtq = torch.cat(rows[0], 0), torch.cat(rows[1], 0)
+    return dq, cols[0], cols[1], dtq, cols[2], cols[3]
+
+
 def fa2_floor_head(q, k, v, do, h, sm_scale):
     """The reference backward's numerics (oracle.fa2_bwd_emulator, bf16 rounding of P
     and dS) for head h, float32, query-chunked the same way."""
@@ -133,6 +155,40 @@ def _check_bwd(dq, dk, dv, q, k, v, do, heads, sm_scale):
     assert r_v <= 2e-2 and r_k <= 2e-2 and r_qk <= 2e-2
 
 
+def _check_bwd_full(grads, x, heads, sm_scale, tangents=True):
+    """The full derivative against the chunked oracle on `heads`; on every head the
+    identities that hold for it at any size:
+      sum_j dV_j = sum_i dO_i, sum_j dVd_j = sum_i dOd_i  (rows of P sum to one,
+          rows of Pd = P*(Sd - mu) to zero),
+      sum_j dK_j = 0, sum_j dKd_j = 0  (rows of dS and dSd sum to zero),
+      <dQ,Q> + <dQd,Qd> = <dK,K> + <dKd,Kd>  ((Q, Qd, K, Kd) -> (aQ, aQd, K/a, Kd/a)
+          leaves S and Sd unchanged)."""
+    names = ("dq", "dk", "dv", "dtq", "dtk", "dtv")
+    for h in heads:
+        ref = oracle_full_bwd_head(x, h, sm_scale, tangents=tangents)
+        e = {n: _rel(g[0, h], r) for n, g, r in zip(names, grads, ref)}
+        print(f"  head {h}: rel-L2 " + " ".join(f"{n} {v:.2e}" for n, v in e.items()), flush=True)
+        assert max(e.values()) <= 1e-2, e
+    dq, dk, dv, dtq, dtk, dtv = (g.double() for g in grads)
+    q, k, tq = x["q"].double(), x["k"].double(), x["tq"].double()
+    tk = x["tk"].double() if tangents else torch.zeros_like(k)
+    L = k.shape[2]
+
+    def col_sum_err(g, target):
+        rms = g.pow(2).mean(dim=(2, 3)).sqrt()[..., None]
+        return float(((g.sum(2) - target).abs() / (rms * L ** 0.5)).max())
+
+    r = {"sum dV - sum dO": col_sum_err(dv, x["do"].double().sum(2)),
+         "sum dVd - sum dOd": col_sum_err(dtv, x["dto"].double().sum(2)),
+         "sum dK": col_sum_err(dk, 0.0), "sum dKd": col_sum_err(dtk, 0.0)}
+    lhs = (dq * q).sum(dim=(2, 3)) + (dtq * tq).sum(dim=(2, 3))
+    rhs = (dk * k).sum(dim=(2, 3)) + (dtk * tk).sum(dim=(2, 3))
+    scale = (dq.pow(2).sum(dim=(2, 3)) * q.pow(2).sum(dim=(2, 3))).sqrt()
+    r["<dQ,Q>+<dQd,Qd> - <dK,K>-<dKd,Kd>"] = float(((lhs - rhs).abs() / scale).max())
+    print("  identities (all heads): " + "  ".join(f"{n} {v:.2e}" for n, v in r.items()), flush=True)
+    assert max(r.values()) <= 2e-2, r
+
+
 def _run(x, tangents=True, backward=False):
     from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
 
@@ -161,6 +217,39 @@ def test_wan13b_self_attention_full_size(gpu):
     _check_bwd(dq, dk, dv, x["q"], x["k"], x["v"], x["do"], heads=(0, 11), sm_scale=s)
 
 
+def test_wan13b_self_attention_full_derivative_full_size(gpu):
+    """BASELINE config 3 at its size: the 1.3B self-attention (H=12, L=32760, RMSNorm + 3D
+    RoPE Q/K) with both cotangents, dO ~ N(0,1) and dOd ~ N(0,0.1^2), and every input
+    requiring grad: the full derivative dQ, dK, dV, dQd, dKd, dVd."""
+    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+
+    print("case wan1.3b self fwd+JVP+full bwd", flush=True)
+    x = make_inputs(1, 12, 32760, 32760, 128, seed=0, device=gpu, grid=(21, 30, 52), with_grads=True, gen_device=gpu)
+    q, k, v, tq, tk, tv = (x[n] for n in ("q", "k", "v", "tq", "tk", "tv"))
+    s = 128 ** -0.5
+    o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+    grads = jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, x["do"], x["dto"], s, True)
+    torch.cuda.synchronize()
+    assert all(g is not None for g in grads)
+    _check_bwd_full(grads, x, heads=(0, 11), sm_scale=s)
+
+
+def test_wan13b_cross_attention_full_size(gpu):
+    """The 1.3B text cross-attention of config 3: H=12, 32760 queries over 512 keys,
+    Kd = Vd = 0 (wan2pt1_jvp.py:366-372); forward+JVP, then the full derivative with
+    dO and dOd (the gradients of the zero K, V tangents included)."""
+    from dmad_amd.jvp_attention import jvp_attention_backward
+
+    print("case wan1.3b cross fwd+JVP+full bwd", flush=True)
+    x = make_inputs(1, 12, 32760, 512, 128, seed=4, device=gpu, with_grads=True, gen_device=gpu)
+    (o, to, lse, mu), _, s = _run(x, tangents=False)
+    _check_fwd(o, to, lse, mu, x["q"], x["k"], x["v"], x["tq"], None, None, heads=(0, 11), sm_scale=s)
+    grads = jvp_attention_backward(x["q"], x["k"], x["v"], x["tq"], None, None, o, to, lse, mu, x["do"], x["dto"],
+                                   s, True)
+    torch.cuda.synchronize()
+    _check_bwd_full(grads, x, heads=(0, 7), sm_scale=s, tangents=False)
+
+
 def test_wan14b_cross_attention_full_size(gpu):
     """Wan2.1-14B text cross-attention: H=40, 32760 queries over 512 keys, Kd = Vd = 0."""
     print("case wan14b cross fwd+JVP", flush=True)
@@ -170,14 +259,15 @@ def test_wan14b_cross_attention_full_size(gpu):
 
 
 def test_wan14b_720p_self_attention_full_size(gpu):
-    """Wan2.1-14B at 720p: L=75600 (21x45x80 latent), two of the 40 heads' worth of work."""
-    print("case wan14b 720p self fwd+JVP+bwd (H=2)", flush=True)
-    x = make_inputs(1, 2, 75600, 75600, 128, seed=2, device=gpu, grid=(21, 45, 80), with_grads=True, gen_device=gpu)
+    """Wan2.1-14B at 720p, the grid config 5 runs: B=1, H=40, L=75600 (21x45x80 latent);
+    two heads against the oracle, the backward identities on all 40."""
+    print("case wan14b 720p self fwd+JVP+bwd (H=40)", flush=True)
+    x = make_inputs(1, 40, 75600, 75600, 128, seed=2, device=gpu, grid=(21, 45, 80), with_grads=True, gen_device=gpu)
     (o, to, lse, mu), (dq, dk, dv), s = _run(x, backward=True)
     args = (x["q"], x["k"], x["v"], x["tq"], x["tk"], x["tv"])
-    _check_fwd(o, to, lse, mu, *args, heads=(1,), sm_scale=s)
+    _check_fwd(o, to, lse, mu, *args, heads=(1, 39), sm_scale=s)
     _check_rows_against_cpu(o, to, *args, h=0, rows=[0, 1, 4097, 37800, 75598, 75599], sm_scale=s)
-    _check_bwd(dq, dk, dv, x["q"], x["k"], x["v"], x["do"], heads=(0,), sm_scale=s)
+    _check_bwd(dq, dk, dv, x["q"], x["k"], x["v"], x["do"], heads=(0, 26), sm_scale=s)
 
 
 def test_wan14b_self_attention_bench_shape(gpu):

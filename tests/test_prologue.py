@@ -138,6 +138,34 @@ def test_kernel_matches_oracle(gpu, B, L, H, D, grid):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B,L,H,D", [(1, 300, 8, 96), (2, 70, 20, 40), (1, 50, 30, 24), (1, 40, 11, 112)])
+def test_kernel_matches_oracle_odd_head_dims(gpu, B, L, H, D):
+    """Head dims whose 16-byte chunk count D/8 does not divide the 64 lanes of a wave
+    (a lane's chunks then sit at different positions inside their heads, so each
+    chunk needs its own rotation angles), at model dims C = H*D above 512 so that
+    every lane holds more than one chunk."""
+    from dmad_amd import apply_rope_with_tangent, rmsnorm_rope_with_tangent
+
+    print(f"case prologue odd head dim B={B} L={L} H={H} D={D}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(D)
+    C = H * D
+    y = torch.randn(B, L, C, generator=g, device=gpu).to(torch.bfloat16)
+    ty = (torch.randn(B, L, C, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(C, generator=g, device=gpu)).to(torch.bfloat16)
+    freqs = torch.rand(L, D // 2, generator=g, device=gpu) * 40
+    q, tq = rmsnorm_rope_with_tangent((y, ty), w, 1e-6, freqs, H)
+    x = y.view(B, L, H, D)
+    out, tout = apply_rope_with_tangent(x, ty.view(B, L, H, D), freqs)
+    torch.cuda.synchronize()
+    rq, rtq = orp.rmsnorm_rope_jvp(y.cpu(), ty.cpu(), w.cpu(), 1e-6, freqs.cpu(), H)
+    ro, rto = orp.rope_jvp(x.cpu(), ty.view(B, L, H, D).cpu(), freqs.cpu())
+    for got, ref, name in ((q, rq, "q"), (tq, rtq, "q_dot"), (out, ro, "rope"), (tout, rto, "rope_dot")):
+        ulps = _bf16_ulp_ratio(got.cpu(), ref)
+        print(f"  {name}: max {ulps:.2f} ulp")
+        assert ulps <= 2.0, name
+
+
+@pytest.mark.gpu
 def test_kernel_primal_only_and_no_rope(gpu):
     from dmad_amd import rmsnorm_rope_with_tangent
 
