@@ -58,7 +58,15 @@ SIGNATURES = {
                                  _P, _P, _I64P, _P, _P, _P, _P, _I64P,
                                  _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
                                  _F, _P, _SZ, _P]),
+    "dmad_attn_jvp_bwd_noalloc": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64,
+                                         _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
+                                         _P, _P, _I64P, _P, _P, _P, _P, _I64P,
+                                         _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
+                                         _F, _P]),
 }
+
+# Bytes of the static device scratch of dmad_attn_jvp_bwd_noalloc (DMAD_BWD_SCRATCH_BYTES).
+BWD_SCRATCH_BYTES = 64 << 20
 
 
 class DmadError(RuntimeError):

@@ -1,7 +1,9 @@
 // C ABI entry points (include/dmad_attn.h): argument validation, workspace
-// carving and kernel dispatch. Nothing here allocates device memory.
+// carving and kernel dispatch. Nothing here allocates device memory; the
+// allocation-free backward uses this file's static device array `scratch`.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "dmad_attn.h"
@@ -352,86 +354,56 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
   return ok();
 }
 
-}  // namespace
+// Workspace of dmad_attn_jvp_bwd_noalloc: a static device array, one copy per
+// GPU at that GPU's own address, held until the process ends. Host code never
+// uses the name `scratch` as a device address (on the host it is a stand-in
+// object); it uses the address hipGetSymbolAddress returns for the device.
+// Every call on one GPU shares that GPU's copy: calls that overlap on one GPU
+// (two streams, two threads) race. Each call's statistics pass rewrites every
+// byte the backward kernels read before they read it, so nothing needs clearing.
+static __device__ __attribute__((aligned(256))) char scratch[DMAD_BWD_SCRATCH_BYTES];
 
-extern "C" {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
-int dmad_abi_version(void) { return 1; }
-
-const char* dmad_last_error(void) { return g_last_error.c_str(); }
-
-int dmad_set_kernel_events(void* const* events, int count) {
-  if (count < 0 || count > kMaxEvents || (count % 2) != 0)
-    return fail(DMAD_ERR_INVALID, "count must be an even number in [0, %d]", kMaxEvents);
-  if (count > 0 && events == nullptr) return fail(DMAD_ERR_INVALID, "events: null pointer");
-  for (int i = 0; i < count; ++i) g_events[i] = (hipEvent_t)events[i];
-  g_nevents = count;
-  return ok();
+// Device address of `scratch` on the current device, looked up on the first
+// call on each device (that device current) and kept. `stream` must belong to
+// the current device.
+int scratch_of_device(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DMAD_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DMAD_ERR_UNSUPPORTED, "device ordinal %d out of range", dev);
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) return fail(DMAD_ERR_HIP, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(DMAD_ERR_INVALID, "the stream belongs to device %d but device %d is current", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(DMAD_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    if (((uintptr_t)p & 255) != 0) return fail(DMAD_ERR_HIP, "scratch is not 256-byte aligned on device %d", dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DMAD_OK;
 }
 
-int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv,
-                                  size_t* bytes) {
-  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
-  if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
-  if (B < 0 || H < 0 || Lk < 0 || !head_dim_ok(Dqk) || !head_dim_ok(Dv)) return fail(DMAD_ERR_INVALID, "bad sizes");
-  *bytes = (size_t)fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
-  return ok();
-}
-
-int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
-                      const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
-                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4], void* o,
-                      void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale, void* workspace,
-                      size_t workspace_bytes, void* stream) {
-  return fwd_impl(dtype, mode, B, H, Lq, Lk, Dqk, Dv, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to,
-                  o_strides, lse, mu, sm_scale, workspace, workspace_bytes, stream, nullptr);
-}
-
-int dmad_attn_jvp_fwd_magi(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
-                           const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
-                           const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
-                           void* o, void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale,
-                           const int32_t* q_ranges, const int32_t* k_ranges, const int32_t* qk_map, int64_t G,
-                           int64_t R, const int32_t* task_group, const int32_t* task_qtile, int64_t T,
-                           int64_t block_m, void* workspace, size_t workspace_bytes, void* stream) {
-  if (block_m != dmad::kMagiBlockM)
-    return fail(DMAD_ERR_UNSUPPORTED, "tasks must be built for %d-query tiles, got BLOCK_M=%lld", dmad::kMagiBlockM,
-                (long long)block_m);
-  if (G < 1 || R < 0 || T < 0 || G >= ((int64_t)1 << 30) || R >= ((int64_t)1 << 30) || T >= ((int64_t)1 << 30))
-    return fail(DMAD_ERR_INVALID, "bad table sizes G=%lld R=%lld T=%lld", (long long)G, (long long)R, (long long)T);
-  if (q_ranges == nullptr || qk_map == nullptr || (R > 0 && k_ranges == nullptr) ||
-      (T > 0 && (task_group == nullptr || task_qtile == nullptr)))
-    return fail(DMAD_ERR_INVALID, "block-sparse tables: null pointer");
-  const MagiArgs mg{q_ranges, k_ranges, qk_map, task_group, task_qtile, G, R, T};
-  return fwd_impl(dtype, mode, B, H, Lq, Lk, Dqk, Dv, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to,
-                  o_strides, lse, mu, sm_scale, workspace, workspace_bytes, stream, &mg);
-}
-
-int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv, const void* q,
-                  const void* k, const void* v, const int64_t q_strides[4], const int64_t k_strides[4],
-                  const int64_t v_strides[4], void* o, const int64_t o_strides[4], float* lse, float sm_scale,
-                  void* workspace, size_t workspace_bytes, void* stream) {
-  return dmad_attn_jvp_fwd(dtype, DMAD_FWD_PLAIN, B, H, Lq, Lk, Dqk, Dv, q, k, v, nullptr, nullptr, nullptr,
-                           q_strides, k_strides, v_strides, o, nullptr, o_strides, lse, nullptr, sm_scale, workspace,
-                           workspace_bytes, stream);
-}
-
-int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes) {
-  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
-  if (full < 0 || full > 2) return fail(DMAD_ERR_INVALID, "full must be 0, 1 or 2");
-  if (B < 0 || H < 0 || Lq < 0 || Lk < 0 || !head_dim_ok(D)) return fail(DMAD_ERR_INVALID, "bad sizes");
-  *bytes = (size_t)bwd_ws(full, B, H, Lq, Lk, D).total;
-  return ok();
-}
-
-int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
-                      const void* k, const void* v, const void* tq, const void* tk, const void* tv,
-                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
-                      const void* o, const void* to, const int64_t o_strides[4], const float* lse, const float* mu,
-                      const void* dout, const void* dto, const int64_t do_strides[4], void* dq, void* dk, void* dv,
-                      void* dtq, void* dtk, void* dtv, const int64_t dq_strides[4], const int64_t dk_strides[4],
-                      const int64_t dv_strides[4], float sm_scale, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+// Shared body of dmad_attn_jvp_bwd (caller workspace) and
+// dmad_attn_jvp_bwd_noalloc (use_scratch: the device's copy of `scratch`).
+int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q, const void* k,
+             const void* v, const void* tq, const void* tk, const void* tv, const int64_t q_strides[4],
+             const int64_t k_strides[4], const int64_t v_strides[4], const void* o, const void* to,
+             const int64_t o_strides[4], const float* lse, const float* mu, const void* dout, const void* dto,
+             const int64_t do_strides[4], void* dq, void* dk, void* dv, void* dtq, void* dtk, void* dtv,
+             const int64_t dq_strides[4], const int64_t dk_strides[4], const int64_t dv_strides[4], float sm_scale,
+             void* workspace, size_t workspace_bytes, void* stream, bool use_scratch) {
   if (dtype != DMAD_BF16 && dtype != DMAD_F16) return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
   if (B < 0 || H < 0 || Lq < 0 || Lk < 0) return fail(DMAD_ERR_INVALID, "negative size");
   if (!head_dim_ok(D)) return fail(DMAD_ERR_UNSUPPORTED, "head dim must be in {16,32,64,128,256}, got %lld", (long long)D);
@@ -471,6 +443,16 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
   }
   const int fl = full ? (tgrad ? 2 : 1) : 0;
   const BwdWs w = bwd_ws(fl, B, H, Lq, Lk, D);
+  if (use_scratch) {
+    if (w.total > (int64_t)DMAD_BWD_SCRATCH_BYTES)
+      return fail(DMAD_ERR_UNSUPPORTED,
+                  "this backward needs %lld bytes of workspace; the static scratch of dmad_attn_jvp_bwd_noalloc "
+                  "holds %lld (call dmad_attn_jvp_bwd with a workspace instead)",
+                  (long long)w.total, (long long)DMAD_BWD_SCRATCH_BYTES);
+    int rc_s;
+    if ((rc_s = scratch_of_device(stream, &workspace))) return rc_s;
+    workspace_bytes = DMAD_BWD_SCRATCH_BYTES;
+  }
   if (workspace == nullptr || (int64_t)workspace_bytes < w.total)
     return fail(DMAD_ERR_WORKSPACE, "workspace needs %lld bytes, got %lld", (long long)w.total, (long long)workspace_bytes);
   if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
@@ -627,6 +609,105 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
     mark(3, true, s);
   }
   return ok();
+}
+
+
+}  // namespace
+
+extern "C" {
+
+int dmad_abi_version(void) { return 1; }
+
+const char* dmad_last_error(void) { return g_last_error.c_str(); }
+
+int dmad_set_kernel_events(void* const* events, int count) {
+  if (count < 0 || count > kMaxEvents || (count % 2) != 0)
+    return fail(DMAD_ERR_INVALID, "count must be an even number in [0, %d]", kMaxEvents);
+  if (count > 0 && events == nullptr) return fail(DMAD_ERR_INVALID, "events: null pointer");
+  for (int i = 0; i < count; ++i) g_events[i] = (hipEvent_t)events[i];
+  g_nevents = count;
+  return ok();
+}
+
+int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv,
+                                  size_t* bytes) {
+  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
+  if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
+  if (B < 0 || H < 0 || Lk < 0 || !head_dim_ok(Dqk) || !head_dim_ok(Dv)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  *bytes = (size_t)fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
+  return ok();
+}
+
+int dmad_attn_jvp_fwd(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
+                      const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4], void* o,
+                      void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  return fwd_impl(dtype, mode, B, H, Lq, Lk, Dqk, Dv, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to,
+                  o_strides, lse, mu, sm_scale, workspace, workspace_bytes, stream, nullptr);
+}
+
+int dmad_attn_jvp_fwd_magi(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv,
+                           const void* q, const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                           const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                           void* o, void* to, const int64_t o_strides[4], float* lse, float* mu, float sm_scale,
+                           const int32_t* q_ranges, const int32_t* k_ranges, const int32_t* qk_map, int64_t G,
+                           int64_t R, const int32_t* task_group, const int32_t* task_qtile, int64_t T,
+                           int64_t block_m, void* workspace, size_t workspace_bytes, void* stream) {
+  if (block_m != dmad::kMagiBlockM)
+    return fail(DMAD_ERR_UNSUPPORTED, "tasks must be built for %d-query tiles, got BLOCK_M=%lld", dmad::kMagiBlockM,
+                (long long)block_m);
+  if (G < 1 || R < 0 || T < 0 || G >= ((int64_t)1 << 30) || R >= ((int64_t)1 << 30) || T >= ((int64_t)1 << 30))
+    return fail(DMAD_ERR_INVALID, "bad table sizes G=%lld R=%lld T=%lld", (long long)G, (long long)R, (long long)T);
+  if (q_ranges == nullptr || qk_map == nullptr || (R > 0 && k_ranges == nullptr) ||
+      (T > 0 && (task_group == nullptr || task_qtile == nullptr)))
+    return fail(DMAD_ERR_INVALID, "block-sparse tables: null pointer");
+  const MagiArgs mg{q_ranges, k_ranges, qk_map, task_group, task_qtile, G, R, T};
+  return fwd_impl(dtype, mode, B, H, Lq, Lk, Dqk, Dv, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to,
+                  o_strides, lse, mu, sm_scale, workspace, workspace_bytes, stream, &mg);
+}
+
+int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv, const void* q,
+                  const void* k, const void* v, const int64_t q_strides[4], const int64_t k_strides[4],
+                  const int64_t v_strides[4], void* o, const int64_t o_strides[4], float* lse, float sm_scale,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  return dmad_attn_jvp_fwd(dtype, DMAD_FWD_PLAIN, B, H, Lq, Lk, Dqk, Dv, q, k, v, nullptr, nullptr, nullptr,
+                           q_strides, k_strides, v_strides, o, nullptr, o_strides, lse, nullptr, sm_scale, workspace,
+                           workspace_bytes, stream);
+}
+
+int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes) {
+  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
+  if (full < 0 || full > 2) return fail(DMAD_ERR_INVALID, "full must be 0, 1 or 2");
+  if (B < 0 || H < 0 || Lq < 0 || Lk < 0 || !head_dim_ok(D)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  *bytes = (size_t)bwd_ws(full, B, H, Lq, Lk, D).total;
+  return ok();
+}
+
+int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
+                      const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                      const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                      const void* o, const void* to, const int64_t o_strides[4], const float* lse, const float* mu,
+                      const void* dout, const void* dto, const int64_t do_strides[4], void* dq, void* dk, void* dv,
+                      void* dtq, void* dtk, void* dtv, const int64_t dq_strides[4], const int64_t dk_strides[4],
+                      const int64_t dv_strides[4], float sm_scale, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  return bwd_impl(dtype, B, H, Lq, Lk, D, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to, o_strides, lse,
+                  mu, dout, dto, do_strides, dq, dk, dv, dtq, dtk, dtv, dq_strides, dk_strides, dv_strides, sm_scale,
+                  workspace, workspace_bytes, stream, false);
+}
+
+int dmad_attn_jvp_bwd_noalloc(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
+                              const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                              const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                              const void* o, const void* to, const int64_t o_strides[4], const float* lse,
+                              const float* mu, const void* dout, const void* dto, const int64_t do_strides[4],
+                              void* dq, void* dk, void* dv, void* dtq, void* dtk, void* dtv,
+                              const int64_t dq_strides[4], const int64_t dk_strides[4], const int64_t dv_strides[4],
+                              float sm_scale, void* stream) {
+  return bwd_impl(dtype, B, H, Lq, Lk, D, q, k, v, tq, tk, tv, q_strides, k_strides, v_strides, o, to, o_strides, lse,
+                  mu, dout, dto, do_strides, dq, dk, dv, dtq, dtk, dtv, dq_strides, dk_strides, dv_strides, sm_scale,
+                  nullptr, 0, stream, true);
 }
 
 int dmad_rmsnorm_rope_jvp(int dtype, int64_t rows, int64_t L, int64_t H, int64_t D, const void* y, const void* ty,

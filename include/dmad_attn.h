@@ -138,6 +138,33 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
                       const int64_t dv_strides[4], float sm_scale, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* Size of the static device scratch of dmad_attn_jvp_bwd_noalloc (64 MiB). */
+#define DMAD_BWD_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * Allocation-free backward. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid hipMalloc). Same arguments, results and
+ * errors as dmad_attn_jvp_bwd without the workspace: the per-row statistics
+ * (and any transposed copies) go to a static device array of
+ * DMAD_BWD_SCRATCH_BYTES in the library, one copy per GPU, held until the
+ * process ends. Problems whose dmad_attn_bwd_workspace_bytes exceeds that size
+ * fail with DMAD_ERR_UNSUPPORTED (e.g. the dO-only backward of 64- and 128-wide
+ * heads fits up to B*H*Lq ~ 8.4M rows: Wan2.1-14B at 720p needs 24 MB). The
+ * call allocates nothing; the first call on a device looks up that device's
+ * copy of the array. Calls that overlap on one GPU (concurrent streams or
+ * threads) share the array and race; serialise them. `stream` must belong to
+ * the current device.
+ */
+int dmad_attn_jvp_bwd_noalloc(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
+                              const void* k, const void* v, const void* tq, const void* tk, const void* tv,
+                              const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+                              const void* o, const void* to, const int64_t o_strides[4], const float* lse,
+                              const float* mu, const void* dout, const void* dto, const int64_t do_strides[4],
+                              void* dq, void* dk, void* dv, void* dtq, void* dtk, void* dtv,
+                              const int64_t dq_strides[4], const int64_t dk_strides[4], const int64_t dv_strides[4],
+                              float sm_scale, void* stream);
+
 /*
  * Fused attention-input prologue: RMSNorm over the model dim C = H*D, then the
  * interleaved rotary embedding, for a Linear output and its tangent in one HBM

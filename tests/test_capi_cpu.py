@@ -260,3 +260,43 @@ def test_bwd_empty_problem_is_a_no_op(nat):
     assert _bwd(nat, B=0) == 0
     assert _bwd(nat, H=0) == 0
     assert _bwd(nat, Lq=0, Lk=0) == 0
+
+
+def _bwd_noalloc(nat, **over):
+    st = _strides(8192, 4096, 64, 1)
+    args = dict(dtype=0, B=1, H=2, Lq=64, Lk=64, D=64, q=256, k=256, v=256, tq=0, tk=0, tv=0, qs=st, ks=st, vs=st,
+                o=256, to=0, os=st, lse=256, mu=0, do=256, dto=0, dos=st, dq=256, dk=256, dv=256, dtq=0, dtk=0,
+                dtv=0, dqs=st, dks=st, dvs=st, scale=0.125, stream=0)
+    args.update(over)
+    a = args
+    p = ctypes.c_void_p
+    return nat.lib().dmad_attn_jvp_bwd_noalloc(
+        a["dtype"], a["B"], a["H"], a["Lq"], a["Lk"], a["D"], p(a["q"]), p(a["k"]), p(a["v"]), p(a["tq"]),
+        p(a["tk"]), p(a["tv"]), a["qs"], a["ks"], a["vs"], p(a["o"]), p(a["to"]), a["os"], p(a["lse"]), p(a["mu"]),
+        p(a["do"]), p(a["dto"]), a["dos"], p(a["dq"]), p(a["dk"]), p(a["dv"]), p(a["dtq"]), p(a["dtk"]), p(a["dtv"]),
+        a["dqs"], a["dks"], a["dvs"], a["scale"], p(a["stream"]))
+
+
+def test_bwd_noalloc_rejects_problems_beyond_its_scratch(nat):
+    """The allocation-free backward refuses, before any HIP call, a problem whose
+    workspace exceeds its 64 MiB static scratch: here the full derivative at the
+    Wan2.1-14B 720p shape (transposed copies of several GB)."""
+    st = _strides(75600 * 40 * 128, 128, 40 * 128, 1)
+    rc = _bwd_noalloc(nat, **_FULL, B=1, H=40, Lq=75600, Lk=75600, D=128, qs=st, ks=st, vs=st, os=st, dos=st, dqs=st,
+                      dks=st, dvs=st)
+    assert rc == 2
+    assert "static scratch" in nat.lib().dmad_last_error().decode()
+    n = ctypes.c_size_t(0)
+    assert nat.lib().dmad_attn_bwd_workspace_bytes(1, 1, 40, 75600, 75600, 128, ctypes.byref(n)) == 0
+    assert n.value > nat.BWD_SCRATCH_BYTES
+
+
+@pytest.mark.parametrize("over,code,needle", [(dict(dtype=7), 2, "dtype"), (dict(q=0), 1, "q: null"),
+                                              (dict(D=48), 2, "head dim")])
+def test_bwd_noalloc_rejects_bad_arguments(nat, over, code, needle):
+    assert _bwd_noalloc(nat, **over) == code
+    assert needle in nat.lib().dmad_last_error().decode()
+
+
+def test_bwd_noalloc_empty_problem_is_a_no_op(nat):
+    assert _bwd_noalloc(nat, B=0) == 0
