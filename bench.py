@@ -79,7 +79,9 @@ def _args():
     ap.add_argument("--no-prologue", dest="prologue", action="store_false",
                     help="skip timing the fused RMSNorm+RoPE prologue (extra field)")
     ap.add_argument("--power", action="store_true",
-                    help="sample board power and GFX clock with amd-smi during the timed steps (extra field)")
+                    help="also sample board power and GFX clock over the forward and backward alone (extra field)")
+    ap.add_argument("--no-clock", dest="clock", action="store_false",
+                    help="do not sample the GFX clock and board power during the timed steps")
     ap.add_argument("--no-plain", dest="plain", action="store_false",
                     help="skip timing plain attention forward + backward (extra field)")
     ap.add_argument("--no-magi", dest="magi", action="store_false",
@@ -102,10 +104,25 @@ def _traffic_from_profiles(name):
         return None
 
 
-def cpu_baseline(L, D, H, seconds):
+def _cpu_model():
+    """CPU model name as lscpu reports it (None if unavailable)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return None
+
+
+def cpu_baseline(x, H, seconds):
     """Oracle float32 math path on the host: torch.func.jvp for (O, Od), autograd for dQ/dK/dV.
 
-    Runs 2048-row query chunks of one head at full Lk until `seconds` of work are
+    Runs on the benchmark's own inputs (head 0 of the same seeded tensors, copied
+    to the host): 2048-row query chunks at full Lk until `seconds` of work are
     done; FLOP/s are extrapolated linearly (the work is linear in rows and heads).
     """
     import torch
@@ -113,34 +130,33 @@ def cpu_baseline(L, D, H, seconds):
     sys.path.insert(0, ROOT)
     from oracle.attention import math_attention
 
-    g = torch.Generator().manual_seed(0)
-    k = torch.randn((1, 1, L, D), generator=g)
-    v = torch.randn((1, 1, L, D), generator=g)
-    tk = torch.randn((1, 1, L, D), generator=g) * 0.1
-    tv = torch.randn((1, 1, L, D), generator=g) * 0.1
+    h0 = {n: x[n][0, 0].float().cpu()[None, None] for n in ("q", "k", "v", "tq", "tk", "tv", "do")}
+    L, D = h0["k"].shape[-2], h0["k"].shape[-1]
+    k, v, tk, tv = h0["k"], h0["v"], h0["tk"], h0["tv"]
     rows, done, t = 2048, 0, 0.0
     s = D ** -0.5
     while t < seconds:
-        q = torch.randn((1, 1, rows, D), generator=g)
-        tq = torch.randn((1, 1, rows, D), generator=g) * 0.1
-        do = torch.randn((1, 1, rows, D), generator=g)
+        r0 = done % L
+        q, tq, do = (h0[n][..., r0:r0 + rows, :] for n in ("q", "tq", "do"))
         t0 = time.perf_counter()
         fn = lambda a, b, c: math_attention(a, b, c, s)[0]  # noqa: E731
         torch.func.jvp(fn, (q, k, v), (tq, tk, tv))
-        leaves = [x.clone().requires_grad_(True) for x in (q, k, v)]
+        leaves = [y.clone().requires_grad_(True) for y in (q, k, v)]
         o = math_attention(*leaves, s)[0]
         torch.autograd.grad(o, leaves, do)
         t += time.perf_counter() - t0
-        done += rows
+        done += q.shape[-2]
     flops = 22.0 * done * L * D
     return {
         "value": round(flops / t / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": _cpu_model(),
         "kind": "port",
-        "sample": f"1 head x {done} query rows x {L} keys, D={D}, fp32 torch.func.jvp + autograd "
-                  f"(fwd+JVP+dO-only bwd) in {t:.1f} s; extrapolates to "
-                  f"{H * L / done * t / 60:.0f} min for the 14B layer",
+        "sample": f"head 0 of the benchmark inputs: {done} query rows x {L} keys, D={D}, fp32 torch.func.jvp "
+                  f"+ autograd (fwd+JVP+dO-only bwd) in {t:.1f} s on {torch.get_num_threads()} threads; "
+                  f"extrapolates to {H * L / done * t / 60:.0f} min for the {H}-head layer",
     }
 
 
@@ -305,7 +321,7 @@ def main():
         sys.exit(2)
 
     sampler = None
-    if args.power:  # before any GPU use in this process
+    if args.power or args.clock:  # before any GPU use in this process
         import tempfile
 
         power_file = tempfile.NamedTemporaryFile(prefix="dmad_power_", suffix=".txt", delete=False).name
@@ -322,10 +338,10 @@ def main():
     torch.cuda.set_device(dev)
     H, L, D, LKX = args.heads, args.seq, 128, 512
     grid = (21, 30, 52) if L == 32760 else ((21, 45, 80) if L == 75600 else None)
-    x = make_inputs(1, H, L, L, D, dtype=torch.bfloat16, seed=0, device=dev, grid=grid, with_grads=True,
-                    gen_device=dev)
+    # one CPU generator seeded 0, draws in the order Q, K, V, Qd, Kd, Vd, dO, dOd (reproducible on any host)
+    x = make_inputs(1, H, L, L, D, dtype=torch.bfloat16, seed=0, device=dev, grid=grid, with_grads=True)
     q, k, v, tq, tk, tv, do = (x[n] for n in ("q", "k", "v", "tq", "tk", "tv", "do"))
-    xc = make_inputs(1, H, L, LKX, D, dtype=torch.bfloat16, seed=1, device=dev, gen_device=dev)
+    xc = make_inputs(1, H, L, LKX, D, dtype=torch.bfloat16, seed=1, device=dev)
     kc, vc = xc["k"], xc["v"]
     s = D ** -0.5
     lib = _native.lib()
@@ -392,7 +408,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded; RMSNorm + 3D RoPE Q/K, N(0,1) V, N(0,0.1^2) tangents, N(0,1) dO)",
+        "data": "synthetic: one CPU torch.Generator seeded 0, drawn in the order Q, K, V, Qd, Kd, Vd, dO, dOd as "
+                "float32 and cast to bf16 (Q, K: N(0,1) RMS-normalised over H*D and 3D-RoPE rotated; V, dO ~ N(0,1); "
+                "tangents, dOd ~ N(0,0.1^2)); cross-attention keys from a second generator seeded 1",
         "config": {
             "workload": f"Wan2.1 self-attn fwd+JVP+bwd(dO-only) + text cross-attn fwd+JVP, one layer",
             "B": 1, "H": H, "L": L, "D": D, "cross_keys": LKX,
@@ -415,7 +433,15 @@ def main():
         },
         "wall_s_timed": round(wall, 3),
     }
-    if sampler is not None:
+    if sampler is not None and not args.power:
+        time.sleep(0.3)
+        sampler.terminate()
+        sampler.wait()
+        # mean GFX clock and board power over the timed steps: the board runs at its power
+        # limit, so the clock (not only the kernels) sets the step time
+        out["clock_timed"] = _power_summary(power_file, w0, w1)
+        os.unlink(power_file)
+    if sampler is not None and args.power:
         # then each main pass alone for ~3 s, so each gets its own power/clock window
         def phase(fn):
             a = time.time()
@@ -466,7 +492,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(L, D, H, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(x, H, args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 
