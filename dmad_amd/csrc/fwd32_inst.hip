@@ -29,6 +29,17 @@ static hipError_t fwd32_magi_launch(const FwdParams& p, int grid, hipStream_t s)
   return hipGetLastError();
 }
 
+template <typename T, int MODE, int D>
+static hipError_t fwd32p_launch(const FwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_fwd32_persist_kernel<T, MODE, D>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int D>
+static FwdLaunchFn fwd32p_mode(int mode) {
+  return mode == kFwdJvpQOnly ? &fwd32p_launch<Elt, kFwdJvpQOnly, D> : nullptr;
+}
+
 template <int D>
 static FwdLaunchFn fwd32_magi_mode(int mode) {
   switch (mode) {
@@ -51,6 +62,11 @@ static FwdLaunchFn fwd32_mode(int mode) {
 template <>
 FwdLaunchFn fwd32_magi_select<Elt>(int mode, int d) {
   return d == 64 ? fwd32_magi_mode<64>(mode) : d == 128 ? fwd32_magi_mode<128>(mode) : nullptr;
+}
+
+template <>
+FwdLaunchFn fwd32p_select<Elt>(int mode, int d) {
+  return d == 128 ? fwd32p_mode<128>(mode) : nullptr;
 }
 
 template <>

@@ -22,6 +22,14 @@ FwdLaunchFn fwd32_select(int mode, int d);
 template <> FwdLaunchFn fwd32_select<__bf16>(int, int);
 template <> FwdLaunchFn fwd32_select<_Float16>(int, int);
 
+// Persistent forward (attn_fwd32_persist_kernel; mode kFwdJvpQOnly, 128-wide
+// heads, key-tile count a multiple of 4): the grid is at most the number of
+// workgroups resident on the device.
+template <typename T>
+FwdLaunchFn fwd32p_select(int mode, int d);
+template <> FwdLaunchFn fwd32p_select<__bf16>(int, int);
+template <> FwdLaunchFn fwd32p_select<_Float16>(int, int);
+
 // Block-sparse (MagiMask) forward launchers, JVP modes only; the grid is
 // tasks * B * H workgroups of 256 threads, each task a 128-query tile.
 template <typename T, int DQK>
