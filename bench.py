@@ -75,7 +75,8 @@ def _args():
     ap.add_argument("--seq", type=int, default=32760)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--full-bwd", action="store_true", help="also time the full-derivative backward (extra field)")
+    ap.add_argument("--no-full-bwd", dest="full_bwd", action="store_false",
+                    help="skip timing the full-derivative backward (extra field)")
     ap.add_argument("--no-prologue", dest="prologue", action="store_false",
                     help="skip timing the fused RMSNorm+RoPE prologue (extra field)")
     ap.add_argument("--power", action="store_true",
@@ -222,6 +223,38 @@ def plain_timing(q, k, v, do, dev):
             "ms_fwd": round(best_f, 3), "ms_bwd": round(best_b, 3),
             "fwd_pct_peak": round(100 * 4.0 * unit / (best_f * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
             "TFLOPs_fwd_bwd": round(tfs, 1), "pct_peak_fwd_bwd": round(100 * tfs / PEAK_BF16_TFLOPS, 2)}
+
+
+def full_bwd_timing(q, k, v, tq, tk, tv, do, dto):
+    """The full-derivative backward (the cotangent dOd of the tangent output included)
+    at the step's shape: gradients of q, k, v only, and all six gradients (the
+    tangents' too). Whole library calls (statistics and passes), best of 3.
+    Algorithmic flops: 24 and 30 units of H*L^2*D (12 and 15 GEMMs of 2*L^2*D)."""
+    import torch
+
+    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+
+    s = q.shape[-1] ** -0.5
+    o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+    B, H, L, D = q.shape
+    unit = B * H * L * L * D
+    res = {"kernels": "bwd_prep_kernel + attn_bwd_kv_full_kernel + attn_bwd_dq_full_kernel "
+                      "[+ attn_bwd_kv_tr_kernel for the tangents' dK, dV]"}
+    for tg, units, name in ((False, 24.0, "dq_dk_dv"), (True, 30.0, "all_six")):
+        jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, dto, s, tg)
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, dto, s, tg)
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b))
+        tfs = units * unit / (best * 1e-3) / 1e12
+        res[f"ms_{name}"] = round(best, 3)
+        res[f"pct_peak_{name}"] = round(100 * tfs / PEAK_BF16_TFLOPS, 2)
+    return res
 
 
 def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384)):
@@ -463,16 +496,7 @@ def main():
         out["power"] = {name: _power_summary(power_file, a + 0.5, b) for name, (a, b) in windows.items()}
         os.unlink(power_file)
     if args.full_bwd:
-        o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
-        dto = x["dto"]
-        jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, dto, s, False)
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, dto, s, False)
-        b.record()
-        torch.cuda.synchronize()
-        out["ms_self_bwd_full"] = round(a.elapsed_time(b), 3)
+        out["full_derivative_bwd"] = full_bwd_timing(q, k, v, tq, tk, tv, do, x["dto"])
     # fused RMSNorm(+JVP) + RoPE prologue that produces q and k for this layer,
     # timed after the step (HBM-bound; not part of the step or its flops)
     if args.prologue:

@@ -58,6 +58,7 @@ def units():
         out.append(("fwd32_inst.hip", f"fwd32_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
         out.append(("bwd_dq_inst.hip", f"bwd_dq_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
         out.append(("bwd_kv_inst.hip", f"bwd_kv_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
+        out.append(("bwd_full_inst.hip", f"bwd_full_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
         for d in HEAD_DIMS:
             out.append(("fwd_inst.hip", f"fwd_{tname}_d{d}", [f"-DDMAD_T={t}", f"-DDMAD_D={d}"]))
             if os.path.exists(os.path.join(CSRC, "bwd_inst.hip")):

@@ -35,6 +35,7 @@ struct DqParams {
   const void* tkT;  // Kd^T [BH][DP][LKP] (mode B)
   const float* stats;  // per-row statistics in the layout of the key-stationary kernel
   void* dq;
+  void* dtq;  // dQd (full derivative with tangent gradients, 128-wide heads)
   int64_t q_sb, q_sh, q_sl;     // shared by Q, Qd
   int64_t do_sb, do_sh, do_sl;  // shared by dO, dOd
   int64_t k_sb, k_sh, k_sl;     // shared by K, Kd

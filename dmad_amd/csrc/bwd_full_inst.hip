@@ -1,0 +1,41 @@
+// Instantiates the full-derivative passes for 128-wide heads (attn_bwd_full.h)
+// for one element type (-DDMAD_T=<0 bf16 | 1 f16>). Compiled with MFMAs in VGPR
+// form: the score tiles feed the VALU without AGPR->VGPR copies, while the
+// stationary rows and the accumulators stay in AGPRs.
+#include "launch.h"
+
+#ifndef DMAD_T
+#error "DMAD_T must be defined"
+#endif
+
+namespace dmad {
+
+#if DMAD_T == 0
+using Elt = __bf16;
+#else
+using Elt = _Float16;
+#endif
+
+template <typename T>
+static hipError_t kv_full_launch(const BwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_kv_full_kernel<T, 128>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, bool TG>
+static hipError_t dq_full_launch(const DqParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_dq_full_kernel<T, 128, TG>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <>
+BwdLaunchFn kv_full_select<Elt>() {
+  return &kv_full_launch<Elt>;
+}
+
+template <>
+DqLaunchFn dq_full_select<Elt>(bool tangent_grads) {
+  return tangent_grads ? &dq_full_launch<Elt, true> : &dq_full_launch<Elt, false>;
+}
+
+}  // namespace dmad

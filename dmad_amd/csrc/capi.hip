@@ -221,6 +221,18 @@ dmad::BwdLaunchFn pick_bwd(int dtype, int64_t d, int mode) {
   return nullptr;
 }
 
+dmad::BwdLaunchFn pick_kv_full(int dtype) {
+  if (dtype == DMAD_BF16) return dmad::kv_full_select<__bf16>();
+  if (dtype == DMAD_F16) return dmad::kv_full_select<_Float16>();
+  return nullptr;
+}
+
+dmad::DqLaunchFn pick_dq_full(int dtype, bool tangent_grads) {
+  if (dtype == DMAD_BF16) return dmad::dq_full_select<__bf16>(tangent_grads);
+  if (dtype == DMAD_F16) return dmad::dq_full_select<_Float16>(tangent_grads);
+  return nullptr;
+}
+
 dmad::DqLaunchFn pick_dq(int dtype, int64_t d, int mode) {
   using namespace dmad;
   if (dtype == DMAD_BF16) {
@@ -257,10 +269,10 @@ BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) 
   const int64_t BH = B * H, dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign);
   BwdWs w{};
   // transposed copies of Q, dO (and Qd, dOd) and K (and Kd): the full derivative
-  // and the dO-only passes of the head dims that read transposed copies
-  const bool copies = full != 0 || !dmad::dout_only_reads_rows((int)D);
-  w.nq = full ? 4 : (copies ? 2 : 0);
-  w.nk = full ? 2 : (copies ? 1 : 0);
+  // and the dO-only passes of the head dims whose kernels read transposed copies
+  const bool copies = full != 0 ? !dmad::full_reads_rows((int)D) : !dmad::dout_only_reads_rows((int)D);
+  w.nq = copies ? (full ? 4 : 2) : 0;
+  w.nk = copies ? (full ? 2 : 1) : 0;
   w.tgrad = full == 2;
   w.trq = round_up(BH * dp * lqp * 2, 256);
   w.trk = round_up(BH * dp * lkp * 2, 256);
@@ -507,21 +519,24 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   const int64_t dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign), BH = B * H;
   if (dp * lqp * 2 >= kMaxHeadBytes || dp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "sequence too long");
   const int mode = full ? dmad::kBwdFull : dmad::kBwdDoutOnly;
-  dmad::BwdLaunchFn fn = pick_bwd(dtype, D, mode);
-  dmad::DqLaunchFn fq = pick_dq(dtype, D, mode);
+  // 128-wide heads: the full derivative's query pass also gives dQd, so the
+  // tangent gradients need only the dO-only key pass (dKd, dVd)
+  const bool full_rows = full && dmad::full_reads_rows((int)D);
+  dmad::BwdLaunchFn fn = full_rows ? pick_kv_full(dtype) : pick_bwd(dtype, D, mode);
+  dmad::DqLaunchFn fq = full_rows ? pick_dq_full(dtype, tgrad) : pick_dq(dtype, D, mode);
   dmad::BwdLaunchFn fn_a = tgrad ? pick_bwd(dtype, D, dmad::kBwdDoutOnly) : nullptr;
-  dmad::DqLaunchFn fq_a = tgrad ? pick_dq(dtype, D, dmad::kBwdDoutOnly) : nullptr;
-  if (fn == nullptr || fq == nullptr || (tgrad && (fn_a == nullptr || fq_a == nullptr)))
+  dmad::DqLaunchFn fq_a = tgrad && !full_rows ? pick_dq(dtype, D, dmad::kBwdDoutOnly) : nullptr;
+  if (fn == nullptr || fq == nullptr || (tgrad && (fn_a == nullptr || (!full_rows && fq_a == nullptr))))
     return fail(DMAD_ERR_UNSUPPORTED, "no backward kernel for D=%lld", (long long)D);
 
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   char* trq = w.nq ? ws : nullptr;
   char* trdo = w.nq ? ws + w.trq : nullptr;
-  char* trtq = full ? ws + 2 * w.trq : nullptr;
-  char* trdto = full ? ws + 3 * w.trq : nullptr;
+  char* trtq = full && w.nq ? ws + 2 * w.trq : nullptr;
+  char* trdto = full && w.nq ? ws + 3 * w.trq : nullptr;
   char* trk = w.nk ? ws + w.nq * w.trq : nullptr;
-  char* trtk = full ? trk + w.trk : nullptr;
+  char* trtk = full && w.nk ? trk + w.trk : nullptr;
   float* stats = (float*)(ws + w.nq * w.trq + w.nk * w.trk);
   float* stats_bt = w.tgrad ? (float*)((char*)stats + w.stats) : nullptr;
 
@@ -530,13 +545,14 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     dmad::TransposeParams tp{x, y, st[0], st[1], st[2], (int)H, (int)L, (int)D, (int)LP, (int)dp};
     return dmad::launch_transpose_pad(tp, (int)BH, s);
   };
-  // the full-derivative kernels, and the dO-only ones for some head dims, read
-  // transposed copies of Q, dO (and Qd, dOd) and K (and Kd)
-  const bool need_tr = full || !dmad::dout_only_reads_rows((int)D);
+  // the full-derivative kernels of head dims other than 128, and the dO-only
+  // ones of some head dims, read transposed copies of Q, dO (and Qd, dOd) and K
+  // (and Kd)
+  const bool need_tr = w.nq > 0;
   if (need_tr && ((e = tr(q, q_strides, trq, Lq, lqp)) != hipSuccess ||
                   (e = tr(dout, do_strides, trdo, Lq, lqp)) != hipSuccess || (e = tr(k, k_strides, trk, Lk, lkp)) != hipSuccess))
     return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
-  if (full && ((e = tr(tq, q_strides, trtq, Lq, lqp)) != hipSuccess || (e = tr(dto, do_strides, trdto, Lq, lqp)) != hipSuccess ||
+  if (need_tr && full && ((e = tr(tq, q_strides, trtq, Lq, lqp)) != hipSuccess || (e = tr(dto, do_strides, trdto, Lq, lqp)) != hipSuccess ||
                (e = tr(tk, k_strides, trtk, Lk, lkp)) != hipSuccess))
     return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
 
@@ -610,6 +626,7 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   pq.tkT = full ? trtk : trk;
   pq.stats = stats;
   pq.dq = dq;
+  pq.dtq = dtq;
   pq.q_sb = q_strides[0]; pq.q_sh = q_strides[1]; pq.q_sl = q_strides[2];
   pq.do_sb = do_strides[0]; pq.do_sh = do_strides[1]; pq.do_sl = do_strides[2];
   pq.k_sb = k_strides[0]; pq.k_sh = k_strides[1]; pq.k_sl = k_strides[2];
@@ -635,7 +652,8 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
   mark(1, true, s);
   if (tgrad) {
-    // tangent gradients: the dO-only passes with (dO, D) := (dOd, rho)
+    // tangent gradients: the dO-only passes with (dO, D) := (dOd, rho) (the
+    // query pass only where the full derivative's query pass did not give dQd)
     dmad::BwdParams pt = p;
     pt.dout = dto;
     pt.doT = trdto;
@@ -651,10 +669,12 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     pqt.stats = stats_bt;
     pqt.stat_tile = ba;
     pqt.dq = dtq;
-    mark(3, false, s);
-    if (nqt > 0 && (e = fq_a(pqt, (int)(nqt * BH), s)) != hipSuccess)
-      return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
-    mark(3, true, s);
+    if (fq_a != nullptr) {
+      mark(3, false, s);
+      if (nqt > 0 && (e = fq_a(pqt, (int)(nqt * BH), s)) != hipSuccess)
+        return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
+      mark(3, true, s);
+    }
   }
   return ok();
 }

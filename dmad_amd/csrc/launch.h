@@ -7,6 +7,7 @@
 #include "attn_fwd32.h"
 #include "attn_bwd.h"
 #include "attn_bwd_dq.h"
+#include "attn_bwd_full.h"
 
 namespace dmad {
 
@@ -68,6 +69,19 @@ template <> DqLaunchFn dq_tr_select<__bf16, 64>();
 template <> DqLaunchFn dq_tr_select<__bf16, 128>();
 template <> DqLaunchFn dq_tr_select<_Float16, 64>();
 template <> DqLaunchFn dq_tr_select<_Float16, 128>();
+
+// Full-derivative passes for 128-wide heads (bwd_full_inst.hip): the key pass
+// (dK, dV) and the query pass (dQ, and dQd when tangent_grads).
+template <typename T>
+BwdLaunchFn kv_full_select();
+template <> BwdLaunchFn kv_full_select<__bf16>();
+template <> BwdLaunchFn kv_full_select<_Float16>();
+template <typename T>
+DqLaunchFn dq_full_select(bool tangent_grads);
+template <> DqLaunchFn dq_full_select<__bf16>(bool);
+template <> DqLaunchFn dq_full_select<_Float16>(bool);
+// Head dims whose full derivative runs on those passes.
+inline bool full_reads_rows(int d) { return d == 128; }
 
 // Query tile of the dK/dV kernel, which fixes the layout of the backward
 // statistics (the full-derivative kernel always uses 32-query tiles).

@@ -110,8 +110,8 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
 /* Bytes of workspace dmad_attn_jvp_bwd needs. full: 0 = dO-only gradients,
  * 1 = full derivative (dto given), 2 = full derivative plus tangent gradients
  * (dto, dtq, dtk, dtv given). The per-row statistics always; transposed copies
- * of Q, dO, K (and the tangents) for the full derivative and for the dO-only
- * gradients of head dims other than 64 and 128. */
+ * of Q, dO, K (and the tangents) for the full derivative of head dims other
+ * than 128 and for the dO-only gradients of head dims other than 64 and 128. */
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes);
 
 /*
@@ -150,7 +150,8 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
  * DMAD_BWD_SCRATCH_BYTES in the library, one copy per GPU, held until the
  * process ends. Problems whose dmad_attn_bwd_workspace_bytes exceeds that size
  * fail with DMAD_ERR_UNSUPPORTED (e.g. the dO-only backward of 64- and 128-wide
- * heads fits up to B*H*Lq ~ 8.4M rows: Wan2.1-14B at 720p needs 24 MB). The
+ * heads fits up to B*H*Lq ~ 8.4M rows: Wan2.1-14B at 720p needs 24 MB; the full
+ * derivative of 128-wide heads with tangent gradients up to ~2.8M rows). The
  * call allocates nothing; the first call on a device looks up that device's
  * copy of the array. Calls that overlap on one GPU (concurrent streams or
  * threads) share the array and race; serialise them. `stream` must belong to
@@ -196,8 +197,9 @@ int dmad_rmsnorm_rope_jvp(int dtype, int64_t rows, int64_t L, int64_t H, int64_t
  * this thread records events[2i] and events[2i+1] on its stream immediately
  * before and after its i-th main kernel, excluding the layout and statistics
  * passes. Main kernels in order: forward -> {attention}; backward -> {dK/dV
- * pass, dQ pass[, tangent dK/dV pass, tangent dQ pass]}. Kernels without a
- * pair of events are not timed. count = 0 (events may be NULL) stops.
+ * pass, dQ pass[, tangent dK/dV pass[, tangent dQ pass]]} (for 128-wide heads
+ * the full derivative's dQ pass also gives dQd: no tangent dQ pass). Kernels
+ * without a pair of events are not timed. count = 0 (events may be NULL) stops.
  */
 int dmad_set_kernel_events(void* const* events, int count);
 

@@ -251,9 +251,14 @@ def test_bwd_workspace_query(nat):
     # 32-wide heads read transposed copies of Q, dO and K
     copy = 40 * 32 * 32768 * 2
     assert q(0, 1, 40, 32760, 32760, 32, ctypes.byref(n)) == 0 and n.value == 3 * copy + stats
-    # the full derivative: Q, dO, Qd, dOd, K, Kd copies and four statistics per row
-    copy = 40 * 128 * 32768 * 2
-    assert q(1, 1, 40, 32760, 32760, 128, ctypes.byref(n)) == 0 and n.value == 6 * copy + 2 * stats
+    # the full derivative of 128-wide heads reads rows: four statistics per row
+    # (lse2, D', mu, rho), and two more (lse2, rho) for the tangent gradients
+    assert q(1, 1, 40, 32760, 32760, 128, ctypes.byref(n)) == 0 and n.value == 2 * stats
+    assert q(2, 1, 40, 32760, 32760, 128, ctypes.byref(n)) == 0 and n.value == 3 * stats
+    # other head dims: Q, dO, Qd, dOd, K, Kd copies as well
+    copy = 40 * 64 * 32768 * 2
+    stats64 = 40 * 32768 * 2 * 4
+    assert q(1, 1, 40, 32760, 32760, 64, ctypes.byref(n)) == 0 and n.value == 6 * copy + 2 * stats64
 
 
 def test_bwd_empty_problem_is_a_no_op(nat):
