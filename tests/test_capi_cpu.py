@@ -284,16 +284,20 @@ def _bwd_noalloc(nat, **over):
 
 def test_bwd_noalloc_rejects_problems_beyond_its_scratch(nat):
     """The allocation-free backward refuses, before any HIP call, a problem whose
-    workspace exceeds its 64 MiB static scratch: here the full derivative at the
-    Wan2.1-14B 720p shape (transposed copies of several GB)."""
+    workspace exceeds its 64 MiB static scratch: here the full derivative with
+    tangent gradients at the Wan2.1-14B 720p shape (24 bytes of statistics per
+    (head, query row): 72.6 MB)."""
     st = _strides(75600 * 40 * 128, 128, 40 * 128, 1)
-    rc = _bwd_noalloc(nat, **_FULL, B=1, H=40, Lq=75600, Lk=75600, D=128, qs=st, ks=st, vs=st, os=st, dos=st, dqs=st,
-                      dks=st, dvs=st)
+    rc = _bwd_noalloc(nat, **_FULL, dtq=256, dtk=256, dtv=256, B=1, H=40, Lq=75600, Lk=75600, D=128, qs=st, ks=st,
+                      vs=st, os=st, dos=st, dqs=st, dks=st, dvs=st)
     assert rc == 2
     assert "static scratch" in nat.lib().dmad_last_error().decode()
     n = ctypes.c_size_t(0)
-    assert nat.lib().dmad_attn_bwd_workspace_bytes(1, 1, 40, 75600, 75600, 128, ctypes.byref(n)) == 0
+    assert nat.lib().dmad_attn_bwd_workspace_bytes(2, 1, 40, 75600, 75600, 128, ctypes.byref(n)) == 0
     assert n.value > nat.BWD_SCRATCH_BYTES
+    # without the tangent gradients the same problem fits
+    assert nat.lib().dmad_attn_bwd_workspace_bytes(1, 1, 40, 75600, 75600, 128, ctypes.byref(n)) == 0
+    assert n.value <= nat.BWD_SCRATCH_BYTES
 
 
 @pytest.mark.parametrize("over,code,needle", [(dict(dtype=7), 2, "dtype"), (dict(q=0), 1, "q: null"),
