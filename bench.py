@@ -88,7 +88,8 @@ def _args():
     ap.add_argument("--no-magi", dest="magi", action="store_false",
                     help="skip timing the block-sparse forward on the causal-student masks (extra field)")
     ap.add_argument("--harness", action="store_true",
-                    help="also time the reference perf harness configuration (B=4, H=32, D=64 and 128, fp16)")
+                    help="also time the reference perf harness configuration (B=4, H=32, D=64 and 128, fp16), "
+                         "and the same at head dims 16, 32 and 256")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one elementwise kernel that reads and writes this many MiB "
                          "(a known-size reference for HBM byte counters under a profiler)")
@@ -507,6 +508,8 @@ def main():
         out["magi_fwd_jvp"] = magi_timing(H, D, dev)
     if args.harness:
         out["reference_harness"] = [harness_timing(dev, D=d) for d in (64, 128)]
+        # the head dims the reference also accepts (:471-472), on the generic kernels
+        out["other_head_dims"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384)) for d in (16, 32, 256)]
     if args.calibration_copy_mib:
         n = args.calibration_copy_mib * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)

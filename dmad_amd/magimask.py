@@ -135,7 +135,8 @@ def _teacher_forcing_rects(spec: AttnMaskSpec, Q: int, KV: int):
     assert nclean > 0
     clean = pat.blocks_to_tokens(nclean)
     assert Q == 2 * clean and KV == 2 * clean, (
-        f"teacher_forcing expects Q_real==KV_real==2*clean_len ({2 * clean}), got Q_real={Q}, KV_real={KV}")
+        f"teacher forcing packs a clean and a noisy copy: query and key lengths must both be "
+        f"{2 * clean} (twice the {clean} clean tokens), got {Q} and {KV}")
     window = spec.local_attn_blocks - 1
     hb = pat.block_bounds(q_bo=0, Q=clean)
     for i in range(nclean):
@@ -186,13 +187,13 @@ def merge_k_ranges(q_ranges: torch.Tensor, k_ranges: torch.Tensor, KV_real: int)
     i = 0
     while i < len(qs):
         q0, q1 = int(qs[i, 0]), int(qs[i, 1])
-        assert q0 < q1, f"Invalid q range [{q0}, {q1})"
+        assert q0 < q1, f"query range [{q0}, {q1}) is empty or reversed"
         j = i
         while j < len(qs) and qs[j, 0] == q0 and qs[j, 1] == q1:
             j += 1
         clipped = np.clip(ks[i:j], 0, KV_real)
         segs = sorted((int(a), int(b)) for a, b in clipped if b > a)
-        assert segs, f"Empty-k group for q=[{q0},{q1})."
+        assert segs, f"query rows [{q0}, {q1}) have no key range inside [0, {KV_real})"
         lo, hi = segs[0]
         for a, b in segs[1:]:
             if a <= hi:
