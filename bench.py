@@ -63,7 +63,7 @@ def _power_summary(path, t0, t1):
         return {"samples": 0}
     return {"samples": len(rows), "avg_W": round(sum(r[0] for r in rows) / len(rows), 1),
             "max_W": max(r[0] for r in rows), "avg_gfx_MHz": round(sum(r[1] for r in rows) / len(rows)),
-            "source": "amd-smi metric -p -c (SOCKET_POWER, mean GFX CLK over the XCDs) during the timed steps"}
+            "source": "amd-smi metric -p -c (SOCKET_POWER, mean GFX CLK over the XCDs)"}
 
 
 def _args():
@@ -468,12 +468,21 @@ def main():
         "wall_s_timed": round(wall, 3),
     }
     if sampler is not None and not args.power:
+        # mean GFX clock and board power over the timed steps: the board runs at its power
+        # limit, so the clock (not only the kernels) sets the step time. amd-smi gives about
+        # one reading per 0.1 s and its power reading trails a change of load, so the window
+        # skips its first 0.5 s and is continued with the same step, untimed, until it spans 3 s.
+        extra = 0
+        while time.time() - w0 < 3.0:
+            step(False)
+            torch.cuda.synchronize()
+            extra += 1
+        w2 = time.time()
         time.sleep(0.3)
         sampler.terminate()
         sampler.wait()
-        # mean GFX clock and board power over the timed steps: the board runs at its power
-        # limit, so the clock (not only the kernels) sets the step time
-        out["clock_timed"] = _power_summary(power_file, w0, w1)
+        out["clock_timed"] = _power_summary(power_file, w0 + 0.5, w2)
+        out["clock_timed"].update({"window_s": round(w2 - w0 - 0.5, 2), "untimed_steps_after": extra})
         os.unlink(power_file)
     if sampler is not None and args.power:
         # then each main pass alone for ~3 s, so each gets its own power/clock window

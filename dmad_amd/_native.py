@@ -8,6 +8,7 @@ library is missing, every GPU entry point raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 
 import torch  # noqa: F401  (loads the HIP runtime the library must share)
@@ -107,16 +108,60 @@ def check(code: int) -> None:
         raise DmadError(code, msg)
 
 
+# The helpers below sit on every call's host path, which the GPU waits on when a
+# call follows a synchronisation (tens of microseconds against a 0.12 ms
+# forward at 1024 tokens): plain ints go to ctypes as c_void_p, stride arrays
+# are made once per stride tuple, and the workspace sizes (pure functions of
+# the shape) are asked once per shape.
+_strides_cache: dict = {}
+
+
 def strides4(t: torch.Tensor):
-    return (ctypes.c_int64 * 4)(*t.stride())
+    st = t.stride()
+    arr = _strides_cache.get(st)
+    if arr is None:
+        if len(_strides_cache) > 4096:
+            _strides_cache.clear()
+        arr = _strides_cache[st] = (ctypes.c_int64 * 4)(*st)
+    return arr
 
 
 def ptr(t):
-    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+    """Device address of ``t`` (None -> NULL) as an int, which ctypes passes as c_void_p."""
+    return None if t is None else t.data_ptr()
 
 
-def stream_ptr(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_ptr(device: torch.device) -> int:
+    """The current HIP stream of ``device`` (what torch launches on) as an int."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+@functools.lru_cache(maxsize=1024)
+def fwd_workspace_bytes(mode: int, B: int, H: int, Lk: int, Dqk: int, Dv: int) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv, ctypes.byref(n)))
+    return int(n.value)
+
+
+@functools.lru_cache(maxsize=1024)
+def bwd_workspace_bytes(mode: int, B: int, H: int, Lq: int, Lk: int, D: int) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().dmad_attn_bwd_workspace_bytes(mode, B, H, Lq, Lk, D, ctypes.byref(n)))
+    return int(n.value)
+
+
+def workspace(nbytes: int, device: torch.device):
+    """(pointer, size) of a fresh workspace of ``nbytes`` (NULL, 0 when none is needed) and the
+    tensor that owns it, which the caller keeps alive until the launch is queued."""
+    if nbytes == 0:
+        return None, 0, None
+    ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
+    return ws.data_ptr(), nbytes, ws
 
 
 class KernelTimer:

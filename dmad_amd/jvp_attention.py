@@ -151,16 +151,14 @@ def jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale, need_mu=True):
     lse = torch.empty((B, H, Lq), device=dev, dtype=torch.float32)
     mu = torch.empty_like(lse) if tq is not None else None
     lib = nat.lib()
-    ws_bytes = nat.ctypes.c_size_t(0)
-    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv, nat.ctypes.byref(ws_bytes)))
-    ws = torch.empty(max(int(ws_bytes.value), 1), device=dev, dtype=torch.uint8)
+    ws_ptr, ws_size, ws = nat.workspace(nat.fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv), dev)
     nat.check(
         lib.dmad_attn_jvp_fwd(
             code, mode, B, H, Lq, Lk, Dqk, Dv,
             nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(tq), nat.ptr(tk), nat.ptr(tv),
             nat.strides4(q), nat.strides4(k), nat.strides4(v),
             nat.ptr(o), nat.ptr(to), nat.strides4(o), nat.ptr(lse), nat.ptr(mu),
-            float(sm_scale), nat.ptr(ws), ws.numel(), nat.stream_ptr(dev),
+            float(sm_scale), ws_ptr, ws_size, nat.stream_ptr(dev),
         )
     )
     return o, to, lse, mu
@@ -204,9 +202,7 @@ def jvp_attention_forward_magi(q, k, v, tq, tk, tv, sm_scale, magi_mask):
     lse = torch.empty((B, H, Lq), device=dev, dtype=torch.float32)
     mu = torch.empty_like(lse)
     lib = nat.lib()
-    ws_bytes = nat.ctypes.c_size_t(0)
-    nat.check(lib.dmad_attn_fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv, nat.ctypes.byref(ws_bytes)))
-    ws = torch.empty(max(int(ws_bytes.value), 1), device=dev, dtype=torch.uint8)
+    ws_ptr, ws_size, ws = nat.workspace(nat.fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv), dev)
     nat.check(
         lib.dmad_attn_jvp_fwd_magi(
             code, mode, B, H, Lq, Lk, Dqk, Dv,
@@ -215,7 +211,7 @@ def jvp_attention_forward_magi(q, k, v, tq, tk, tv, sm_scale, magi_mask):
             nat.ptr(o), nat.ptr(to), nat.strides4(o), nat.ptr(lse), nat.ptr(mu), float(sm_scale),
             nat.ptr(q_unique), nat.ptr(k_flat), nat.ptr(qk_map), G, R,
             nat.ptr(task_group), nat.ptr(task_qtile), T, mm.KERNEL_BLOCK_M,
-            nat.ptr(ws), ws.numel(), nat.stream_ptr(dev),
+            ws_ptr, ws_size, nat.stream_ptr(dev),
         )
     )
     return o, to, lse, mu
@@ -256,10 +252,8 @@ def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_sc
     dtk = torch.empty_like(dk) if tgrads else None
     dtv = torch.empty_like(dv) if tgrads else None
     lib = nat.lib()
-    ws_bytes = nat.ctypes.c_size_t(0)
     ws_mode = (2 if tgrads else 1) if full else 0
-    nat.check(lib.dmad_attn_bwd_workspace_bytes(ws_mode, B, H, Lq, Lk, D, nat.ctypes.byref(ws_bytes)))
-    ws = torch.empty(max(int(ws_bytes.value), 1), device=q.device, dtype=torch.uint8)
+    ws_ptr, ws_size, ws = nat.workspace(nat.bwd_workspace_bytes(ws_mode, B, H, Lq, Lk, D), q.device)
     nat.check(
         lib.dmad_attn_jvp_bwd(
             code, B, H, Lq, Lk, D,
@@ -269,7 +263,7 @@ def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_sc
             nat.ptr(dout), nat.ptr(dto), nat.strides4(dout),
             nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dtq), nat.ptr(dtk), nat.ptr(dtv),
             nat.strides4(dq), nat.strides4(dk), nat.strides4(dv),
-            float(sm_scale), nat.ptr(ws), ws.numel(), nat.stream_ptr(q.device),
+            float(sm_scale), ws_ptr, ws_size, nat.stream_ptr(q.device),
         )
     )
     return dq, dk, dv, dtq, dtk, dtv
