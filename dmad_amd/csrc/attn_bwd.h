@@ -62,6 +62,7 @@ struct BwdParams {
   int64_t dv_sb, dv_sh, dv_sl;
   int B, H, Lq, Lk, LQP;
   float scale, scale_log2;
+  int xcd_order;  // work items contiguous per XCD (common.h)
 };
 
 template <int D, int MODE>
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nkt, kt = work - bh * nkt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
@@ -418,7 +419,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nkt, kt = work - bh * nkt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
@@ -738,7 +739,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nkt, kt = work - bh * nkt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;

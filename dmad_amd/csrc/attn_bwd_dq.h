@@ -44,6 +44,7 @@ struct DqParams {
   int B, H, Lq, Lk, LQP, LKP;
   int stat_tile;  // query tile of the statistics layout
   float scale, scale_log2;
+  int xcd_order;  // work items contiguous per XCD (common.h)
 };
 
 template <int D, int MODE>
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(DqParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -334,7 +335,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq_pipe_kernel(DqParams p) {
   const int col = lane & 15, grp = lane >> 4;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -555,7 +556,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_tr_kernel(DqParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int ntiles = (p.Lk + BN - 1) / BN;

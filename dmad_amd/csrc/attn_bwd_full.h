@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nkt, kt = work - bh * nkt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
@@ -441,7 +441,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_full_kernel(DqParams p) {
   const int col = lane & 31, half = lane >> 5;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
   const int ntiles = (p.Lk + BN - 1) / BN;

@@ -71,6 +71,7 @@ struct FwdParams {
   const int* task_group;  // [T]
   const int* task_qtile;  // [T]
   int G, R, T;
+  int xcd_order;  // dense kernels: work items contiguous per XCD (common.h)
 };
 
 // One (query group, 128-query tile) task of the block-sparse forward: group
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
   const int col = lane & 15, grp = lane >> 4;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -549,7 +550,7 @@ __global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
   const int col = lane & 15, grp = lane >> 4;
 
   const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int work = blockIdx.x;  // head-major order (common.h)
+  const int work = work_item(p.xcd_order);  // block order (common.h)
   const int bh = work / nqt, qt = work - bh * nqt;
   const int b = bh / p.H, h = bh - b * p.H;
 
@@ -927,7 +928,7 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
     cm.seek(p, BN);
   } else {
     const int nqt = (p.Lq + C::BM - 1) / C::BM;
-    const int work = blockIdx.x;  // head-major order (common.h)
+    const int work = work_item(p.xcd_order);  // block order (common.h)
     bh = work / nqt;
     qt = work - bh * nqt;
     ntiles = (p.Lk + BN - 1) / BN;

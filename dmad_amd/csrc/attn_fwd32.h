@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void attn_fwd32_kernel(FwdPa
     }
   } else {
     const int nqt = (p.Lq + C::BM - 1) / C::BM;
-    const int work = blockIdx.x;  // head-major order (common.h)
+    const int work = work_item(p.xcd_order);  // block order (common.h)
     bh = work / nqt;
     qt = work - bh * nqt;
     ntiles = (p.Lk + BN - 1) / BN;

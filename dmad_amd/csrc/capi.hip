@@ -392,6 +392,7 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
   }
   if (units * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
   int64_t grid = units * BH;
+  p.xcd_order = units < dmad::kHeadMajorMinTiles;  // block order (common.h)
   // short key sequences, K and V tangents zero (the text cross-attention): the
   // persistent kernel (one workgroup per slot, looping over the query tiles)
   // overlaps each tile's Q reads and O writes with the key loop of the next
@@ -644,6 +645,8 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
 
   const int64_t nkt = (Lk + 127) / 128, nqt = (Lq + 127) / 128;
   if (nkt * BH >= ((int64_t)1 << 31) || nqt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  p.xcd_order = nkt < dmad::kHeadMajorMinTiles;  // block order (common.h)
+  pq.xcd_order = nqt < dmad::kHeadMajorMinTiles;
   mark(0, false, s);
   if ((e = fn(p, (int)(nkt * BH), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   mark(0, true, s);

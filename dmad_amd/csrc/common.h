@@ -231,20 +231,36 @@ enum SchedMask : int { kSchedVALU = 0x2, kSchedSALU = 0x4, kSchedMFMA = 0x8, kSc
                        kSchedDSWrite = 0x200, kSchedTrans = 0x400 };
 
 // Block order. The hardware deals workgroups to the 8 XCDs round-robin by
-// block id. The dense kernels use the block id as the work item, head-major
-// (work = head * tiles + tile): the 256 workgroups in flight then cover one
-// head and all 8 XCDs stream that head's K/V (or Q/dO) at the same time, so
-// their L2 misses fall on one head's 34 MB in the memory-side cache instead of
-// eight heads' 268 MB. That measured 1-2% faster than giving each XCD its own
-// head (xcd_remap below), with the same L2 fetch volume.
+// block id. When a head has at least 256 tiles (the Wan shapes), the dense
+// kernels use the block id as the work item, head-major (work = head * tiles +
+// tile): the 256 workgroups in flight then cover one head and all 8 XCDs
+// stream that head's K/V (or Q/dO) at the same time, so their L2 misses fall
+// on one head's 34 MB in the memory-side cache instead of eight heads' 268 MB.
+// That measured 1-2% faster than giving each XCD its own head (xcd_remap
+// below), with the same L2 fetch volume.
 //
-// The block-sparse kernels use xcd_remap instead: each XCD takes a contiguous
-// range of work items, so consecutive tasks of one query group (which walk the
-// same key ranges) share one L2 (3-4% faster there than head-major order).
+// With fewer tiles per head the workgroups in flight span several heads, and
+// round-robin dealing would put each head's tiles on all 8 XCDs, each L2
+// fetching the whole head. There the launcher sets xcd_order and the kernels
+// use xcd_remap: each XCD takes a contiguous range of work items, so a head's
+// tiles share one L2 (B=4, H=32, L=1024-4096: 2-8% faster per kernel; neutral
+// from 128 tiles per head on). The block-sparse kernels always use xcd_remap:
+// consecutive tasks of one query group walk the same key ranges (3-4% faster
+// there than head-major order).
 __device__ __forceinline__ int xcd_remap(int bid, int total) {
   const int xcd = bid & 7, slot = bid >> 3;
   const int per = total >> 3, rem = total & 7;
   return (xcd < rem) ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
 }
+
+// This workgroup's work item of a dense kernel (the grid is exactly the work
+// items): head-major, or contiguous per XCD when xcd_order is set.
+__device__ __forceinline__ int work_item(int xcd_order) {
+  const int bid = (int)blockIdx.x;
+  return xcd_order ? xcd_remap(bid, (int)gridDim.x) : bid;
+}
+
+// Head tiles from which the dense launches keep head-major order.
+constexpr int kHeadMajorMinTiles = 256;
 
 }  // namespace dmad
