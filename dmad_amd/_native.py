@@ -23,6 +23,7 @@ DMAD_ERR_HIP = 4
 
 DMAD_BF16 = 0
 DMAD_F16 = 1
+DMAD_F32 = 2
 
 DMAD_FWD_PLAIN = 0
 DMAD_FWD_JVP = 1
@@ -198,6 +199,8 @@ def dtype_code(dtype: torch.dtype) -> int:
         return DMAD_BF16
     if dtype == torch.float16:
         return DMAD_F16
+    if dtype == torch.float32:
+        return DMAD_F32
     raise NotImplementedError(
-        f"dtype {dtype} is not supported by the gfx950 kernels (bfloat16 or float16 operands)"
+        f"dtype {dtype} is not supported by the gfx950 kernels (bfloat16, float16 or float32 operands)"
     )

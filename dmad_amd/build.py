@@ -63,6 +63,8 @@ def units():
             out.append(("fwd_inst.hip", f"fwd_{tname}_d{d}", [f"-DDMAD_T={t}", f"-DDMAD_D={d}"]))
             if os.path.exists(os.path.join(CSRC, "bwd_inst.hip")):
                 out.append(("bwd_inst.hip", f"bwd_{tname}_d{d}", [f"-DDMAD_T={t}", f"-DDMAD_D={d}"]))
+    for d in HEAD_DIMS:
+        out.append(("f32_inst.hip", f"f32_d{d}", [f"-DDMAD_D={d}"]))
     return out
 
 

@@ -1,0 +1,698 @@
+// fp32 operands. The reference's Triton forward (flash_attention_jvp_triton.py:
+// 107-232, 242-409) runs its dots on whatever dtype the op receives, fp32
+// included, and the plain attention entry point (rcm/utils/attention.py:120-167)
+// routes fp32 to PyTorch's memory-efficient SDPA, forward and backward. These
+// kernels give both on gfx950's fp32 MFMA (v_mfma_f32_16x16x4_f32, exact fp32
+// products, 157 TFLOP/s dense peak): the forward in every mode (plain, JVP,
+// K/V-tangent-free, block-sparse) and the dO-only backward as a key pass (dK,
+// dV) and a query pass (dQ). Softmax, P and H~ stay in fp32 (the reference's
+// p.to(v.dtype) is then no rounding), and the running max is exact.
+//
+// MFMA 16x16x4 fp32 layouts:
+//   A (16 x 4): lane l holds row l%16, k = l/16
+//   B (4 x 16): lane l holds col l%16, k = l/16
+//   C (16 x 16): lane l holds col l%16, rows 4*(l/16) + r, r = 0..3
+// A 16-byte LDS read of 4 consecutive d (or key) values per lane feeds four
+// MFMAs: MFMA u takes element u, so its k index l/16 stands for d = 4*(l/16)+u
+// (+16 per chunk); both operands of a product use the same map, so the four
+// MFMAs sum every d once. P (and dS) come out of the score MFMAs in the C
+// layout, whose rows 4*(l/16)+r are exactly the k operand of the following
+// MFMA r: no data moves between lanes except for the row reductions.
+//
+// LDS tiles are padded by 4 floats per row: 16 lanes reading 16 bytes at one
+// column of 16 consecutive rows then touch 16 distinct 16-byte slots of the
+// 64 banks for every head dim here.
+#pragma once
+#include "attn_bwd.h"
+#include "attn_bwd_dq.h"
+#include "attn_fwd.h"
+#include "common.h"
+
+namespace dmad {
+
+__device__ __forceinline__ f32x4_t mfma16_f32(float a, float b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Reductions over the four lanes that share l%16 (one query row or key).
+__device__ __forceinline__ float quad_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+__device__ __forceinline__ f32x4_t ld4(const float* p) { return *(const f32x4_t*)p; }
+__device__ __forceinline__ f32x4_t buf_load_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(f32x4_t, buf_load16(r, voff));
+}
+__device__ __forceinline__ void buf_store_f4(__amdgpu_buffer_rsrc_t r, f32x4_t v, uint32_t voff) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), r, (int)voff, 0, 0);
+}
+
+// ------------------------------------------------------------------ forward
+// 8 waves x 16 queries = 128-query tiles (the block-sparse task size), 32-key
+// steps. V is processed in column chunks (128 wide, 64 when Q and K are
+// 256 wide), each chunk by its own workgroup recomputing the scores, so Q, Qd
+// and the O~, C~ accumulators fit 256 registers without spills.
+template <int DQK, int DV, int MODE>
+struct F32FwdCfg {
+  static constexpr int NW = 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BM = 16 * NW;
+  static constexpr int BN = 32;
+  static constexpr int NB = BN / 16;
+  static constexpr int DVC = DV < (DQK > 128 ? 64 : 128) ? DV : (DQK > 128 ? 64 : 128);  // V columns per workgroup
+  static constexpr int NCH = DV / DVC;             // workgroups per query tile
+  static constexpr int KT = DQK / 16;              // 16-wide d chunks of the scores
+  static constexpr int DB = DVC / 16;              // 16-row blocks of O^T
+  static constexpr int KP = DQK + 4;               // K row pitch (floats)
+  static constexpr int VP = BN + 4;                // V^T row pitch
+  static constexpr bool JVP = MODE != kFwdPlain;
+  static constexpr bool KVT = MODE == kFwdJvp;
+  static constexpr int K_FLOATS = BN * KP;
+  static constexpr int V_FLOATS = DVC * VP;
+  static constexpr int LDS_FLOATS = (KVT ? 2 : 1) * (K_FLOATS + V_FLOATS);
+  static constexpr int KCH = BN * DQK / 4;  // float4 chunks of a K tile
+  static constexpr int VCH = BN * DVC / 4;  // ... of a V tile (one column chunk)
+  static constexpr int KPT = (KCH + NT - 1) / NT;
+  static constexpr int VPT = (VCH + NT - 1) / NT;
+  // the next tile is prefetched into registers while this one is used, unless
+  // that would push the wave past 256 registers
+  static constexpr bool PREFETCH = (KVT ? 2 : 1) * (KPT + VPT) * 4 + (JVP ? 2 : 1) * DQK / 4 + 2 * DVC / 4 <= 176;
+  static_assert(LDS_FLOATS * 4 <= 160 * 1024, "tile exceeds LDS");
+};
+
+template <int DQK, int DV, int MODE, bool MAGI>
+__global__ __launch_bounds__(512) void attn_f32_fwd_kernel(FwdParams p) {
+  using C = F32FwdCfg<DQK, DV, MODE>;
+  constexpr int BN = C::BN, NB = C::NB, KT = C::KT, DB = C::DB, KP = C::KP, VP = C::VP, DVC = C::DVC;
+  __shared__ __attribute__((aligned(16))) float smem[C::LDS_FLOATS];
+  float* const sk = smem;                   // K rows  [BN][KP]
+  float* const sv = smem + C::K_FLOATS;     // V^T     [DVC][VP]
+  float* const skt = sv + C::V_FLOATS;      // Kd rows (mode kFwdJvp)
+  float* const svt = skt + C::K_FLOATS;     // Vd^T
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, g = lane >> 4;
+
+  int bh, row0, chunk, ntiles;
+  int q_lo = 0, q_hi = p.Lq;  // rows this workgroup stores
+  MagiCursor cm{0, 0, 0, 0, 0};
+  if constexpr (MAGI) {
+    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H * C::NCH);
+    chunk = work % C::NCH;
+    const int w2 = work / C::NCH;
+    bh = w2 / p.T;
+    const MagiTask t = magi_task(p, w2 - bh * p.T, C::BM);
+    row0 = t.row0;
+    q_lo = t.q_lo;
+    q_hi = t.q_hi;
+    ntiles = magi_ntiles(p, t, BN);
+    if (ntiles == 0) {  // uniform over the workgroup: the rows get O = Od = 0, LSE = -inf
+      const int b = bh / p.H, h = bh - b * p.H;
+      const int lo = max(t.row0, t.q_lo), hi = min(t.row0 + C::BM, t.q_hi);
+      const int64_t obase = b * p.o_sb + h * p.o_sh;
+      for (int idx = tid; idx < (hi - lo) * (DVC / 4); idx += C::NT) {
+        const int r = lo + idx / (DVC / 4), c4 = idx % (DVC / 4);
+        const int64_t off = obase + (int64_t)r * p.o_sl + chunk * DVC + 4 * c4;
+        *(f32x4_t*)((float*)p.o + off) = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (C::JVP) *(f32x4_t*)((float*)p.to + off) = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      if (chunk == 0) {
+        for (int r = lo + tid; r < hi; r += C::NT) {
+          p.lse[(int64_t)bh * p.Lq + r] = -__builtin_inff();
+          if constexpr (C::JVP) p.mu[(int64_t)bh * p.Lq + r] = 0.f;
+        }
+      }
+      return;
+    }
+    cm = MagiCursor{t.r_beg, t.r_end, 0, 0, 0};
+    cm.seek(p, BN);
+  } else {
+    const int work = work_item(p.xcd_order);
+    chunk = work % C::NCH;
+    const int w2 = work / C::NCH;
+    const int nqt = (p.Lq + C::BM - 1) / C::BM;
+    bh = w2 / nqt;
+    row0 = (w2 - bh * nqt) * C::BM;
+    ntiles = (p.Lk + BN - 1) / BN;
+  }
+  MagiCursor ci = cm;  // MAGI: the tile requested next
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + DQK) * 4);
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + DQK) * 4);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + DV) * 4);
+  const int64_t qh = b * p.q_sb + h * p.q_sh;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const float*)p.q + qh, q_bytes);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const float*)p.k + b * p.k_sb + h * p.k_sh, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const float*)p.v + b * p.v_sb + h * p.v_sh, v_bytes);
+  __amdgpu_buffer_rsrc_t rtq = rq, rtk = rk, rtv = rv;
+  if constexpr (C::JVP) rtq = make_rsrc((const float*)p.tq + qh, q_bytes);
+  if constexpr (C::KVT) {
+    rtk = make_rsrc((const float*)p.tk + b * p.k_sb + h * p.k_sh, k_bytes);
+    rtv = make_rsrc((const float*)p.tv + b * p.v_sb + h * p.v_sh, v_bytes);
+  }
+
+  // ---- Q (and Qd) fragments: lane (query col, g) holds d = 16t + 4g .. +3
+  const int qrow = row0 + wave * 16 + col;
+  const uint32_t qoff = qrow < p.Lq ? (uint32_t)((int64_t)qrow * p.q_sl * 4) + g * 16 : q_bytes;
+  f32x4_t q4[KT], tq4[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    q4[t] = buf_load_f4(rq, qoff + t * 64);
+    if constexpr (C::JVP) tq4[t] = buf_load_f4(rtq, qoff + t * 64);
+  }
+
+  // ---- one key tile: global -> registers -> LDS (K rows, V transposed);
+  // keys at or beyond Lk read as zero (and are masked in the scores)
+  f32x4_t kr[C::KPT], ktr[C::KPT], vr[C::VPT], vtr[C::VPT];
+  auto fetch = [&](int start) {
+#pragma unroll
+    for (int j = 0; j < C::KPT; ++j) {
+      const int c = tid + j * C::NT;
+      const int row = c / (DQK / 4), c4 = c % (DQK / 4);
+      const int key = start + row;
+      const uint32_t off = (c < C::KCH && key < p.Lk) ? (uint32_t)((int64_t)key * p.k_sl * 4) + c4 * 16 : k_bytes;
+      kr[j] = buf_load_f4(rk, off);
+      if constexpr (C::KVT) ktr[j] = buf_load_f4(rtk, off);
+    }
+#pragma unroll
+    for (int j = 0; j < C::VPT; ++j) {
+      const int c = tid + j * C::NT;
+      const int key = c % BN, c4 = c / BN;  // consecutive threads on consecutive keys
+      const int kg = start + key;
+      const uint32_t off =
+          (c < C::VCH && kg < p.Lk) ? (uint32_t)((int64_t)kg * p.v_sl * 4) + (chunk * DVC + 4 * c4) * 4 : v_bytes;
+      vr[j] = buf_load_f4(rv, off);
+      if constexpr (C::KVT) vtr[j] = buf_load_f4(rtv, off);
+    }
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int j = 0; j < C::KPT; ++j) {
+      const int c = tid + j * C::NT;
+      if (c < C::KCH) {
+        const int row = c / (DQK / 4), c4 = c % (DQK / 4);
+        *(f32x4_t*)(sk + row * KP + 4 * c4) = kr[j];
+        if constexpr (C::KVT) *(f32x4_t*)(skt + row * KP + 4 * c4) = ktr[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::VPT; ++j) {
+      const int c = tid + j * C::NT;
+      if (c < C::VCH) {
+        const int key = c % BN, c4 = c / BN;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sv[(4 * c4 + e) * VP + key] = vr[j][e];
+          if constexpr (C::KVT) svt[(4 * c4 + e) * VP + key] = vtr[j][e];
+        }
+      }
+    }
+  };
+
+  f32x4_t oacc[DB], cacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+    oacc[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    cacc[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
+
+  if constexpr (C::PREFETCH) fetch(MAGI ? ci.start : 0);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int start = MAGI ? cm.start : kt * BN;
+    __syncthreads();  // every wave is done with the previous tile
+    if constexpr (!C::PREFETCH) fetch(start);
+    put();
+    if constexpr (MAGI) ci.next(p, BN);
+    if constexpr (C::PREFETCH) {
+      if (kt + 1 < ntiles) fetch(MAGI ? ci.start : (kt + 1) * BN);
+    }
+    __syncthreads();
+
+    // ---- S^T, Sd^T (16 keys x 16 queries per block)
+    f32x4_t sacc[NB], tacc[NB];
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+      sacc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      tacc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int off = (kb * 16 + col) * KP + 16 * t + 4 * g;
+        const f32x4_t ak = ld4(sk + off);
+        f32x4_t akt;
+        if constexpr (C::KVT) akt = ld4(skt + off);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          sacc[kb] = mfma16_f32(ak[u], q4[t][u], sacc[kb]);
+          if constexpr (C::JVP) tacc[kb] = mfma16_f32(ak[u], tq4[t][u], tacc[kb]);
+          if constexpr (C::KVT) tacc[kb] = mfma16_f32(akt[u], q4[t][u], tacc[kb]);
+        }
+      }
+    }
+
+    // ---- keys beyond Lk (MAGI: outside the current range) -> -inf
+    if constexpr (MAGI) {
+      if (cm.partial(BN)) {
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (cm.masked(start + kb * 16 + 4 * g + r)) sacc[kb][r] = -__builtin_inff();
+          }
+        }
+      }
+      cm.next(p, BN);
+    } else if (start + BN > p.Lk) {
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (start + kb * 16 + 4 * g + r >= p.Lk) sacc[kb][r] = -__builtin_inff();
+        }
+      }
+    }
+
+    // ---- online softmax, log2 domain, exact running max
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sacc[kb][r]);
+    }
+    mx = quad_max(mx);
+    const float m_new = fmaxf(m_i, mx * p.scale_log2);
+    const float alpha = fast_exp2(m_i - m_new);
+    float ls = 0.f, rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = fast_exp2(fmaf(sacc[kb][r], p.scale_log2, -m_new));
+        sacc[kb][r] = pv;
+        ls += pv;
+        if constexpr (C::JVP) {
+          const float hv = pv * (tacc[kb][r] * p.scale);
+          tacc[kb][r] = hv;
+          rs += hv;
+        }
+      }
+    }
+    l_i = l_i * alpha + ls;
+    if constexpr (C::JVP) r_i = r_i * alpha + rs;
+    m_i = m_new;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      oacc[d] *= alpha;
+      if constexpr (C::JVP) cacc[d] *= alpha;
+    }
+
+    // ---- O~^T += V^T P^T; C~^T += Vd^T P^T + V^T H~^T
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int off = (d * 16 + col) * VP + kb * 16 + 4 * g;
+        const f32x4_t av = ld4(sv + off);
+        f32x4_t avt;
+        if constexpr (C::KVT) avt = ld4(svt + off);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          oacc[d] = mfma16_f32(av[r], sacc[kb][r], oacc[d]);
+          if constexpr (C::KVT) cacc[d] = mfma16_f32(avt[r], sacc[kb][r], cacc[d]);
+          if constexpr (C::JVP) cacc[d] = mfma16_f32(av[r], tacc[kb][r], cacc[d]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: O = O~/l, Od = C~/l - mu O, LSE, mu
+  const float l = quad_sum(l_i);
+  const float inv_l = 1.0f / l;
+  float mu = 0.f;
+  if constexpr (C::JVP) mu = quad_sum(r_i) * inv_l;
+  const int64_t obase = b * p.o_sb + h * p.o_sh;
+  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + DV) * 4);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc((float*)p.o + obase, o_bytes);
+  __amdgpu_buffer_rsrc_t rto = ro;
+  if constexpr (C::JVP) rto = make_rsrc((float*)p.to + obase, o_bytes);
+  const bool keep = qrow < p.Lq && qrow >= q_lo && qrow < q_hi;
+  const uint32_t orow = keep ? (uint32_t)((int64_t)qrow * p.o_sl * 4) : o_bytes;
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+    f32x4_t ov, tv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ov[r] = oacc[d][r] * inv_l;
+      if constexpr (C::JVP) tv[r] = cacc[d][r] * inv_l - mu * ov[r];
+    }
+    const uint32_t off = orow + (chunk * DVC + d * 16 + 4 * g) * 4;
+    buf_store_f4(ro, ov, off);
+    if constexpr (C::JVP) buf_store_f4(rto, tv, off);
+  }
+  if (g == 0 && chunk == 0 && keep) {
+    const int64_t si = (int64_t)bh * p.Lq + qrow;
+    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    if constexpr (C::JVP) p.mu[si] = mu;
+  }
+}
+
+// ------------------------------------------------------------------ backward
+// Statistics of the fp32 dO-only backward, [BH][LQP] each: the log2-domain
+// LSE (LSE * log2 e; +inf on padding rows, so their P is 0) and
+// D = rowsum(dO * O) (0 on padding rows).
+struct F32PrepParams {
+  const float* o;
+  const float* dout;
+  const float* lse;
+  float* lse2;
+  float* dd;
+  int64_t o_sb, o_sh, o_sl;
+  int64_t do_sb, do_sh, do_sl;
+  int H, Lq, LQP, BH;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_f32_bwd_prep_kernel(F32PrepParams p) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.BH * p.LQP) return;
+  const int bh = (int)(i / p.LQP), q = (int)(i - (int64_t)bh * p.LQP);
+  const int b = bh / p.H, h = bh - b * p.H;
+  if (q >= p.Lq) {
+    p.lse2[i] = __builtin_inff();
+    p.dd[i] = 0.f;
+    return;
+  }
+  const float* o = p.o + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_sl;
+  const float* dout = p.dout + b * p.do_sb + h * p.do_sh + (int64_t)q * p.do_sl;
+  float acc = 0.f;
+#pragma unroll 4
+  for (int c = 0; c < D; c += 4) {
+    const f32x4_t a = ld4(o + c), d = ld4(dout + c);
+    acc += a[0] * d[0] + a[1] * d[1] + a[2] * d[2] + a[3] * d[3];
+  }
+  p.lse2[i] = p.lse[(int64_t)bh * p.Lq + q] * 1.4426950408889634f;
+  p.dd[i] = acc;
+}
+
+// Key pass: each wave keeps 16 keys' K and V (B operands of S = Q K^T and
+// dP = dO V^T) and their dK^T, dV^T accumulators; the queries stream through
+// LDS 32 at a time, as rows (A operands of S, dP) and transposed (A operands
+// of dV^T += dO^T P, dK^T += Q^T dS). 256-wide heads run 4 waves (512
+// registers each), the others 8.
+template <int D>
+struct F32KvCfg {
+  static constexpr int NW = D > 128 ? 4 : 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BK = 16 * NW;  // keys per workgroup
+  static constexpr int BMQ = D > 128 ? 16 : 32;  // queries per step
+  static constexpr int QB = BMQ / 16;
+  static constexpr int KT = D / 16;
+  static constexpr int RP = D + 4;    // row pitch
+  static constexpr int TP = BMQ + 4;  // transposed pitch
+  static constexpr int R_FLOATS = BMQ * RP;
+  static constexpr int T_FLOATS = D * TP;
+  static constexpr int LDS_FLOATS = 2 * R_FLOATS + 2 * T_FLOATS + 2 * BMQ;
+  static constexpr int CH = BMQ * D / 4;  // float4 chunks of a Q (or dO) tile
+  static constexpr int PT = (CH + NT - 1) / NT;
+  static_assert(LDS_FLOATS * 4 <= 160 * 1024, "tile exceeds LDS");
+};
+
+template <int D>
+__global__ __launch_bounds__(F32KvCfg<D>::NT) void attn_f32_bwd_kv_kernel(BwdParams p, const float* lse2,
+                                                                          const float* dd) {
+  using C = F32KvCfg<D>;
+  constexpr int BMQ = C::BMQ, QB = C::QB, KT = C::KT, RP = C::RP, TP = C::TP;
+  __shared__ __attribute__((aligned(16))) float smem[C::LDS_FLOATS];
+  float* const sq = smem;                  // Q rows   [BMQ][RP]
+  float* const sdo = sq + C::R_FLOATS;     // dO rows
+  float* const sqt = sdo + C::R_FLOATS;    // Q^T      [D][TP]
+  float* const sdot = sqt + C::T_FLOATS;   // dO^T
+  float* const sst = sdot + C::T_FLOATS;   // lse2 [BMQ], D [BMQ]
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, g = lane >> 4;
+  const int nkt = (p.Lk + C::BK - 1) / C::BK;
+  const int work = work_item(p.xcd_order);
+  const int bh = work / nkt, kt = work - bh * nkt;
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 4);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 4);
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 4);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 4);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const float*)p.q + b * p.q_sb + h * p.q_sh, q_bytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const float*)p.dout + b * p.do_sb + h * p.do_sh, do_bytes);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const float*)p.k + b * p.k_sb + h * p.k_sh, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const float*)p.v + b * p.v_sb + h * p.v_sh, v_bytes);
+
+  // ---- this wave's 16 keys: lane (key col, g) holds d = 16t + 4g .. +3
+  const int key = kt * C::BK + wave * 16 + col;
+  const uint32_t koff = key < p.Lk ? (uint32_t)((int64_t)key * p.k_sl * 4) + g * 16 : k_bytes;
+  const uint32_t voff = key < p.Lk ? (uint32_t)((int64_t)key * p.v_sl * 4) + g * 16 : v_bytes;
+  f32x4_t k4[KT], v4[KT], dk[KT], dv[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    k4[t] = buf_load_f4(rk, koff + t * 64);
+    v4[t] = buf_load_f4(rv, voff + t * 64);
+    dk[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    dv[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const float* lse2_h = lse2 + (int64_t)bh * p.LQP;
+  const float* dd_h = dd + (int64_t)bh * p.LQP;
+  f32x4_t qr[C::PT], dr[C::PT];
+  float stat = 0.f;
+  auto fetch = [&](int q0) {
+#pragma unroll
+    for (int j = 0; j < C::PT; ++j) {
+      const int c = tid + j * C::NT;
+      const int row = c / (D / 4), c4 = c % (D / 4);
+      const int q = q0 + row;
+      const bool in = c < C::CH && q < p.Lq;
+      qr[j] = buf_load_f4(rq, in ? (uint32_t)((int64_t)q * p.q_sl * 4) + c4 * 16 : q_bytes);
+      dr[j] = buf_load_f4(rdo, in ? (uint32_t)((int64_t)q * p.do_sl * 4) + c4 * 16 : do_bytes);
+    }
+    // padded statistics rows (q < LQP) exist; q0 + BMQ <= LQP
+    if (tid < 2 * BMQ) stat = tid < BMQ ? lse2_h[q0 + tid] : dd_h[q0 + tid - BMQ];
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int j = 0; j < C::PT; ++j) {
+      const int c = tid + j * C::NT;
+      if (c < C::CH) {
+        const int row = c / (D / 4), c4 = c % (D / 4);
+        *(f32x4_t*)(sq + row * RP + 4 * c4) = qr[j];
+        *(f32x4_t*)(sdo + row * RP + 4 * c4) = dr[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sqt[(4 * c4 + e) * TP + row] = qr[j][e];
+          sdot[(4 * c4 + e) * TP + row] = dr[j][e];
+        }
+      }
+    }
+    if (tid < 2 * BMQ) sst[tid] = stat;
+  };
+
+  const int nq = (p.Lq + BMQ - 1) / BMQ;
+  fetch(0);
+  for (int qt = 0; qt < nq; ++qt) {
+    __syncthreads();
+    put();
+    if (qt + 1 < nq) fetch((qt + 1) * BMQ);
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      // S, dP: 16 queries x 16 keys; lane (key col, g) holds queries 4g + r
+      f32x4_t s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int off = (qb * 16 + col) * RP + 16 * t + 4 * g;
+        const f32x4_t aq = ld4(sq + off), ado = ld4(sdo + off);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          s = mfma16_f32(aq[u], k4[t][u], s);
+          dp = mfma16_f32(ado[u], v4[t][u], dp);
+        }
+      }
+      const f32x4_t l2 = ld4(sst + qb * 16 + 4 * g), dq = ld4(sst + BMQ + qb * 16 + 4 * g);
+      f32x4_t pv, ds;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pv[r] = fast_exp2(fmaf(s[r], p.scale_log2, -l2[r]));
+        ds[r] = pv[r] * (dp[r] - dq[r]);
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS (16 d x 16 keys per block)
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int off = (t * 16 + col) * TP + qb * 16 + 4 * g;
+        const f32x4_t adot = ld4(sdot + off), aqt = ld4(sqt + off);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          dv[t] = mfma16_f32(adot[r], pv[r], dv[t]);
+          dk[t] = mfma16_f32(aqt[r], ds[r], dk[t]);
+        }
+      }
+    }
+  }
+
+  // ---- lane (key col, g) holds dK, dV[key][16t + 4g .. +3]
+  const uint32_t dk_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.dk_sl + D) * 4);
+  const uint32_t dv_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.dv_sl + D) * 4);
+  const __amdgpu_buffer_rsrc_t rdk = make_rsrc((float*)p.dk + b * p.dk_sb + h * p.dk_sh, dk_bytes);
+  const __amdgpu_buffer_rsrc_t rdv = make_rsrc((float*)p.dv + b * p.dv_sb + h * p.dv_sh, dv_bytes);
+  const uint32_t okd = key < p.Lk ? (uint32_t)((int64_t)key * p.dk_sl * 4) + g * 16 : dk_bytes;
+  const uint32_t ovd = key < p.Lk ? (uint32_t)((int64_t)key * p.dv_sl * 4) + g * 16 : dv_bytes;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    buf_store_f4(rdk, dk[t] * p.scale, okd + t * 64);
+    buf_store_f4(rdv, dv[t], ovd + t * 64);
+  }
+}
+
+// Query pass: each wave keeps 16 queries' Q and dO (B operands of S^T = K Q^T
+// and dP^T = V dO^T), their statistics and the dQ^T accumulator; the keys
+// stream through LDS 32 at a time, as rows (A operands of S^T, dP^T) and K
+// transposed (A operand of dQ^T += K^T dS^T).
+template <int D>
+struct F32DqCfg {
+  static constexpr int NW = D > 128 ? 4 : 8;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BM = 16 * NW;  // queries per workgroup
+  static constexpr int BN = 32;       // keys per step
+  static constexpr int NB = BN / 16;
+  static constexpr int KT = D / 16;
+  static constexpr int RP = D + 4;
+  static constexpr int TP = BN + 4;
+  static constexpr int R_FLOATS = BN * RP;
+  static constexpr int T_FLOATS = D * TP;
+  static constexpr int LDS_FLOATS = 2 * R_FLOATS + T_FLOATS;
+  static constexpr int CH = BN * D / 4;
+  static constexpr int PT = (CH + NT - 1) / NT;
+  static_assert(LDS_FLOATS * 4 <= 160 * 1024, "tile exceeds LDS");
+};
+
+template <int D>
+__global__ __launch_bounds__(F32DqCfg<D>::NT) void attn_f32_bwd_dq_kernel(DqParams p, const float* lse2,
+                                                                          const float* dd) {
+  using C = F32DqCfg<D>;
+  constexpr int BN = C::BN, NB = C::NB, KT = C::KT, RP = C::RP, TP = C::TP;
+  __shared__ __attribute__((aligned(16))) float smem[C::LDS_FLOATS];
+  float* const sk = smem;               // K rows [BN][RP]
+  float* const sv = sk + C::R_FLOATS;   // V rows
+  float* const skt = sv + C::R_FLOATS;  // K^T [D][TP]
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, g = lane >> 4;
+  const int nqt = (p.Lq + C::BM - 1) / C::BM;
+  const int work = work_item(p.xcd_order);
+  const int bh = work / nqt, qt = work - bh * nqt;
+  const int b = bh / p.H, h = bh - b * p.H;
+
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 4);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.do_sl + D) * 4);
+  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 4);
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 4);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc((const float*)p.q + b * p.q_sb + h * p.q_sh, q_bytes);
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc((const float*)p.dout + b * p.do_sb + h * p.do_sh, do_bytes);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const float*)p.k + b * p.k_sb + h * p.k_sh, k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const float*)p.v + b * p.v_sb + h * p.v_sh, v_bytes);
+
+  // ---- this wave's 16 queries: lane (query col, g) holds d = 16t + 4g .. +3
+  const int q = qt * C::BM + wave * 16 + col;
+  const uint32_t qoff = q < p.Lq ? (uint32_t)((int64_t)q * p.q_sl * 4) + g * 16 : q_bytes;
+  const uint32_t dooff = q < p.Lq ? (uint32_t)((int64_t)q * p.do_sl * 4) + g * 16 : do_bytes;
+  f32x4_t q4[KT], do4[KT], dq[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    q4[t] = buf_load_f4(rq, qoff + t * 64);
+    do4[t] = buf_load_f4(rdo, dooff + t * 64);
+    dq[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // rows q < LQP of the statistics exist (padding rows: lse2 = +inf, D = 0)
+  const float l2 = q < p.LQP ? lse2[(int64_t)bh * p.LQP + q] : __builtin_inff();
+  const float dq_row = q < p.LQP ? dd[(int64_t)bh * p.LQP + q] : 0.f;
+
+  f32x4_t kr[C::PT], vr[C::PT];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < C::PT; ++j) {
+      const int c = tid + j * C::NT;
+      const int row = c / (D / 4), c4 = c % (D / 4);
+      const int key = k0 + row;
+      const bool in = c < C::CH && key < p.Lk;
+      kr[j] = buf_load_f4(rk, in ? (uint32_t)((int64_t)key * p.k_sl * 4) + c4 * 16 : k_bytes);
+      vr[j] = buf_load_f4(rv, in ? (uint32_t)((int64_t)key * p.v_sl * 4) + c4 * 16 : v_bytes);
+    }
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int j = 0; j < C::PT; ++j) {
+      const int c = tid + j * C::NT;
+      if (c < C::CH) {
+        const int row = c / (D / 4), c4 = c % (D / 4);
+        *(f32x4_t*)(sk + row * RP + 4 * c4) = kr[j];
+        *(f32x4_t*)(sv + row * RP + 4 * c4) = vr[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) skt[(4 * c4 + e) * TP + row] = kr[j][e];
+      }
+    }
+  };
+
+  const int nk = (p.Lk + BN - 1) / BN;
+  fetch(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    __syncthreads();
+    put();
+    if (kt + 1 < nk) fetch((kt + 1) * BN);
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+      // S^T, dP^T: 16 keys x 16 queries; lane (query col, g) holds keys 4g + r
+      f32x4_t s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int off = (kb * 16 + col) * RP + 16 * t + 4 * g;
+        const f32x4_t ak = ld4(sk + off), av = ld4(sv + off);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          s = mfma16_f32(ak[u], q4[t][u], s);
+          dp = mfma16_f32(av[u], do4[t][u], dp);
+        }
+      }
+      f32x4_t ds;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kg = kt * BN + kb * 16 + 4 * g + r;
+        const float pv = kg < p.Lk ? fast_exp2(fmaf(s[r], p.scale_log2, -l2)) : 0.f;
+        ds[r] = pv * (dp[r] - dq_row);
+      }
+      // dQ^T += K^T dS^T (16 d x 16 queries per block)
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const f32x4_t akt = ld4(skt + (t * 16 + col) * TP + kb * 16 + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dq[t] = mfma16_f32(akt[r], ds[r], dq[t]);
+      }
+    }
+  }
+
+  const uint32_t dq_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.dq_sl + D) * 4);
+  const __amdgpu_buffer_rsrc_t rdq = make_rsrc((float*)p.dq + b * p.dq_sb + h * p.dq_sh, dq_bytes);
+  const uint32_t oq = q < p.Lq ? (uint32_t)((int64_t)q * p.dq_sl * 4) + g * 16 : dq_bytes;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) buf_store_f4(rdq, dq[t] * p.scale, oq + t * 64);
+}
+
+}  // namespace dmad

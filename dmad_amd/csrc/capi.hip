@@ -88,24 +88,51 @@ constexpr int64_t kLkAlign = 64;                       // key padding of transpo
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// Checks one [B,H,L,D] operand: pointer, unit inner stride, 16-byte alignment
-// of every row start, and that one (b, h) slice fits 32-bit byte offsets
-// (with 256 rows of slack for tile overrun).
-int check_operand(const char* name, const void* ptr, const int64_t* st, int64_t L, int64_t D) {
+// Checks one [B,H,L,D] operand of `esz`-byte elements: pointer, unit inner
+// stride, 16-byte alignment of every row start, and that one (b, h) slice fits
+// 32-bit byte offsets (with 256 rows of slack for tile overrun).
+int check_operand(const char* name, const void* ptr, const int64_t* st, int64_t L, int64_t D, int esz = 2) {
   if (ptr == nullptr) return fail(DMAD_ERR_INVALID, "%s: null pointer", name);
   if (st == nullptr) return fail(DMAD_ERR_INVALID, "%s: null strides", name);
   if (st[3] != 1) return fail(DMAD_ERR_INVALID, "%s: stride of the head dim must be 1, got %lld", name, (long long)st[3]);
+  const int align = 16 / esz;
   for (int i = 0; i < 3; ++i) {
     if (st[i] < 0) return fail(DMAD_ERR_INVALID, "%s: negative stride %lld", name, (long long)st[i]);
-    if (st[i] % 8 != 0)
-      return fail(DMAD_ERR_INVALID, "%s: strides must be multiples of 8 elements (16 bytes), got %lld", name,
+    if (st[i] % align != 0)
+      return fail(DMAD_ERR_INVALID, "%s: strides must be multiples of %d elements (16 bytes), got %lld", name, align,
                   (long long)st[i]);
   }
   if (L > 1 && st[2] < D) return fail(DMAD_ERR_INVALID, "%s: rows overlap (stride %lld < D %lld)", name, (long long)st[2], (long long)D);
   if (((uintptr_t)ptr & 15) != 0) return fail(DMAD_ERR_INVALID, "%s: base pointer must be 16-byte aligned", name);
-  if (((L + 256) * st[2] + D) * 2 >= kMaxHeadBytes)
+  if (((L + 256) * st[2] + D) * esz >= kMaxHeadBytes)
     return fail(DMAD_ERR_UNSUPPORTED, "%s: one (batch, head) slice spans more than 2 GiB", name);
   return DMAD_OK;
+}
+
+int elem_size(int dtype) { return dtype == DMAD_F32 ? 4 : 2; }
+
+dmad::FwdLaunchFn pick_fwd_f32(int64_t dqk, int64_t dv, int mode, bool magi) {
+  using namespace dmad;
+  switch (dqk) {
+    case 16: return f32_fwd_select<16>((int)dv, mode, magi);
+    case 32: return f32_fwd_select<32>((int)dv, mode, magi);
+    case 64: return f32_fwd_select<64>((int)dv, mode, magi);
+    case 128: return f32_fwd_select<128>((int)dv, mode, magi);
+    case 256: return f32_fwd_select<256>((int)dv, mode, magi);
+  }
+  return nullptr;
+}
+
+dmad::F32BwdFns pick_bwd_f32(int64_t d) {
+  using namespace dmad;
+  switch (d) {
+    case 16: return f32_bwd_select<16>();
+    case 32: return f32_bwd_select<32>();
+    case 64: return f32_bwd_select<64>();
+    case 128: return f32_bwd_select<128>();
+    case 256: return f32_bwd_select<256>();
+  }
+  return F32BwdFns{};
 }
 
 // Bytes of the transposed, key-padded V (and Vd) copies the generic forward
@@ -288,7 +315,8 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
              const int64_t k_strides[4], const int64_t v_strides[4], void* o, void* to, const int64_t o_strides[4],
              float* lse, float* mu, float sm_scale, void* workspace, size_t workspace_bytes, void* stream,
              const MagiArgs* mg) {
-  if (dtype != DMAD_BF16 && dtype != DMAD_F16) return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+  if (dtype != DMAD_BF16 && dtype != DMAD_F16 && dtype != DMAD_F32)
+    return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
   if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
   if (B < 0 || H < 0 || Lq < 0 || Lk < 0) return fail(DMAD_ERR_INVALID, "negative size");
   if (!head_dim_ok(Dqk) || !head_dim_ok(Dv))
@@ -302,29 +330,32 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
   if (B * H > ((int64_t)1 << 24) || Lq >= ((int64_t)1 << 26) || Lk >= ((int64_t)1 << 26))
     return fail(DMAD_ERR_UNSUPPORTED, "sizes too large");
   const bool jvp = mode != DMAD_FWD_PLAIN, kvt = mode == DMAD_FWD_JVP;
+  const bool f32 = dtype == DMAD_F32;
+  const int esz = elem_size(dtype);
   int rc;
-  if ((rc = check_operand("q", q, q_strides, Lq, Dqk))) return rc;
-  if ((rc = check_operand("k", k, k_strides, Lk, Dqk))) return rc;
-  if ((rc = check_operand("v", v, v_strides, Lk, Dv))) return rc;
-  if ((rc = check_operand("o", o, o_strides, Lq, Dv))) return rc;
+  if ((rc = check_operand("q", q, q_strides, Lq, Dqk, esz))) return rc;
+  if ((rc = check_operand("k", k, k_strides, Lk, Dqk, esz))) return rc;
+  if ((rc = check_operand("v", v, v_strides, Lk, Dv, esz))) return rc;
+  if ((rc = check_operand("o", o, o_strides, Lq, Dv, esz))) return rc;
   if (jvp) {
-    if ((rc = check_operand("tq", tq, q_strides, Lq, Dqk))) return rc;
-    if ((rc = check_operand("to", to, o_strides, Lq, Dv))) return rc;
+    if ((rc = check_operand("tq", tq, q_strides, Lq, Dqk, esz))) return rc;
+    if ((rc = check_operand("to", to, o_strides, Lq, Dv, esz))) return rc;
     if (mu == nullptr) return fail(DMAD_ERR_INVALID, "mu: null pointer");
   }
   if (kvt) {
-    if ((rc = check_operand("tk", tk, k_strides, Lk, Dqk))) return rc;
-    if ((rc = check_operand("tv", tv, v_strides, Lk, Dv))) return rc;
+    if ((rc = check_operand("tk", tk, k_strides, Lk, Dqk, esz))) return rc;
+    if ((rc = check_operand("tv", tv, v_strides, Lk, Dv, esz))) return rc;
   }
   if (lse == nullptr) return fail(DMAD_ERR_INVALID, "lse: null pointer");
-  const int64_t need = fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
+  const int64_t need = f32 ? 0 : fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
   if (need > 0 && (workspace == nullptr || (int64_t)workspace_bytes < need))
     return fail(DMAD_ERR_WORKSPACE, "workspace needs %lld bytes, got %lld", (long long)need, (long long)workspace_bytes);
   if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
   const int64_t dvp = Dv < 32 ? 32 : Dv, lkp = round_up(Lk, kLkAlign);
   if (dvp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "Lk too large");
 
-  dmad::FwdLaunchFn fn = mg ? pick_fwd_magi(dtype, Dqk, Dv, mode) : pick_fwd(dtype, Dqk, Dv, mode);
+  dmad::FwdLaunchFn fn = f32 ? pick_fwd_f32(Dqk, Dv, mode, mg != nullptr)
+                             : mg ? pick_fwd_magi(dtype, Dqk, Dv, mode) : pick_fwd(dtype, Dqk, Dv, mode);
   if (fn == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no kernel for Dqk=%lld Dv=%lld", (long long)Dqk, (long long)Dv);
 
   hipStream_t s = (hipStream_t)stream;
@@ -333,7 +364,7 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
   const int64_t vt_bytes = round_up(B * H * dvp * lkp * 2, 256);
   // kernels for 128-wide heads transpose V on the LDS read; the others read a
   // transposed, key-padded copy made here
-  const bool need_vt = !dmad::fwd32_supported((int)Dqk, (int)Dv);
+  const bool need_vt = !f32 && !dmad::fwd32_supported((int)Dqk, (int)Dv);
   hipError_t e = hipSuccess;
   dmad::TransposeParams tp{v, ws, v_strides[0], v_strides[1], v_strides[2], (int)H, (int)Lk, (int)Dv, (int)lkp, (int)dvp};
   if (need_vt) e = dmad::launch_transpose_pad(tp, BH, s);
@@ -390,14 +421,16 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
     p.T = (int)mg->T;
     units = mg->T;
   }
-  if (units * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
-  int64_t grid = units * BH;
+  // fp32: wide V runs several workgroups per query tile, one per column chunk (attn_f32.h)
+  const int64_t chunks = f32 ? dmad::f32_fwd_chunks((int)Dqk, (int)Dv) : 1;
+  if (units * BH * chunks >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  int64_t grid = units * BH * chunks;
   p.xcd_order = units < dmad::kHeadMajorMinTiles;  // block order (common.h)
   // short key sequences, K and V tangents zero (the text cross-attention): the
   // persistent kernel (one workgroup per slot, looping over the query tiles)
   // overlaps each tile's Q reads and O writes with the key loop of the next
   const int64_t ktiles = (Lk + 31) / 32;
-  if (mg == nullptr && mode == DMAD_FWD_JVP_KV_TANGENT_ZERO && Dqk == Dv && dmad::fwd32p_supported(mode, (int)Dqk) &&
+  if (!f32 && mg == nullptr && mode == DMAD_FWD_JVP_KV_TANGENT_ZERO && Dqk == Dv && dmad::fwd32p_supported(mode, (int)Dqk) &&
       ktiles % 4 == 0 &&
       ktiles <= kPersistMaxKeyTiles) {
     int slots = 0;
@@ -465,7 +498,8 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
              const int64_t do_strides[4], void* dq, void* dk, void* dv, void* dtq, void* dtk, void* dtv,
              const int64_t dq_strides[4], const int64_t dk_strides[4], const int64_t dv_strides[4], float sm_scale,
              void* workspace, size_t workspace_bytes, void* stream, bool use_scratch) {
-  if (dtype != DMAD_BF16 && dtype != DMAD_F16) return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+  if (dtype != DMAD_BF16 && dtype != DMAD_F16 && dtype != DMAD_F32)
+    return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
   if (B < 0 || H < 0 || Lq < 0 || Lk < 0) return fail(DMAD_ERR_INVALID, "negative size");
   if (!head_dim_ok(D)) return fail(DMAD_ERR_UNSUPPORTED, "head dim must be in {16,32,64,128,256}, got %lld", (long long)D);
   if (!(sm_scale > 0.f)) return fail(DMAD_ERR_UNSUPPORTED, "sm_scale must be positive");
@@ -474,33 +508,36 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   if (tgrad && !(dtq && dtk && dtv)) return fail(DMAD_ERR_INVALID, "dtq, dtk, dtv must be all set or all null");
   if (tgrad && !full) return fail(DMAD_ERR_INVALID, "tangent gradients need the cotangent dto");
   if (full && D > 128) return fail(DMAD_ERR_UNSUPPORTED, "the full backward supports head dims up to 128");
+  const bool f32 = dtype == DMAD_F32;
+  if (full && f32) return fail(DMAD_ERR_UNSUPPORTED, "the full backward takes bf16 or fp16 operands (fp32: dO only)");
+  const int esz = elem_size(dtype);
   if (B == 0 || H == 0 || (Lq == 0 && Lk == 0)) return ok();
   if (Lk == 0) return fail(DMAD_ERR_INVALID, "Lk must be at least 1");
   if (Lq == 0) return fail(DMAD_ERR_INVALID, "Lq must be at least 1 (with no query rows dK and dV are zero)");
   if (B * H > ((int64_t)1 << 24) || Lq >= ((int64_t)1 << 26) || Lk >= ((int64_t)1 << 26))
     return fail(DMAD_ERR_UNSUPPORTED, "sizes too large");
   int rc;
-  if ((rc = check_operand("q", q, q_strides, Lq, D))) return rc;
-  if ((rc = check_operand("k", k, k_strides, Lk, D))) return rc;
-  if ((rc = check_operand("v", v, v_strides, Lk, D))) return rc;
-  if ((rc = check_operand("o", o, o_strides, Lq, D))) return rc;
-  if ((rc = check_operand("dout", dout, do_strides, Lq, D))) return rc;
-  if ((rc = check_operand("dq", dq, dq_strides, Lq, D))) return rc;
-  if ((rc = check_operand("dk", dk, dk_strides, Lk, D))) return rc;
-  if ((rc = check_operand("dv", dv, dv_strides, Lk, D))) return rc;
+  if ((rc = check_operand("q", q, q_strides, Lq, D, esz))) return rc;
+  if ((rc = check_operand("k", k, k_strides, Lk, D, esz))) return rc;
+  if ((rc = check_operand("v", v, v_strides, Lk, D, esz))) return rc;
+  if ((rc = check_operand("o", o, o_strides, Lq, D, esz))) return rc;
+  if ((rc = check_operand("dout", dout, do_strides, Lq, D, esz))) return rc;
+  if ((rc = check_operand("dq", dq, dq_strides, Lq, D, esz))) return rc;
+  if ((rc = check_operand("dk", dk, dk_strides, Lk, D, esz))) return rc;
+  if ((rc = check_operand("dv", dv, dv_strides, Lk, D, esz))) return rc;
   if (lse == nullptr) return fail(DMAD_ERR_INVALID, "lse: null pointer");
   if (full) {
-    if ((rc = check_operand("tq", tq, q_strides, Lq, D))) return rc;
-    if ((rc = check_operand("tk", tk, k_strides, Lk, D))) return rc;
-    if ((rc = check_operand("tv", tv, v_strides, Lk, D))) return rc;
-    if ((rc = check_operand("to", to, o_strides, Lq, D))) return rc;
-    if ((rc = check_operand("dto", dto, do_strides, Lq, D))) return rc;
+    if ((rc = check_operand("tq", tq, q_strides, Lq, D, esz))) return rc;
+    if ((rc = check_operand("tk", tk, k_strides, Lk, D, esz))) return rc;
+    if ((rc = check_operand("tv", tv, v_strides, Lk, D, esz))) return rc;
+    if ((rc = check_operand("to", to, o_strides, Lq, D, esz))) return rc;
+    if ((rc = check_operand("dto", dto, do_strides, Lq, D, esz))) return rc;
     if (mu == nullptr) return fail(DMAD_ERR_INVALID, "mu: null pointer");
   }
   if (tgrad) {
-    if ((rc = check_operand("dtq", dtq, dq_strides, Lq, D))) return rc;
-    if ((rc = check_operand("dtk", dtk, dk_strides, Lk, D))) return rc;
-    if ((rc = check_operand("dtv", dtv, dv_strides, Lk, D))) return rc;
+    if ((rc = check_operand("dtq", dtq, dq_strides, Lq, D, esz))) return rc;
+    if ((rc = check_operand("dtk", dtk, dk_strides, Lk, D, esz))) return rc;
+    if ((rc = check_operand("dtv", dtv, dv_strides, Lk, D, esz))) return rc;
   }
   const int fl = full ? (tgrad ? 2 : 1) : 0;
   const BwdWs w = bwd_ws(fl, B, H, Lq, Lk, D);
@@ -519,6 +556,49 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
   const int64_t dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign), BH = B * H;
   if (dp * lqp * 2 >= kMaxHeadBytes || dp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "sequence too long");
+  if (f32) {
+    // fp32 (dO only): statistics [BH][LQP] (log2 LSE, then D) at the start of
+    // the workspace, which the query sizes for the bf16 path and so always holds them
+    const dmad::F32BwdFns f = pick_bwd_f32(D);
+    if (f.prep == nullptr || f.kv == nullptr || f.dq == nullptr)
+      return fail(DMAD_ERR_UNSUPPORTED, "no fp32 backward kernel for D=%lld", (long long)D);
+    hipStream_t s = (hipStream_t)stream;
+    float* lse2 = (float*)workspace;
+    float* dd = lse2 + BH * lqp;
+    dmad::F32PrepParams pp{(const float*)o, (const float*)dout, lse, lse2, dd, o_strides[0], o_strides[1],
+                           o_strides[2], do_strides[0], do_strides[1], do_strides[2], (int)H, (int)Lq, (int)lqp,
+                           (int)BH};
+    dmad::BwdParams p{};
+    p.q = q; p.k = k; p.v = v; p.dout = dout; p.dk = dk; p.dv = dv;
+    p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_sl = q_strides[2];
+    p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_sl = k_strides[2];
+    p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_sl = v_strides[2];
+    p.do_sb = do_strides[0]; p.do_sh = do_strides[1]; p.do_sl = do_strides[2];
+    p.dk_sb = dk_strides[0]; p.dk_sh = dk_strides[1]; p.dk_sl = dk_strides[2];
+    p.dv_sb = dv_strides[0]; p.dv_sh = dv_strides[1]; p.dv_sl = dv_strides[2];
+    p.B = (int)B; p.H = (int)H; p.Lq = (int)Lq; p.Lk = (int)Lk; p.LQP = (int)lqp;
+    p.scale = sm_scale;
+    p.scale_log2 = sm_scale * 1.4426950408889634f;
+    dmad::DqParams pq{};
+    pq.q = q; pq.dout = dout; pq.k = k; pq.v = v; pq.dq = dq;
+    pq.q_sb = q_strides[0]; pq.q_sh = q_strides[1]; pq.q_sl = q_strides[2];
+    pq.do_sb = do_strides[0]; pq.do_sh = do_strides[1]; pq.do_sl = do_strides[2];
+    pq.k_sb = k_strides[0]; pq.k_sh = k_strides[1]; pq.k_sl = k_strides[2];
+    pq.v_sb = v_strides[0]; pq.v_sh = v_strides[1]; pq.v_sl = v_strides[2];
+    pq.dq_sb = dq_strides[0]; pq.dq_sh = dq_strides[1]; pq.dq_sl = dq_strides[2];
+    pq.B = (int)B; pq.H = (int)H; pq.Lq = (int)Lq; pq.Lk = (int)Lk; pq.LQP = (int)lqp; pq.LKP = (int)lkp;
+    pq.scale = sm_scale;
+    pq.scale_log2 = sm_scale * 1.4426950408889634f;
+    hipError_t e;
+    if ((e = f.prep(pp, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "prep launch: %s", hipGetErrorString(e));
+    mark(0, false, s);
+    if ((e = f.kv(p, lse2, dd, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+    mark(0, true, s);
+    mark(1, false, s);
+    if ((e = f.dq(pq, lse2, dd, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
+    mark(1, true, s);
+    return ok();
+  }
   const int mode = full ? dmad::kBwdFull : dmad::kBwdDoutOnly;
   // 128-wide heads: the full derivative's query pass also gives dQd, so the
   // tangent gradients need only the dO-only key pass (dKd, dVd)

@@ -8,6 +8,7 @@
 #include "attn_bwd.h"
 #include "attn_bwd_dq.h"
 #include "attn_bwd_full.h"
+#include "attn_f32.h"
 
 namespace dmad {
 
@@ -107,6 +108,34 @@ inline bool dout_only_reads_rows(int d) {
     default: return KvTrCfg<256, kKvTrBmq>::FITS && DqTrCfg<256>::FITS;
   }
 }
+
+// fp32 operands (attn_f32.h; f32_inst.hip, one compilation per head dim).
+// Forward launcher for (Dqk, Dv, mode), dense or block-sparse, or nullptr; the
+// grid is (query tiles or tasks) * B * H * f32_fwd_chunks(Dqk, Dv) workgroups.
+template <int DQK>
+FwdLaunchFn f32_fwd_select(int dv, int mode, bool magi);
+template <> FwdLaunchFn f32_fwd_select<16>(int, int, bool);
+template <> FwdLaunchFn f32_fwd_select<32>(int, int, bool);
+template <> FwdLaunchFn f32_fwd_select<64>(int, int, bool);
+template <> FwdLaunchFn f32_fwd_select<128>(int, int, bool);
+template <> FwdLaunchFn f32_fwd_select<256>(int, int, bool);
+constexpr int f32_fwd_chunks(int dqk, int dv) {
+  const int dvc = dqk > 128 ? 64 : 128;
+  return dv > dvc ? dv / dvc : 1;
+}
+// dO-only backward: statistics, key pass, query pass (each sizes its own grid).
+struct F32BwdFns {
+  hipError_t (*prep)(const F32PrepParams&, hipStream_t);
+  hipError_t (*kv)(const BwdParams&, const float* lse2, const float* dd, hipStream_t);
+  hipError_t (*dq)(const DqParams&, const float* lse2, const float* dd, hipStream_t);
+};
+template <int D>
+F32BwdFns f32_bwd_select();
+template <> F32BwdFns f32_bwd_select<16>();
+template <> F32BwdFns f32_bwd_select<32>();
+template <> F32BwdFns f32_bwd_select<64>();
+template <> F32BwdFns f32_bwd_select<128>();
+template <> F32BwdFns f32_bwd_select<256>();
 
 // Fused RMSNorm(+tangent) + interleaved RoPE prologue (prologue.hip).
 constexpr int kPrologueMaxChunks = 20;  // 16-byte chunks per lane: C <= 64 * 8 * 20

@@ -66,8 +66,9 @@ FULL_BWD_MAX_HEAD_DIM = 128
 _warned_full_fallback = False
 
 
-def _full_backward_unavailable(dqk: int, dv: int) -> bool:
-    """Backward mode for head dims the full derivative does not cover.
+def _full_backward_unavailable(dqk: int, dv: int, dtype: torch.dtype) -> bool:
+    """Backward mode for inputs the full derivative does not cover (head dims
+    above 128, fp32 operands).
 
     Mode "auto" falls back to the reference's backward (dO-only gradients, None
     for the tangents, :534-579) with a one-time warning, so the op runs wherever
@@ -75,17 +76,18 @@ def _full_backward_unavailable(dqk: int, dv: int) -> bool:
     raises here, in the forward, before any work is done.
     """
     global _warned_full_fallback
+    what = (f"head dims up to {FULL_BWD_MAX_HEAD_DIM} (got Dqk={dqk}, Dv={dv})" if max(dqk, dv) > FULL_BWD_MAX_HEAD_DIM
+            else f"bfloat16 and float16 operands (got {dtype})")
     if _BACKWARD_MODE == "full":
         raise NotImplementedError(
-            f"the full-derivative backward supports head dims up to {FULL_BWD_MAX_HEAD_DIM} "
-            f"(got Dqk={dqk}, Dv={dv}); use set_backward_mode('auto') or ('reference') for the "
-            "reference's dO-only gradients"
+            f"the full-derivative backward supports {what}; use set_backward_mode('auto') or ('reference') "
+            "for the reference's dO-only gradients"
         )
     if not _warned_full_fallback:
         import warnings
 
         warnings.warn(
-            f"head dim {max(dqk, dv)} > {FULL_BWD_MAX_HEAD_DIM}: the tangents get no gradients and the "
+            f"the full-derivative backward supports {what}: the tangents get no gradients and the "
             "cotangent of `to` is ignored (the reference backward's behaviour)",
             stacklevel=3,
         )
@@ -97,7 +99,8 @@ def _kernel_ready(t: torch.Tensor) -> bool:
     """Unit inner stride, 16-byte aligned rows (what the kernels load from)."""
     if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
         return False
-    return all(s % 8 == 0 for s in t.stride()[:-1])
+    per16 = 16 // t.element_size()
+    return all(s % per16 == 0 for s in t.stride()[:-1])
 
 
 def _prep(*ts):
@@ -113,6 +116,11 @@ def _pair(x, tx):
     if x.stride() == tx.stride() and _kernel_ready(x) and _kernel_ready(tx):
         return x, tx
     return x.contiguous(), tx.contiguous()
+
+
+def _fwd_ws_bytes(dtype, mode, B, H, Lk, Dqk, Dv) -> int:
+    """Forward workspace: transposed V copies of the bf16/fp16 kernels for some head dims; none for fp32."""
+    return 0 if dtype == torch.float32 else nat.fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv)
 
 
 def _check_device(*ts):
@@ -151,7 +159,7 @@ def jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale, need_mu=True):
     lse = torch.empty((B, H, Lq), device=dev, dtype=torch.float32)
     mu = torch.empty_like(lse) if tq is not None else None
     lib = nat.lib()
-    ws_ptr, ws_size, ws = nat.workspace(nat.fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv), dev)
+    ws_ptr, ws_size, ws = nat.workspace(_fwd_ws_bytes(q.dtype, mode, B, H, Lk, Dqk, Dv), dev)
     nat.check(
         lib.dmad_attn_jvp_fwd(
             code, mode, B, H, Lq, Lk, Dqk, Dv,
@@ -202,7 +210,7 @@ def jvp_attention_forward_magi(q, k, v, tq, tk, tv, sm_scale, magi_mask):
     lse = torch.empty((B, H, Lq), device=dev, dtype=torch.float32)
     mu = torch.empty_like(lse)
     lib = nat.lib()
-    ws_ptr, ws_size, ws = nat.workspace(nat.fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv), dev)
+    ws_ptr, ws_size, ws = nat.workspace(_fwd_ws_bytes(q.dtype, mode, B, H, Lk, Dqk, Dv), dev)
     nat.check(
         lib.dmad_attn_jvp_fwd_magi(
             code, mode, B, H, Lq, Lk, Dqk, Dv,
@@ -310,8 +318,9 @@ class _attention(torch.autograd.Function):
         # reference keeps (q, k, v, o, LSE: :500-502), so tangent activations and
         # `to` are not held until the backward
         full = _BACKWARD_MODE == "full" or (_BACKWARD_MODE == "auto" and tangent_grad)
-        if full and (is_grad or tangent_grad) and max(HEAD_DIM_QK, HEAD_DIM_V) > FULL_BWD_MAX_HEAD_DIM:
-            full = _full_backward_unavailable(HEAD_DIM_QK, HEAD_DIM_V)
+        if full and (is_grad or tangent_grad) and (max(HEAD_DIM_QK, HEAD_DIM_V) > FULL_BWD_MAX_HEAD_DIM
+                                                   or q.dtype == torch.float32):
+            full = _full_backward_unavailable(HEAD_DIM_QK, HEAD_DIM_V, q.dtype)
         # an output that does not reach the loss arrives in backward as None
         # (not zeros), so an unused `to` keeps the dO-only kernel
         ctx.set_materialize_grads(False)

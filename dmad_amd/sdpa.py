@@ -20,9 +20,11 @@ def attention(q, k, v, dropout_p=0.0, softmax_scale=None, q_scale=None, causal=F
 
     As the reference: q, k, v share one dtype, ``q_scale`` multiplies q first,
     ``softmax_scale=None`` means D^-1/2. The kernels are deterministic, so
-    ``deterministic=True`` needs nothing more. Attention dropout, the causal
-    mask and float32 inputs are not provided by these kernels and raise
-    ``NotImplementedError`` (the Wan models call it with neither).
+    ``deterministic=True`` needs nothing more. bfloat16, float16 and float32
+    inputs run on the gfx950 kernels (float32 on fp32 MFMAs, where the reference
+    takes PyTorch's memory-efficient SDPA). Attention dropout and the causal
+    mask are not provided by these kernels and raise ``NotImplementedError``
+    (the Wan models call it with neither).
     """
     assert q.dtype == k.dtype and k.dtype == v.dtype
     del deterministic
@@ -30,8 +32,9 @@ def attention(q, k, v, dropout_p=0.0, softmax_scale=None, q_scale=None, causal=F
         raise NotImplementedError("attention dropout is not implemented by the gfx950 kernels")
     if causal:
         raise NotImplementedError("the causal mask is not implemented by the dense gfx950 kernels")
-    if q.dtype not in (torch.bfloat16, torch.float16):
-        raise NotImplementedError(f"dtype {q.dtype} is not supported by the gfx950 kernels (bfloat16 or float16)")
+    if q.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise NotImplementedError(
+            f"dtype {q.dtype} is not supported by the gfx950 kernels (bfloat16, float16 or float32)")
     if q_scale is not None:
         q = q * q_scale
     out = plain_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), softmax_scale)

@@ -36,7 +36,14 @@ enum dmad_status {
   DMAD_ERR_HIP = 4          /* the HIP runtime reported an error at launch */
 };
 
-enum dmad_dtype { DMAD_BF16 = 0, DMAD_F16 = 1 };
+/* Operand types. bf16 and fp16: bf16/fp16 MFMAs with fp32 accumulation, every
+ * entry point. fp32 (what the reference's Triton forward also accepts, and what
+ * rcm/utils/attention.py:120-167 routes to PyTorch's SDPA): fp32 MFMAs, the
+ * forward in every mode, dense and block-sparse, and the dO-only backward; the
+ * full-derivative backward and the RMSNorm/RoPE prologue are DMAD_ERR_UNSUPPORTED.
+ * Operand rows must start 16-byte aligned: strides are multiples of 8 elements
+ * for bf16/fp16 and of 4 for fp32. fp32 needs no forward workspace. */
+enum dmad_dtype { DMAD_BF16 = 0, DMAD_F16 = 1, DMAD_F32 = 2 };
 
 enum dmad_fwd_mode {
   DMAD_FWD_PLAIN = 0,           /* O and LSE only */
@@ -51,8 +58,9 @@ int dmad_abi_version(void);
 const char* dmad_last_error(void);
 
 /* Bytes of workspace dmad_attn_jvp_fwd / dmad_attn_fwd / dmad_attn_jvp_fwd_magi need
- * for these sizes: 0 for Dqk = Dv = 64 or 128 (V is read in place; the workspace
- * pointer may then be NULL), else room for transposed copies of V (and Vd). */
+ * for these sizes with bf16/fp16 operands: 0 for Dqk = Dv = 64 or 128 (V is read in
+ * place; the workspace pointer may then be NULL), else room for transposed copies of
+ * V (and Vd). fp32 operands need none. */
 int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv, size_t* bytes);
 
 /*
@@ -111,7 +119,8 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
  * 1 = full derivative (dto given), 2 = full derivative plus tangent gradients
  * (dto, dtq, dtk, dtv given). The per-row statistics always; transposed copies
  * of Q, dO, K (and the tangents) for the full derivative of head dims other
- * than 128 and for the dO-only gradients of head dims other than 64 and 128. */
+ * than 128 and for the dO-only gradients of head dims other than 64 and 128.
+ * The size holds for every dtype (fp32 uses only the statistics part). */
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes);
 
 /*

@@ -70,6 +70,9 @@ def _fwd(nat, **over):
         (dict(wsb=16, Dqk=32, Dv=32), 3, "workspace"),  # 32-wide heads read a transposed copy of V
         (dict(ws=0, Dqk=32, Dv=32), 3, "workspace"),
         (dict(Lq=1 << 22, qs=_strides(0, 0, 4096, 1)), 2, "2 GiB"),
+        # fp32 operands: rows 16-byte aligned means strides in multiples of 4 elements
+        (dict(dtype=2, ks=_strides(8192, 4096, 62, 1)), 1, "multiples of 4"),
+        (dict(dtype=2, Lq=1 << 21, qs=_strides(0, 0, 256, 1)), 2, "2 GiB"),
     ],
 )
 def test_fwd_rejects_bad_arguments(nat, over, code, needle):
@@ -232,6 +235,8 @@ _FULL = dict(tq=256, tk=256, tv=256, to=256, mu=256, dto=256)
         (dict(_FULL, dtq=256, dtk=256, dtv=0), 1, "all set or all null"),
         (dict(wsb=16), 3, "workspace"),
         (dict(ws=272), 1, "256-byte"),
+        (dict(_FULL, dtype=2), 2, "bf16 or fp16"),  # fp32: dO-only gradients
+        (dict(dtype=2, dos=_strides(8192, 4096, 66, 1)), 1, "multiples of 4"),
     ],
 )
 def test_bwd_rejects_bad_arguments(nat, over, code, needle):

@@ -81,7 +81,7 @@ def test_selective_checkpointing_saves_the_attention_forward(gpu, monkeypatch):
 
 def test_sdpa_twin_refuses_what_the_kernels_lack():
     """dmad_amd.sdpa.attention (rcm/utils/attention.py:120-167): dropout, causal and
-    float32 raise before anything reaches the GPU."""
+    float64 raise before anything reaches the GPU (float32 runs on the fp32 kernels)."""
     from dmad_amd.sdpa import attention
 
     q = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16)
@@ -89,8 +89,8 @@ def test_sdpa_twin_refuses_what_the_kernels_lack():
         attention(q, q, q, dropout_p=0.1)
     with pytest.raises(NotImplementedError, match="causal"):
         attention(q, q, q, causal=True)
-    with pytest.raises(NotImplementedError, match="float32"):
-        attention(q.float(), q.float(), q.float())
+    with pytest.raises(NotImplementedError, match="float64"):
+        attention(q.double(), q.double(), q.double())
 
 
 @pytest.mark.gpu
