@@ -24,6 +24,7 @@ import sys
 import time
 
 PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 dense bf16 flop/clk/CU
+PEAK_F32_TFLOPS = 157.3  # 256 CU x 2.4 GHz x 256 dense fp32 MFMA flop/clk/CU
 ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
@@ -258,20 +259,23 @@ def full_bwd_timing(q, k, v, tq, tk, tv, do, dto):
     return res
 
 
-def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384)):
+def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384), dtype=None):
     """The configuration of the reference's own perf_report harness
     (flash_attention_jvp_triton.py:662-725): B=4, H=32, fp16, L = 1024..16384,
     forward+JVP and its backward, with the harness's flop convention (12 and 10
-    units of B*H*L^2*D). The reference publishes no result for it."""
+    units of B*H*L^2*D). The reference publishes no result for it. With
+    dtype=float32 the same on the fp32 kernels, against the fp32 MFMA peak."""
     import torch
 
     from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
 
+    dtype = torch.float16 if dtype is None else dtype
+    peak = PEAK_F32_TFLOPS if dtype == torch.float32 else PEAK_BF16_TFLOPS
     B, H = 4, 32
     rows = []
     for L in lengths:
         g = torch.Generator(device=dev).manual_seed(0)
-        q, k, v, tq, tk, tv, do = (torch.randn((B, H, L, D), device=dev, dtype=torch.float16, generator=g)
+        q, k, v, tq, tk, tv, do = (torch.randn((B, H, L, D), device=dev, dtype=dtype, generator=g)
                                    for _ in range(7))
         s = D ** -0.5
         o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
@@ -290,11 +294,13 @@ def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384)):
             best_f = min(best_f, ev[0].elapsed_time(ev[1]))
             best_b = min(best_b, ev[1].elapsed_time(ev[2]))
         unit = B * H * L * L * D
-        rows.append({"L": L, "ms_fwd_jvp": round(best_f, 3),
-                     "fwd_jvp_TFLOPs": round(12.0 * unit / (best_f * 1e-3) / 1e12, 1),
-                     "ms_bwd": round(best_b, 3), "bwd_TFLOPs": round(10.0 * unit / (best_b * 1e-3) / 1e12, 1)})
+        tf_f, tf_b = 12.0 * unit / (best_f * 1e-3) / 1e12, 10.0 * unit / (best_b * 1e-3) / 1e12
+        rows.append({"L": L, "ms_fwd_jvp": round(best_f, 3), "fwd_jvp_TFLOPs": round(tf_f, 1),
+                     "fwd_pct_peak": round(100 * tf_f / peak, 1), "ms_bwd": round(best_b, 3),
+                     "bwd_TFLOPs": round(tf_b, 1), "bwd_pct_peak": round(100 * tf_b / peak, 1)})
         del q, k, v, tq, tk, tv, do, o, to, lse, mu
-    return {"B": 4, "H": 32, "D": D, "dtype": "fp16", "rows": rows}
+    return {"B": 4, "H": 32, "D": D, "dtype": "fp32" if dtype == torch.float32 else "fp16", "peak_TFLOPs": peak,
+            "rows": rows}
 
 
 def magi_timing(H, D, dev):
@@ -519,6 +525,8 @@ def main():
         out["reference_harness"] = [harness_timing(dev, D=d) for d in (64, 128)]
         # the head dims the reference also accepts (:471-472), on the generic kernels
         out["other_head_dims"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384)) for d in (16, 32, 256)]
+        out["fp32_harness"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384), dtype=torch.float32)
+                               for d in (64, 128)]
     if args.calibration_copy_mib:
         n = args.calibration_copy_mib * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)

@@ -4,7 +4,8 @@ CPU: the oracle reproduces every stored output from the stored inputs, and the
 stored outputs agree with an independent route (autodiff where the fixture was
 made with the closed form, and the closed form where it was made with autodiff).
 GPU: the HIP kernels reproduce the stored outputs to the parity bar
-(relative L2 <= 1e-2, |LSE - LSE_ref| <= 2e-3).
+(relative L2 <= 1e-2, |LSE - LSE_ref| <= 2e-3 on bf16 inputs; 1e-5 for the fp32
+plumbing fixture run on the fp32 kernels).
 """
 import os
 
@@ -76,6 +77,24 @@ def test_kernel_matches_forward_fixture(gpu, name):
     print("  rel-L2", {a: f"{b:.2e}" for a, b in e.items()})
     assert max(e.values()) <= 1e-2, e
     assert float((lse.cpu() - f["lse"]).abs().max()) <= 2e-3
+
+
+@pytest.mark.gpu
+def test_fp32_kernel_matches_plumbing_fixture(gpu):
+    """The plumbing configuration is fp32 (B=1, H=2, L=256, D=64): the fp32 kernels take
+    its inputs as stored and reproduce the float64 outputs to 1e-5."""
+    from dmad_amd.jvp_attention import jvp_attention_forward
+
+    print("case golden plumbing fp32", flush=True)
+    f = load("plumbing")
+    q, k, v, tq, tk, tv = (f[n].to(gpu) for n in ("q", "k", "v", "tq", "tk", "tv"))
+    assert q.dtype == torch.float32
+    o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, float(f["sm_scale"]))
+    torch.cuda.synchronize()
+    e = {"o": orc.rel_l2(o, f["o"]), "to": orc.rel_l2(to, f["to"]), "mu": orc.rel_l2(mu, f["mu"])}
+    print("  rel-L2", {a: f"{b:.2e}" for a, b in e.items()})
+    assert max(e.values()) <= 1e-5, e
+    assert float((lse.cpu() - f["lse"]).abs().max()) <= 1e-5
 
 
 @pytest.mark.gpu
