@@ -866,6 +866,13 @@ __global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
   }
 }
 
+// Columns of V one workgroup of attn_fwd_simple_kernel handles: a 256-wide V
+// in the JVP modes is split into two 128-column halves, each workgroup
+// recomputing the scores (3 of the 6 GEMMs run twice), because O~ and C~ for
+// all 256 columns next to Q, Qd and the score tiles spill registers (~650
+// bytes per lane at Dqk = 256, 100-360 at the other Dqk).
+constexpr int fwd_simple_dvc(int mode, int dv) { return (mode != kFwdPlain && dv == 256) ? 128 : dv; }
+
 // Single-stage-per-tile variant for head dims whose four-stage ring does not
 // fit in LDS (a 256-wide Q/K or V head in the full JVP mode): scores, softmax
 // and PV of each 64- or 32-key tile run back to back.
@@ -901,7 +908,9 @@ struct FwdSimpleCfg {
 // keys outside the current range at -inf, only the group's rows stored.
 template <typename T, int DQK, int DV, int MODE, bool MAGI = false>
 __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
-  using C = FwdSimpleCfg<DQK, DV, MODE>;
+  constexpr int DVC = fwd_simple_dvc(MODE, DV);  // V columns of this workgroup
+  constexpr int NCH = DV / DVC;                  // workgroups per query tile
+  using C = FwdSimpleCfg<DQK, DVC, MODE>;
   constexpr int BN = C::BN, NB = C::NB, KS = C::KS, DB = C::DB, CK = C::CK, CV = C::CV;
   __shared__ __attribute__((aligned(1024))) char smem[2 * C::STAGE];
 
@@ -909,19 +918,21 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 31, half = lane >> 5;
 
-  int bh, qt, ntiles;
+  int bh, qt, ntiles, chunk;
   int q_lo = 0, q_hi = p.Lq;         // rows this workgroup stores
   MagiCursor cm{0, 0, 0, 0, 0};      // MAGI: tile in use
   if constexpr (MAGI) {
-    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H);
-    bh = work / p.T;
-    const MagiTask t = magi_task(p, work - bh * p.T, C::BM);
+    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H * NCH);
+    chunk = work % NCH;
+    const int w2 = work / NCH;
+    bh = w2 / p.T;
+    const MagiTask t = magi_task(p, w2 - bh * p.T, C::BM);
     qt = t.row0 / C::BM;
     q_lo = t.q_lo;
     q_hi = t.q_hi;
     ntiles = magi_ntiles(p, t, BN);
     if (ntiles == 0) {  // uniform over the workgroup: nothing requested yet
-      magi_store_empty<T, DV, C::JVP>(p, bh, t, C::BM);
+      if (chunk == 0) magi_store_empty<T, DV, C::JVP>(p, bh, t, C::BM);  // every column of the rows
       return;
     }
     cm = MagiCursor{t.r_beg, t.r_end, 0, 0, 0};
@@ -929,8 +940,10 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   } else {
     const int nqt = (p.Lq + C::BM - 1) / C::BM;
     const int work = work_item(p.xcd_order);  // block order (common.h)
-    bh = work / nqt;
-    qt = work - bh * nqt;
+    chunk = work % NCH;
+    const int w2 = work / NCH;
+    bh = w2 / nqt;
+    qt = w2 - bh * nqt;
     ntiles = (p.Lk + BN - 1) / BN;
   }
   MagiCursor ci = cm;  // MAGI: tile requested next
@@ -940,15 +953,19 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
   const char* kbase = (const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2;
   const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + DQK) * 2);
   const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + DQK) * 2);
+  // V^T copy [B*H][DV padded to 32][LKP]; this workgroup reads rows
+  // [chunk * DVC, (chunk + 1) * DVC) of its head
+  const int64_t vt_head = (int64_t)(DV < 32 ? 32 : DV) * p.LKP * 2;
   const uint32_t vt_bytes = (uint32_t)((int64_t)C::DVP * p.LKP * 2);
+  const int64_t vt_off = (int64_t)bh * vt_head + (int64_t)chunk * DVC * p.LKP * 2;
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, q_bytes);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, k_bytes);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.vt + (int64_t)bh * vt_bytes, vt_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.vt + vt_off, vt_bytes);
   __amdgpu_buffer_rsrc_t rtq = rq, rtk = rk, rtv = rv;
   if constexpr (C::JVP) rtq = make_rsrc((const char*)p.tq + (b * p.q_sb + h * p.q_sh) * 2, q_bytes);
   if constexpr (C::KVT) {
     rtk = make_rsrc((const char*)p.tk + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
-    rtv = make_rsrc((const char*)p.tvt + (int64_t)bh * vt_bytes, vt_bytes);
+    rtv = make_rsrc((const char*)p.tvt + vt_off, vt_bytes);
   }
 
   // ---- Q (and Qd) slices in registers: B operand of S^T = K Q^T
@@ -1167,14 +1184,14 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int dc = d * 32 + 8 * j + 4 * half;
-      if (DV >= 32 || dc < DV) {
+      if (DVC >= 32 || dc < DVC) {
         float ov[4], tv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           ov[r] = oacc[d][4 * j + r] * inv_l;
           if constexpr (C::JVP) tv[r] = cacc[d][4 * j + r] * inv_l - mu * ov[r];
         }
-        const uint32_t off = orow + dc * 2;
+        const uint32_t off = orow + (chunk * DVC + dc) * 2;
         u32x2_t w = {Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])};
         buf_store8(ro, w, off);
         if constexpr (C::JVP) {
@@ -1184,7 +1201,7 @@ __global__ __launch_bounds__(256) void attn_fwd_simple_kernel(FwdParams p) {
       }
     }
   }
-  if (half == 0 && qrow < p.Lq && keep) {
+  if (half == 0 && qrow < p.Lq && keep && chunk == 0) {
     const int64_t si = (int64_t)bh * p.Lq + qrow;
     p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
     if constexpr (C::JVP) p.mu[si] = mu;

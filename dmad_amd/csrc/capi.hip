@@ -421,8 +421,12 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
     p.T = (int)mg->T;
     units = mg->T;
   }
-  // fp32: wide V runs several workgroups per query tile, one per column chunk (attn_f32.h)
-  const int64_t chunks = f32 ? dmad::f32_fwd_chunks((int)Dqk, (int)Dv) : 1;
+  // wide V runs several workgroups per query tile, one per column chunk (fp32:
+  // attn_f32.h; bf16/fp16: fwd_generic_chunks in launch.h)
+  const int64_t chunks = f32 ? dmad::f32_fwd_chunks((int)Dqk, (int)Dv)
+                         : dmad::fwd32_supported((int)Dqk, (int)Dv)
+                             ? 1
+                             : dmad::fwd_generic_chunks(mode, (int)Dqk, (int)Dv, mg != nullptr);
   if (units * BH * chunks >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
   int64_t grid = units * BH * chunks;
   p.xcd_order = units < dmad::kHeadMajorMinTiles;  // block order (common.h)

@@ -43,6 +43,18 @@ template <> FwdLaunchFn fwd32_magi_select<_Float16>(int, int);
 // Query rows per task of the block-sparse kernels.
 constexpr int kMagiBlockM = 128;
 
+// Generic bf16/fp16 forward kernels (the head-dim pairs attn_fwd32_kernel does
+// not take): JVP modes with a 256-wide V run attn_fwd_simple_kernel on
+// 128-column halves of V, two workgroups per 128-query tile, where the other
+// kernels' registers would spill (Dqk = 16, 128, 256, and every block-sparse
+// launch, which always runs attn_fwd_simple_kernel).
+constexpr bool fwd_generic_uses_halves(int mode, int dqk, int dv, bool magi) {
+  return mode != kFwdPlain && dv == 256 && (magi || dqk == 16 || dqk >= 128);
+}
+constexpr int fwd_generic_chunks(int mode, int dqk, int dv, bool magi) {
+  return fwd_generic_uses_halves(mode, dqk, dv, magi) ? 2 : 1;
+}
+
 typedef hipError_t (*BwdLaunchFn)(const BwdParams&, int grid, hipStream_t);
 
 // Launcher for attn_bwd_kernel<T, D, MODE>, or nullptr if unsupported.
