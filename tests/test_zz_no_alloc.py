@@ -3,7 +3,7 @@ static device scratch, called through the C ABI, against dmad_attn_jvp_bwd
 with a caller workspace on the same inputs. Same kernels, same statistics:
 the gradients must be bitwise equal. Two calls in a row, the second smaller
 than the first (the scratch keeps the first call's contents), then the first
-shape again."""
+shape again, and an fp32 call (its statistics in the same scratch)."""
 import ctypes
 
 import pytest
@@ -12,9 +12,9 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(dev, B, H, L, D, seed):
+def _inputs(dev, B, H, L, D, seed, dtype):
     g = torch.Generator().manual_seed(seed)
-    r = lambda sd: (torch.randn((B, L, H, D), generator=g) * sd).to(torch.bfloat16).to(dev).transpose(1, 2)  # noqa: E731
+    r = lambda sd: (torch.randn((B, L, H, D), generator=g) * sd).to(dtype).to(dev).transpose(1, 2)  # noqa: E731
     return {n: r(sd) for n, sd in (("q", 1.0), ("k", 1.0), ("v", 1.0), ("tq", 0.1), ("tk", 0.1), ("tv", 0.1),
                                    ("do", 1.0), ("dto", 0.1))}
 
@@ -50,17 +50,18 @@ def _backward(x, full, noalloc):
 
 
 CALLS = [
-    # (B, H, L, D, full derivative with tangent gradients)
-    (2, 3, 700, 128, True),
-    (1, 2, 300, 64, False),
-    (2, 3, 700, 128, True),
+    # (B, H, L, D, full derivative with tangent gradients, dtype)
+    (2, 3, 700, 128, True, torch.bfloat16),
+    (1, 2, 300, 64, False, torch.bfloat16),
+    (2, 3, 700, 128, True, torch.bfloat16),
+    (1, 2, 257, 32, False, torch.float32),
 ]
 
 
 def test_noalloc_backward_equals_workspace_backward(gpu):
-    for i, (B, H, L, D, full) in enumerate(CALLS):
-        print(f"case noalloc call {i}: B={B} H={H} L={L} D={D} full={full}", flush=True)
-        x = _inputs(gpu, B, H, L, D, seed=i)
+    for i, (B, H, L, D, full, dtype) in enumerate(CALLS):
+        print(f"case noalloc call {i}: B={B} H={H} L={L} D={D} full={full} {dtype}", flush=True)
+        x = _inputs(gpu, B, H, L, D, seed=i, dtype=dtype)
         ref = _backward(x, full, noalloc=False)
         got = _backward(x, full, noalloc=True)
         assert len(got) == (6 if full else 3)
