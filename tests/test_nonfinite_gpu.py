@@ -13,6 +13,7 @@ poisoned element in sample 1, head 0:
     scores drop the key), dQ, dK, dV are non-finite at least there, and where
     both are finite they agree to the usual rel-L2 <= 1e-2;
   * a poisoned tangent leaves O, LSE and the dO-only gradients bitwise unchanged.
+bf16 on the 128- and 64-wide kernels, fp32 on the fp32 kernels.
 """
 import math
 
@@ -27,9 +28,9 @@ B, H, L = 3, 2, 300
 ROW_Q, ROW_K, COL = 37, 123, 5
 
 
-def _inputs(D, seed):
+def _inputs(D, seed, dtype):
     g = torch.Generator().manual_seed(seed)
-    r = lambda sd: (torch.randn((B, H, L, D), generator=g, dtype=torch.float64) * sd).to(torch.bfloat16)  # noqa: E731
+    r = lambda sd: (torch.randn((B, H, L, D), generator=g, dtype=torch.float64) * sd).to(dtype)  # noqa: E731
     return {"q": r(1.0), "k": r(1.0), "v": r(1.0), "tq": r(0.1), "tk": r(0.1), "tv": r(0.1), "do": r(1.0)}
 
 
@@ -61,12 +62,13 @@ def _poison(x, where, val):
     return y
 
 
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.bfloat16), (128, torch.float32),
+                                     (32, torch.float32)])
 @pytest.mark.parametrize("where", ["q", "k", "v", "tq"])
 @pytest.mark.parametrize("val", [math.nan, math.inf])
-def test_nonfinite_input_stays_in_its_slice(gpu, D, where, val):
-    print(f"case nonfinite D={D} {where}={val}", flush=True)
-    x = _inputs(D, seed=D)
+def test_nonfinite_input_stays_in_its_slice(gpu, D, dtype, where, val):
+    print(f"case nonfinite D={D} {dtype} {where}={val}", flush=True)
+    x = _inputs(D, seed=D, dtype=dtype)
     clean = _run(x, gpu)
     y = _poison(x, where, val)
     got = _run(y, gpu)
