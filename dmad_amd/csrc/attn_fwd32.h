@@ -571,444 +571,4 @@ __global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void attn_fwd32_kernel(FwdPa
   }
 }
 
-// ---------------------------------------------------------------- persistent variant for short key sequences
-// With few key tiles (the 512 keys of Wan's text cross-attention: 16 steps of
-// 32 keys) the fixed work of a query tile -- reading its Q (and Qd) rows,
-// writing its O (and Od) rows -- is as long as the key loop, and with one
-// workgroup per CU it ran serialised with the MFMAs: at H=40, Lq=32760 the
-// K, V tangent-free forward took 0.45 ms of its 1.0 ms whatever the key count.
-// Here a workgroup loops over (batch*head, query tile) items (item = blockIdx.x
-// + n gridDim.x, head-major) and the key-tile ring runs on across items: the
-// last three steps of an item request the first three tiles of the next, the
-// next item's Q (and Qd) rows are fetched into a wave-private LDS region while
-// the current item runs, and the finished item's O (and Od) leave through that
-// region as whole rows (RowStage) while the next item starts. Modes whose ring
-// holds K, V only (kFwdJvpQOnly; kFwdPlain compiles too); the key-tile count
-// is a multiple of 4, so every item's tiles start at ring stage 0.
-//
-// vmcnt accounting: loads (ring tiles, staged Q rows) return in order, stores
-// may complete in any order relative to them, so a wait for a ring tile counts
-// only the loads issued after it. The first tile of an item may wait behind
-// [its tiles 1, 2] + [the QREQ requests for the item after next]; its steps 0
-// and 1 leave those requests in flight, and from step 2 on the ring counts as
-// in attn_fwd32_kernel. A wait that follows the finished item's stores also
-// waits for any of them still in flight. Every request and store is issued
-// unconditionally (rows past the end and items past the last fall outside
-// their buffer ranges), so the counts are exact.
-//
-// Plain attention keeps attn_fwd32_kernel: it fits two workgroups per CU,
-// which overlaps one tile's loads and stores with the other's key loop.
-template <int MODE, int DH>
-struct Fwd32PCfg {
-  using B = Fwd32Cfg<MODE, DH>;
-  static_assert(!B::KVT, "the persistent forward streams K and V only");
-  static constexpr int NT = B::JVP ? 2 : 1;                 // Q [, Qd] in / O [, Od] out
-  static constexpr int WST = NT * RowStage<DH>::BYTES;      // wave-private LDS bytes
-  static constexpr int QPT = RowStage<DH>::BYTES / 1024;    // 1 KiB requests per staged tensor
-  static constexpr int QREQ = NT * QPT;                     // staging requests per wave per item
-  static_assert(B::NSTAGE * B::STAGE + B::NW * WST <= 160 * 1024, "ring and staging exceed the LDS");
-  static_assert(2 * B::LOADS + QREQ < 64, "vmcnt is a 6-bit field");
-};
-
-// Shapes the persistent kernel is built for: the K, V tangent-free forward of
-// 128-wide heads. (64-wide heads fit two workgroups per CU with the
-// per-tile kernel, which overlaps the same way and measured 2-5% faster.)
-constexpr bool fwd32p_supported(int mode, int d) { return mode == kFwdJvpQOnly && d == 128; }
-
-template <typename T, int MODE, int DH>
-__global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void attn_fwd32_persist_kernel(FwdParams p) {
-  using C = Fwd32Cfg<MODE, DH>;
-  using PC = Fwd32PCfg<MODE, DH>;
-  using RS = RowStage<DH>;
-  constexpr int D = C::D, BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
-  constexpr int NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
-  constexpr float kSlack = RescaleSlack<T>::value;
-  __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char wst[C::NW][PC::WST];
-
-  const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = lane & 31, half = lane >> 5;
-  lds_char_t* const my = (lds_char_t*)wst[wave];
-
-  const int nqt = (p.Lq + C::BM - 1) / C::BM;
-  const int nitems = p.B * p.H * nqt;
-  const int ntiles = (p.Lk + BN - 1) / BN;  // a multiple of 4 (checked by the launcher)
-  const int stride = gridDim.x;
-  int item = blockIdx.x;  // < nitems (the launcher's grid is at most nitems)
-
-  const uint32_t q_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.q_sl + D) * 2);
-  const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
-  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
-  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + D) * 2);
-  struct Res2 {
-    __amdgpu_buffer_rsrc_t a, b;
-  };
-  // K, V of an item's head; an item past the end gets empty ranges (reads zeros)
-  auto kv_res = [&](int it) -> Res2 {
-    if (it >= nitems) return Res2{make_rsrc(p.k, 0), make_rsrc(p.v, 0)};
-    const int bh = it / nqt, b = bh / p.H, h = bh - b * p.H;
-    return Res2{make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes),
-                make_rsrc((const char*)p.v + (b * p.v_sb + h * p.v_sh) * 2, v_bytes)};
-  };
-
-  // ---- per-lane request offsets: K, V ring tiles and this wave's 32 staged Q rows
-  constexpr int RPW = C::RPW;
-  uint32_t roff_k[RPW], roff_v[RPW];
-#pragma unroll
-  for (int j = 0; j < RPW; ++j) {
-    const int pch = (wave + j * C::NW) * 64 + lane;
-    const int row = pch / CR, phys = pch % CR;
-    const int logical = phys ^ trswz<CR>(row & 15);
-    roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
-    roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
-  }
-  const uint32_t k_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
-  const uint32_t v_step = (uint32_t)((int64_t)BN * p.v_sl * 2);
-  uint32_t roff_q[PC::QPT];
-#pragma unroll
-  for (int j = 0; j < PC::QPT; ++j) {
-    const int pch = j * 64 + lane;
-    const int row = pch / CR, phys = pch % CR;
-    roff_q[j] = (uint32_t)((int64_t)row * p.q_sl * 2) + ((phys ^ trswz<CR>(row & 15)) << 4);
-  }
-
-  auto stage = [&](auto kk) -> lds_char_t* {
-    constexpr int k = decltype(kk)::value & 3;
-    if constexpr (k == 0) return (lds_char_t*)stg0;
-    else if constexpr (k == 1) return (lds_char_t*)stg1;
-    else if constexpr (k == 2) return (lds_char_t*)stg2;
-    else return (lds_char_t*)stg3;
-  };
-  Res2 kv_cur = kv_res(item), kv_next = kv_res(item + stride);
-  // request li (0 <= li < LOADS) of key tile kt of the current item into stage
-  // st; kt >= ntiles names tile kt - ntiles of the next item
-  auto issue_load = [&](lds_char_t* st, int kt, int li) {
-    const bool nxt = kt >= ntiles;
-    const __amdgpu_buffer_rsrc_t rk = nxt ? kv_next.a : kv_cur.a, rv = nxt ? kv_next.b : kv_cur.b;
-    const uint32_t t = (uint32_t)(nxt ? kt - ntiles : kt);
-    const int jj = li / C::NTILE, i = wave + jj * C::NW;
-    if (li % C::NTILE == 0) buf_load16_lds(rk, st + C::OFF_K + i * 1024, roff_k[jj], t * k_step);
-    else buf_load16_lds(rv, st + C::OFF_V + i * 1024, roff_v[jj], t * v_step);
-  };
-  // this wave's 32 Q (and Qd) rows of item `it` into its LDS region
-  auto issue_q = [&](int it) {
-    __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q, 0), rtq = rq;
-    uint32_t base = 0;
-    if (it < nitems) {
-      const int bh = it / nqt, qt = it - bh * nqt, b = bh / p.H, h = bh - b * p.H;
-      const int64_t qhead = b * p.q_sb + h * p.q_sh;
-      rq = make_rsrc((const char*)p.q + qhead * 2, q_bytes);
-      if constexpr (C::JVP) rtq = make_rsrc((const char*)p.tq + qhead * 2, q_bytes);
-      base = (uint32_t)((int64_t)(qt * C::BM + wave * 32) * p.q_sl * 2);
-    }
-#pragma unroll
-    for (int j = 0; j < PC::QPT; ++j) buf_load16_lds(rq, my + j * 1024, roff_q[j], base);
-    if constexpr (C::JVP) {
-#pragma unroll
-      for (int j = 0; j < PC::QPT; ++j) buf_load16_lds(rtq, my + RS::BYTES + j * 1024, roff_q[j], base);
-    }
-  };
-
-  // ---- LDS read offsets: K rows (row perm32(col), chunk 2s + half) and V^T (lds_read_tr16)
-  int sx[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const int r = perm32(col);
-    sx[s] = r * ROWB + (((2 * s + half) ^ trswz<CR>(r & 15)) << 4);
-  }
-  int tx[DB][2];
-  {
-    const int g = lane >> 4, r = (lane & 15) >> 2, c = lane & 3;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int row = 8 * (g >> 1) + 4 * hh + r;
-        const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-        tx[db][hh] = row * ROWB + ((chunk ^ trswz<CR>(row & 15)) << 4) + 8 * (c & 1);
-      }
-    }
-  }
-  auto pin_offsets = [&]() {
-#pragma unroll
-    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(sx[s]));
-#pragma unroll
-    for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(tx[db][0]), "+v"(tx[db][1]));
-  };
-  auto load_op = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int o) -> i32x4_t {
-    if (o < NOPA) return *(lds_i32x4_t*)(s_next + C::OFF_K + sx[o]);
-    const int j = o - NOPA, t = j / DB, db = j % DB;
-    const lds_char_t* base = s_cur + C::OFF_V + t * 16 * ROWB;
-    const u32x2_t lo = lds_read_tr16(base + tx[db][0]);
-    const u32x2_t hi = lds_read_tr16(base + tx[db][1]);
-    return i32x4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
-  };
-
-  // Q (and Qd) of the current item: B operands of S^T = K Q^T (Sd^T = K Qd^T),
-  // read from this wave's LDS region (row col, chunk 2s + half)
-  i32x4_t qreg[KS], tqreg[KS];
-  auto q_from_lds = [&]() {
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int off = col * ROWB + (((2 * s + half) ^ trswz<CR>(col & 15)) << 4);
-      qreg[s] = *(lds_i32x4_t*)(my + off);
-      if constexpr (C::JVP) tqreg[s] = *(lds_i32x4_t*)(my + RS::BYTES + off);
-    }
-    if constexpr (DH == 128) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        asm volatile("" : "+a"(qreg[s]));
-        if constexpr (C::JVP) asm volatile("" : "+a"(tqreg[s]));
-      }
-    }
-  };
-
-  f32x16_t oacc[DB], cacc[DB];
-  const f32x16_t zero16 = {};
-  auto mfma_op = [&](int o, i32x4_t a, f32x16_t& sn, f32x16_t& tn, const i32x4_t (&pk)[2], const i32x4_t (&hk)[2]) {
-    if (o < NOPA) {
-      sn = mfma32(a, qreg[o], o == 0 ? zero16 : sn, T());
-      if constexpr (C::JVP) tn = mfma32(a, tqreg[o], o == 0 ? zero16 : tn, T());
-    } else {
-      const int j = o - NOPA, t = j / DB, db = j % DB;
-      oacc[db] = mfma32(a, pk[t], oacc[db], T());
-      if constexpr (C::JVP) cacc[db] = mfma32(a, hk[t], cacc[db], T());
-    }
-  };
-
-  // online softmax of one tile in NMICRO micro-steps (as attn_fwd32_kernel)
-  constexpr int NMICRO = 18;
-  float m_i, l_i, r_i;
-  struct Soft {
-    float mx, alpha, neg_m, ls, rs, pv;
-    float hv;
-    bool moved;
-  };
-  auto soft_micro = [&](int u, Soft& sm, const f32x16_t& sc, const f32x16_t& tc, i32x4_t (&pk)[2],
-                        i32x4_t (&hk)[2]) {
-    if (u == 0) {
-      float a = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      float b2 = fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]));
-      float c2 = fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11]));
-      float d2 = fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]));
-      sm.mx = fmaxf(fmaxf(a, b2), fmaxf(c2, d2));
-      sm.ls = 0.f;
-      sm.rs = 0.f;
-    } else if (u == 1) {
-      sm.mx = fmaxf(sm.mx, other_half(sm.mx)) * p.scale_log2;
-      sm.moved = __builtin_amdgcn_ballot_w64(sm.mx > m_i + kSlack) != 0;
-      const float m_new = sm.moved ? fmaxf(m_i, sm.mx) : m_i;
-      sm.alpha = fast_exp2(m_i - m_new);
-      m_i = m_new;
-      sm.neg_m = -m_new;
-    } else {
-      const int v = u - 2;
-      const float pe = fast_exp2(fmaf(sc[v], p.scale_log2, sm.neg_m));
-      sm.ls += pe;
-      float he = 0.f;
-      if constexpr (C::JVP) {
-        he = pe * (tc[v] * p.scale);
-        sm.rs += he;
-      }
-      if (v & 1) {
-        pk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(sm.pv, pe);
-        if constexpr (C::JVP) hk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(sm.hv, he);
-      } else {
-        sm.pv = pe;
-        sm.hv = he;
-      }
-    }
-  };
-  auto rescale = [&](float alpha) {
-#pragma unroll
-    for (int d = 0; d < DB; ++d) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        oacc[d][v] *= alpha;
-        if constexpr (C::JVP) cacc[d][v] *= alpha;
-      }
-    }
-  };
-
-  // ring barrier of step i of an item (see the vmcnt accounting above)
-  auto step_sync = [&](int i) {
-    if (i >= 2) ring_sync<C::LOADS>();
-    else ring_sync<C::LOADS + PC::QREQ>();
-  };
-  // step i (i + 1 < ntiles, i % 4 == kk): phase A on tile i+1's K with the
-  // softmax of tile i, phase B on tile i's V; requests tile i+3
-  auto step = [&](auto kk, int i, const f32x16_t& sc, const f32x16_t& tc, f32x16_t& sn, f32x16_t& tn) {
-    constexpr int k = decltype(kk)::value;
-    step_sync(i);  // tile i+1 has landed (tile i+2 may be in flight)
-    pin_offsets();
-    const lds_char_t* s_next = stage(IC<k + 1>{});
-    const lds_char_t* s_cur = stage(IC<k>{});
-    lds_char_t* s_req = stage(IC<k + 3>{});
-    i32x4_t opr[PF];
-#pragma unroll
-    for (int o = 0; o < PF; ++o) opr[o] = load_op(s_next, s_cur, o);
-    Soft sm;
-    i32x4_t pk[2], hk[2];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int o = 0; o < NOPA; ++o) {
-      mfma_op(o, opr[o % PF], sn, tn, pk, hk);
-      if (o + PF < NOP) opr[o % PF] = load_op(s_next, s_cur, o + PF);
-#pragma unroll
-      for (int u = o * NMICRO / NOPA; u < (o + 1) * NMICRO / NOPA; ++u) soft_micro(u, sm, sc, tc, pk, hk);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    l_i = l_i * sm.alpha + sm.ls;
-    if constexpr (C::JVP) r_i = r_i * sm.alpha + sm.rs;
-    asm volatile("" : "+v"(pk[0]), "+v"(pk[1]), "+v"(l_i));
-    if constexpr (C::JVP) asm volatile("" : "+v"(hk[0]), "+v"(hk[1]), "+v"(r_i));
-    if (sm.moved) rescale(sm.alpha);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int o = NOPA; o < NOP; ++o) {
-      mfma_op(o, opr[o % PF], sn, tn, pk, hk);
-      if (o + PF < NOP) opr[o % PF] = load_op(s_next, s_cur, o + PF);
-#pragma unroll
-      for (int li = 0; li < C::LOADS; ++li) {
-        if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, i + 3, li);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  // last tile of an item (i = ntiles - 1, stage 3; may hold keys >= Lk):
-  // masked softmax, rescale, PV; requests tile 2 of the next item into stage 2
-  // once every wave has left step i - 1 (which read stage 2)
-  auto last_step = [&](int i, f32x16_t& sc, const f32x16_t& tc) {
-    ring_sync<2 * C::LOADS>();  // the next item's tiles 0 and 1 may be in flight
-    const lds_char_t* s_cur = stage(IC<3>{});
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      if (i * BN + 16 * (v >> 3) + 8 * half + (v & 7) >= p.Lk) sc[v] = -__builtin_inff();
-    }
-    Soft sm;
-    i32x4_t pk[2], hk[2];
-#pragma unroll
-    for (int u = 0; u < NMICRO; ++u) soft_micro(u, sm, sc, tc, pk, hk);
-    l_i = l_i * sm.alpha + sm.ls;
-    if constexpr (C::JVP) r_i = r_i * sm.alpha + sm.rs;
-    rescale(sm.alpha);
-    f32x16_t un_s, un_t;
-#pragma unroll
-    for (int o = NOPA; o < NOP; ++o) {
-      mfma_op(o, load_op(s_cur, s_cur, o), un_s, un_t, pk, hk);
-#pragma unroll
-      for (int li = 0; li < C::LOADS; ++li) {
-        if (NOPA + li * NOPB / C::LOADS == o) issue_load(stage(IC<2>{}), i + 3, li);
-      }
-    }
-  };
-
-  // ---- prologue: the first item's Q through the staging region, its tiles
-  // 0..2, then the staging requests for the item after it
-  issue_q(item);
-#pragma unroll
-  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
-#pragma unroll
-  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
-#pragma unroll
-  for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
-  wait_vmem_n<3 * C::LOADS>();  // this wave's Q rows have landed in its region
-  q_from_lds();
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the region is read before it is refilled
-  issue_q(item + stride);
-
-  for (;;) {
-    const int bh = item / nqt, qt = item - bh * nqt, b = bh / p.H, h = bh - b * p.H;
-    // ---- scores of tile 0 (stage 0)
-    ring_sync<2 * C::LOADS + PC::QREQ>();
-    f32x16_t sa, ta, sb, tb;
-    {
-      const lds_char_t* s0 = stage(IC<0>{});
-      const i32x4_t none[2] = {};
-#pragma unroll
-      for (int o = 0; o < NOPA; ++o) mfma_op(o, load_op(s0, s0, o), sa, ta, none, none);
-    }
-    m_i = -__builtin_inff();
-    l_i = 0.f;
-    r_i = 0.f;
-#pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      oacc[d] = zero16;
-      cacc[d] = zero16;
-    }
-    int i = 0;
-    for (; i + 4 < ntiles; i += 4) {
-      step(IC<0>{}, i, sa, ta, sb, tb);
-      step(IC<1>{}, i + 1, sb, tb, sa, ta);
-      step(IC<2>{}, i + 2, sa, ta, sb, tb);
-      step(IC<3>{}, i + 3, sb, tb, sa, ta);
-    }
-    step(IC<0>{}, i, sa, ta, sb, tb);
-    step(IC<1>{}, i + 1, sb, tb, sa, ta);
-    step(IC<2>{}, i + 2, sa, ta, sb, tb);
-    last_step(i + 3, sb, tb);
-
-    // ---- next item's Q from the region (landed by step 2), then this item's
-    // O (and Od) out through it as whole rows, LSE (and mu)
-    const int next = item + stride;
-    q_from_lds();
-    const float l = l_i + other_half(l_i);
-    const float inv_l = 1.0f / l;
-    float mu = 0.f;
-    if constexpr (C::JVP) mu = (r_i + other_half(r_i)) * inv_l;
-#pragma unroll
-    for (int d = 0; d < DB; ++d) {
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        float ov[4], tv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ov[e] = oacc[d][4 * jj + e] * inv_l;
-          if constexpr (C::JVP) tv[e] = cacc[d][4 * jj + e] * inv_l - mu * ov[e];
-        }
-        stage_put<D>(my, col, half, d, jj, u32x2_t{Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])});
-        if constexpr (C::JVP)
-          stage_put<D>(my + RS::BYTES, col, half, d, jj,
-                       u32x2_t{Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])});
-      }
-    }
-    const int64_t ohead = b * p.o_sb + h * p.o_sh;
-    const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + ohead * 2, o_bytes);
-    __amdgpu_buffer_rsrc_t rto = ro;
-    if constexpr (C::JVP) rto = make_rsrc((char*)p.to + ohead * 2, o_bytes);
-    const int row0 = qt * C::BM + wave * 32;
-    auto row_off = [&](int r) -> uint32_t {
-      return row0 + r < p.Lq ? (uint32_t)((int64_t)(row0 + r) * p.o_sl * 2) : o_bytes;
-    };
-#pragma unroll
-    for (int kk = 0; kk < RS::NST; ++kk) {
-      stage_store<D>(my, kk, lane, ro, row_off);
-      if constexpr (C::JVP) stage_store<D>(my + RS::BYTES, kk, lane, rto, row_off);
-    }
-    {
-      // per-row statistics from the lanes of the first half (the others fall outside the range)
-      const uint32_t st_bytes = (uint32_t)p.Lq * 4;
-      const uint32_t soff = (half == 0 && row0 + col < p.Lq) ? (uint32_t)(row0 + col) * 4 : st_bytes;
-      const __amdgpu_buffer_rsrc_t rl = make_rsrc(p.lse + (int64_t)bh * p.Lq, st_bytes);
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((m_i + __builtin_log2f(l)) * 0.6931471805599453f), rl,
-                                            (int)soff, 0, 0);
-      if constexpr (C::JVP) {
-        const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.mu + (int64_t)bh * p.Lq, st_bytes);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mu), rm, (int)soff, 0, 0);
-      }
-    }
-    if (next >= nitems) break;
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staged rows are read before the region is refilled
-    issue_q(next + stride);
-    kv_cur = kv_next;
-    kv_next = kv_res(next + stride);
-    item = next;
-  }
-  wait_vmem();  // no request stays in flight when the workgroup ends
-}
-
 }  // namespace dmad

@@ -188,37 +188,17 @@ dmad::FwdLaunchFn pick_fwd_magi(int dtype, int64_t dqk, int64_t dv, int mode) {
   return nullptr;
 }
 
-dmad::FwdLaunchFn pick_fwd32p(int dtype, int64_t d, int mode) {
-  if (dtype == DMAD_BF16) return dmad::fwd32p_select<__bf16>(mode, (int)d);
-  if (dtype == DMAD_F16) return dmad::fwd32p_select<_Float16>(mode, (int)d);
+dmad::FwdLaunchFn pick_fwd32x2(int dtype, int64_t d, int mode) {
+  if (dtype == DMAD_BF16) return dmad::fwd32x2_select<__bf16>(mode, (int)d);
+  if (dtype == DMAD_F16) return dmad::fwd32x2_select<_Float16>(mode, (int)d);
   return nullptr;
 }
 
 // Key-tile counts (32 keys each) up to which the K, V tangent-free forward of
-// 128-wide heads runs on the persistent kernel: measured at H=40, Lq=32760,
-// 1.6x faster at 128 keys, 1.17x at 512, 5% slower at 2048.
-constexpr int64_t kPersistMaxKeyTiles = 32;
-
-std::mutex g_dev_mu;
-int g_cu_count[64] = {};
-
-// Workgroups of the persistent forward resident on the current device at once:
-// one per CU for 128-wide heads, two for 64-wide heads.
-int resident_slots(int d, int* slots) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(DMAD_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
-  if (dev < 0 || dev >= 64) return fail(DMAD_ERR_UNSUPPORTED, "device ordinal %d out of range", dev);
-  std::lock_guard<std::mutex> lock(g_dev_mu);
-  if (g_cu_count[dev] == 0) {
-    int n = 0;
-    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess || n <= 0) return fail(DMAD_ERR_HIP, "CU count of device %d: %s", dev, hipGetErrorString(e));
-    g_cu_count[dev] = n;
-  }
-  *slots = g_cu_count[dev] * (d == 64 ? 2 : 1);
-  return DMAD_OK;
-}
+// 128-wide heads runs on attn_fwd32_x2_kernel: measured at H=40, Lq=32760,
+// 17-18% faster than the one-workgroup-per-CU kernels at 128-256 keys, 7-8% at
+// 512-1024, 3% at 2048; 1-2% slower at 4096-8192 keys.
+constexpr int64_t kX2MaxKeyTiles = 64;
 
 // Block-sparse tables of dmad_attn_jvp_fwd_magi (device pointers).
 struct MagiArgs {
@@ -431,19 +411,10 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
   int64_t grid = units * BH * chunks;
   p.xcd_order = units < dmad::kHeadMajorMinTiles;  // block order (common.h)
   // short key sequences, K and V tangents zero (the text cross-attention): the
-  // persistent kernel (one workgroup per slot, looping over the query tiles)
-  // overlaps each tile's Q reads and O writes with the key loop of the next
-  const int64_t ktiles = (Lk + 31) / 32;
-  if (!f32 && mg == nullptr && mode == DMAD_FWD_JVP_KV_TANGENT_ZERO && Dqk == Dv && dmad::fwd32p_supported(mode, (int)Dqk) &&
-      ktiles % 4 == 0 &&
-      ktiles <= kPersistMaxKeyTiles) {
-    int slots = 0;
-    if ((rc = resident_slots((int)Dqk, &slots))) return rc;
-    dmad::FwdLaunchFn fp = pick_fwd32p(dtype, Dqk, mode);
-    if (fp != nullptr && slots > 0) {
-      fn = fp;
-      grid = grid < slots ? grid : slots;
-    }
+  // two-workgroups-per-CU kernel
+  if (!f32 && mg == nullptr && dmad::fwd32x2_supported(mode, (int)Dqk, (int)Dv) && (Lk + 31) / 32 <= kX2MaxKeyTiles) {
+    fn = pick_fwd32x2(dtype, Dqk, mode);
+    if (fn == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no K, V tangent-free kernel for this dtype");
   }
   mark(0, false, s);
   e = fn(p, (int)grid, s);

@@ -29,15 +29,10 @@ static hipError_t fwd32_magi_launch(const FwdParams& p, int grid, hipStream_t s)
   return hipGetLastError();
 }
 
-template <typename T, int MODE, int D>
-static hipError_t fwd32p_launch(const FwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_fwd32_persist_kernel<T, MODE, D>), dim3(grid), dim3(256), 0, s, p);
+template <typename T>
+static hipError_t fwd32x2_launch(const FwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_fwd32_x2_kernel<T>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
-}
-
-template <int D>
-static FwdLaunchFn fwd32p_mode(int mode) {
-  return mode == kFwdJvpQOnly ? &fwd32p_launch<Elt, kFwdJvpQOnly, D> : nullptr;
 }
 
 template <int D>
@@ -65,8 +60,8 @@ FwdLaunchFn fwd32_magi_select<Elt>(int mode, int d) {
 }
 
 template <>
-FwdLaunchFn fwd32p_select<Elt>(int mode, int d) {
-  return d == 128 ? fwd32p_mode<128>(mode) : nullptr;
+FwdLaunchFn fwd32x2_select<Elt>(int mode, int d) {
+  return fwd32x2_supported(mode, d, d) ? &fwd32x2_launch<Elt> : nullptr;
 }
 
 template <>

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include "attn_fwd.h"
 #include "attn_fwd32.h"
+#include "attn_fwd32_x2.h"
 #include "attn_bwd.h"
 #include "attn_bwd_dq.h"
 #include "attn_bwd_full.h"
@@ -24,13 +25,12 @@ FwdLaunchFn fwd32_select(int mode, int d);
 template <> FwdLaunchFn fwd32_select<__bf16>(int, int);
 template <> FwdLaunchFn fwd32_select<_Float16>(int, int);
 
-// Persistent forward (attn_fwd32_persist_kernel; mode kFwdJvpQOnly, 128-wide
-// heads, key-tile count a multiple of 4): the grid is at most the number of
-// workgroups resident on the device.
+// Two-workgroups-per-CU forward (attn_fwd32_x2_kernel; mode kFwdJvpQOnly,
+// 128-wide heads): one workgroup per 128-query tile.
 template <typename T>
-FwdLaunchFn fwd32p_select(int mode, int d);
-template <> FwdLaunchFn fwd32p_select<__bf16>(int, int);
-template <> FwdLaunchFn fwd32p_select<_Float16>(int, int);
+FwdLaunchFn fwd32x2_select(int mode, int d);
+template <> FwdLaunchFn fwd32x2_select<__bf16>(int, int);
+template <> FwdLaunchFn fwd32x2_select<_Float16>(int, int);
 
 // Block-sparse (MagiMask) forward launchers, JVP modes only; the grid is
 // tasks * B * H workgroups of 256 threads, each task a 128-query tile.

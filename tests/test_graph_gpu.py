@@ -3,8 +3,8 @@
 Serving loops capture a whole denoising step and replay it; the library then
 has to put nothing but kernel launches on the stream (no memsets, no host
 synchronisation, no allocation outside torch's capture pool). One capture holds
-the self-attention forward+JVP, the 512-key text cross-attention forward (the
-persistent kernel), the dO-only backward, the full-derivative backward with
+the self-attention forward+JVP, the 512-key text cross-attention forward (two
+workgroups per CU), the dO-only backward, the full-derivative backward with
 tangent gradients and the allocation-free backward entry point. The graph is
 replayed three times with eager work in between that rewrites other memory,
 and every replay must equal the eager results bit for bit.
