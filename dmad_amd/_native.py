@@ -29,6 +29,34 @@ DMAD_FWD_PLAIN = 0
 DMAD_FWD_JVP = 1
 DMAD_FWD_JVP_KV_TANGENT_ZERO = 2
 
+
+
+class Plan(ctypes.Structure):
+    """``dmad_plan``: the kernels a call runs, their grids, block order, column chunks,
+    transposed copies and workspace (see dmad_attn_fwd_plan / dmad_attn_bwd_plan)."""
+
+    _fields_ = [
+        ("kernel", ctypes.c_char_p),
+        ("kernel2", ctypes.c_char_p),
+        ("kernel3", ctypes.c_char_p),
+        ("kernel4", ctypes.c_char_p),
+        ("grid", ctypes.c_int64),
+        ("grid2", ctypes.c_int64),
+        ("xcd_order", ctypes.c_int32),
+        ("xcd_order2", ctypes.c_int32),
+        ("chunks", ctypes.c_int32),
+        ("transposed_copies", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_int64),
+    ]
+
+    def as_dict(self) -> dict:
+        out = {}
+        for name, _ in self._fields_:
+            v = getattr(self, name)
+            out[name] = v.decode() if isinstance(v, bytes) else v
+        return out
+
+
 # Every function the header declares, with its ctypes signature.
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -55,6 +83,8 @@ SIGNATURES = {
     "dmad_set_kernel_events": (_INT, [ctypes.POINTER(ctypes.c_void_p), _INT]),
     "dmad_rmsnorm_rope_jvp": (_INT, [_INT, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _FP, _F, _P, _P, _I64, _P]),
     "dmad_attn_bwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _SZP]),
+    "dmad_attn_fwd_plan": (_INT, [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.POINTER(Plan)]),
+    "dmad_attn_bwd_plan": (_INT, [_INT, _INT, _INT, _I64, _I64, _I64, _I64, _I64, ctypes.POINTER(Plan)]),
     "dmad_attn_jvp_bwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64,
                                  _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
                                  _P, _P, _I64P, _P, _P, _P, _P, _I64P,
@@ -154,6 +184,24 @@ def bwd_workspace_bytes(mode: int, B: int, H: int, Lq: int, Lk: int, D: int) -> 
     n = ctypes.c_size_t(0)
     check(lib().dmad_attn_bwd_workspace_bytes(mode, B, H, Lq, Lk, D, ctypes.byref(n)))
     return int(n.value)
+
+
+def fwd_plan(dtype: int, mode: int, B: int, H: int, Lq: int, Lk: int, Dqk: int, Dv: int,
+             magi_tasks: int = -1) -> dict:
+    """The launch plan of a forward call (no GPU needed): kernel, grid, block order, column
+    chunks, transposed copies, workspace. ``magi_tasks`` >= 0 for the block-sparse forward."""
+    pl = Plan()
+    check(lib().dmad_attn_fwd_plan(dtype, mode, magi_tasks, B, H, Lq, Lk, Dqk, Dv, ctypes.byref(pl)))
+    return pl.as_dict()
+
+
+def bwd_plan(dtype: int, B: int, H: int, Lq: int, Lk: int, D: int, full: bool = False,
+             tangent_grads: bool = False) -> dict:
+    """The launch plan of a backward call (no GPU needed): the key and query passes (and the
+    tangent passes), their grids and block order, transposed copies, workspace."""
+    pl = Plan()
+    check(lib().dmad_attn_bwd_plan(dtype, int(full), int(tangent_grads), B, H, Lq, Lk, D, ctypes.byref(pl)))
+    return pl.as_dict()
 
 
 def workspace(nbytes: int, device: torch.device):

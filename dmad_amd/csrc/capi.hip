@@ -200,6 +200,58 @@ dmad::FwdLaunchFn pick_fwd32x2(int dtype, int64_t d, int mode) {
 // 512-1024, 3% at 2048; 1-2% slower at 4096-8192 keys.
 constexpr int64_t kX2MaxKeyTiles = 64;
 
+// ---------------------------------------------------------------- launch plans
+// The fixed per-shape table that stands in for the reference's Triton
+// autotuning (configs over BLOCK_M, BLOCK_N, stages and warps keyed on
+// SEQ_LEN_Q, SEQ_LEN_KV, HEAD_DIM_QK, HEAD_DIM_V:
+// train/wan/rcm/utils/flash_attention_jvp_triton.py:98-107). Its keys are the
+// dtype, the mode, the mask, Lq (query tiles per head), Lk (key tiles) and the
+// head dims; the entry points launch what it says, and dmad_attn_fwd_plan /
+// dmad_attn_bwd_plan report it. Inputs are validated by the callers.
+enum class FwdFamily { kRows, kRowsX2, kGeneric, kF32 };
+struct FwdPlan {
+  FwdFamily family;
+  const char* kernel;
+  int64_t grid, chunks;
+  int xcd_order, copies;
+  int64_t ws;
+};
+
+// magi_tasks < 0: dense; otherwise the block-sparse forward with that many tasks
+FwdPlan plan_fwd(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk,
+                 int64_t Dv) {
+  const bool magi = magi_tasks >= 0;
+  FwdPlan pl{};
+  if (dtype == DMAD_F32) {
+    // fp32 operands: fp32-MFMA kernels, V in column chunks for wide heads
+    pl.family = FwdFamily::kF32;
+    pl.kernel = "attn_f32_fwd_kernel";
+    pl.chunks = dmad::f32_fwd_chunks((int)Dqk, (int)Dv);
+  } else if (!magi && dmad::fwd32x2_supported(mode, (int)Dqk, (int)Dv) && (Lk + 31) / 32 <= kX2MaxKeyTiles) {
+    // short key sequences with Kd = Vd = 0 (the text cross-attention): two workgroups per CU
+    pl.family = FwdFamily::kRowsX2;
+    pl.kernel = "attn_fwd32_x2_kernel";
+    pl.chunks = 1;
+  } else if (dmad::fwd32_supported((int)Dqk, (int)Dv)) {
+    // 64- and 128-wide heads: 32-query waves reading K, V row-major
+    pl.family = FwdFamily::kRows;
+    pl.kernel = "attn_fwd32_kernel";
+    pl.chunks = 1;
+  } else {
+    // the other head dims: generic kernels on transposed copies of V (and Vd)
+    pl.family = FwdFamily::kGeneric;
+    pl.kernel = magi ? "attn_fwd_simple_kernel" : dmad::generic_fwd_name((int)Dqk, (int)Dv, mode);
+    pl.chunks = dmad::fwd_generic_chunks(mode, (int)Dqk, (int)Dv, magi);
+    pl.copies = mode == DMAD_FWD_JVP ? 2 : 1;
+  }
+  const int64_t units = magi ? magi_tasks : (Lq + 127) / 128;  // 128-query tiles or tasks
+  pl.grid = units * B * H * pl.chunks;
+  // block order (common.h): the block-sparse kernels always deal contiguous work items per XCD
+  pl.xcd_order = magi ? 1 : units < dmad::kHeadMajorMinTiles;
+  pl.ws = pl.family == FwdFamily::kF32 ? 0 : fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
+  return pl;
+}
+
 // Block-sparse tables of dmad_attn_jvp_fwd_magi (device pointers).
 struct MagiArgs {
   const int32_t *q_ranges, *k_ranges, *qk_map, *task_group, *task_qtile;
@@ -289,6 +341,45 @@ BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) 
   return w;
 }
 
+// Backward plan: the key-stationary pass (dK, dV), the query-stationary pass
+// (dQ [, dQd]), and with tangent gradients the dO-only passes run on (dOd, rho)
+// (the query one only where the full query pass does not give dQd).
+struct BwdPlan {
+  const char *kv, *dq, *kv_t, *dq_t;
+  int64_t grid_kv, grid_dq;
+  int xcd_kv, xcd_dq, copies;
+  int64_t ws;
+};
+
+BwdPlan plan_bwd(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) {
+  BwdPlan pl{};
+  const int64_t BH = B * H;
+  if (dtype == DMAD_F32) {
+    // fp32 operands (dO only): fp32-MFMA passes, head-major order
+    const int64_t bk = D > 128 ? 64 : 128, bm = D > 128 ? 64 : 128;
+    pl.kv = "attn_f32_bwd_kv_kernel";
+    pl.dq = "attn_f32_bwd_dq_kernel";
+    pl.grid_kv = (Lk + bk - 1) / bk * BH;
+    pl.grid_dq = (Lq + bm - 1) / bm * BH;
+    pl.ws = bwd_ws(0, B, H, Lq, Lk, D).total;
+    return pl;
+  }
+  const bool rows = full && dmad::full_reads_rows((int)D);
+  pl.kv = rows ? "attn_bwd_kv_full_kernel" : full ? "attn_bwd_kernel" : dmad::kv_dout_only_name((int)D);
+  pl.dq = rows ? "attn_bwd_dq_full_kernel" : full ? "attn_bwd_dq_kernel" : dmad::dq_dout_only_name((int)D);
+  pl.kv_t = tgrad ? dmad::kv_dout_only_name((int)D) : nullptr;
+  pl.dq_t = tgrad && !rows ? dmad::dq_dout_only_name((int)D) : nullptr;
+  const int64_t nkt = (Lk + 127) / 128, nqt = (Lq + 127) / 128;  // 128 keys / queries per workgroup
+  pl.grid_kv = nkt * BH;
+  pl.grid_dq = nqt * BH;
+  pl.xcd_kv = nkt < dmad::kHeadMajorMinTiles;  // block order (common.h)
+  pl.xcd_dq = nqt < dmad::kHeadMajorMinTiles;
+  const BwdWs w = bwd_ws(full ? (tgrad ? 2 : 1) : 0, B, H, Lq, Lk, D);
+  pl.copies = w.nq + w.nk;
+  pl.ws = w.total;
+  return pl;
+}
+
 // Shared body of the dense and block-sparse forwards (mg == nullptr: dense).
 int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t Dqk, int64_t Dv, const void* q,
              const void* k, const void* v, const void* tq, const void* tk, const void* tv, const int64_t q_strides[4],
@@ -327,24 +418,28 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
     if ((rc = check_operand("tv", tv, v_strides, Lk, Dv, esz))) return rc;
   }
   if (lse == nullptr) return fail(DMAD_ERR_INVALID, "lse: null pointer");
-  const int64_t need = f32 ? 0 : fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
+  // the launch plan (kernel, grid, block order, copies, workspace) for this shape
+  const FwdPlan plan = plan_fwd(dtype, mode, mg ? mg->T : -1, B, H, Lq, Lk, Dqk, Dv);
+  const int64_t need = plan.ws;
   if (need > 0 && (workspace == nullptr || (int64_t)workspace_bytes < need))
     return fail(DMAD_ERR_WORKSPACE, "workspace needs %lld bytes, got %lld", (long long)need, (long long)workspace_bytes);
   if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
   const int64_t dvp = Dv < 32 ? 32 : Dv, lkp = round_up(Lk, kLkAlign);
   if (dvp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "Lk too large");
 
-  dmad::FwdLaunchFn fn = f32 ? pick_fwd_f32(Dqk, Dv, mode, mg != nullptr)
-                             : mg ? pick_fwd_magi(dtype, Dqk, Dv, mode) : pick_fwd(dtype, Dqk, Dv, mode);
+  dmad::FwdLaunchFn fn = plan.family == FwdFamily::kF32      ? pick_fwd_f32(Dqk, Dv, mode, mg != nullptr)
+                         : plan.family == FwdFamily::kRowsX2 ? pick_fwd32x2(dtype, Dqk, mode)
+                         : mg                                ? pick_fwd_magi(dtype, Dqk, Dv, mode)
+                                                             : pick_fwd(dtype, Dqk, Dv, mode);
   if (fn == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no kernel for Dqk=%lld Dv=%lld", (long long)Dqk, (long long)Dv);
 
   hipStream_t s = (hipStream_t)stream;
   const int BH = (int)(B * H);
   char* ws = (char*)workspace;
   const int64_t vt_bytes = round_up(B * H * dvp * lkp * 2, 256);
-  // kernels for 128-wide heads transpose V on the LDS read; the others read a
-  // transposed, key-padded copy made here
-  const bool need_vt = !f32 && !dmad::fwd32_supported((int)Dqk, (int)Dv);
+  // kernels for 64- and 128-wide heads transpose V on the LDS read; the others
+  // read a transposed, key-padded copy made here
+  const bool need_vt = plan.copies > 0;
   hipError_t e = hipSuccess;
   dmad::TransposeParams tp{v, ws, v_strides[0], v_strides[1], v_strides[2], (int)H, (int)Lk, (int)Dv, (int)lkp, (int)dvp};
   if (need_vt) e = dmad::launch_transpose_pad(tp, BH, s);
@@ -389,7 +484,6 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
   p.LKP = (int)lkp;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
-  int64_t units = (Lq + 127) / 128;  // 128-query tiles (dense) or tasks (block-sparse)
   if (mg != nullptr) {
     p.q_ranges = mg->q_ranges;
     p.k_ranges = mg->k_ranges;
@@ -399,23 +493,10 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
     p.G = (int)mg->G;
     p.R = (int)mg->R;
     p.T = (int)mg->T;
-    units = mg->T;
   }
-  // wide V runs several workgroups per query tile, one per column chunk (fp32:
-  // attn_f32.h; bf16/fp16: fwd_generic_chunks in launch.h)
-  const int64_t chunks = f32 ? dmad::f32_fwd_chunks((int)Dqk, (int)Dv)
-                         : dmad::fwd32_supported((int)Dqk, (int)Dv)
-                             ? 1
-                             : dmad::fwd_generic_chunks(mode, (int)Dqk, (int)Dv, mg != nullptr);
-  if (units * BH * chunks >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
-  int64_t grid = units * BH * chunks;
-  p.xcd_order = units < dmad::kHeadMajorMinTiles;  // block order (common.h)
-  // short key sequences, K and V tangents zero (the text cross-attention): the
-  // two-workgroups-per-CU kernel
-  if (!f32 && mg == nullptr && dmad::fwd32x2_supported(mode, (int)Dqk, (int)Dv) && (Lk + 31) / 32 <= kX2MaxKeyTiles) {
-    fn = pick_fwd32x2(dtype, Dqk, mode);
-    if (fn == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no K, V tangent-free kernel for this dtype");
-  }
+  if (plan.grid >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  const int64_t grid = plan.grid;
+  p.xcd_order = plan.xcd_order;  // block order (common.h)
   mark(0, false, s);
   e = fn(p, (int)grid, s);
   mark(0, true, s);
@@ -698,15 +779,17 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   pq.scale = sm_scale;
   pq.scale_log2 = sm_scale * 1.4426950408889634f;
 
-  const int64_t nkt = (Lk + 127) / 128, nqt = (Lq + 127) / 128;
-  if (nkt * BH >= ((int64_t)1 << 31) || nqt * BH >= ((int64_t)1 << 31)) return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
-  p.xcd_order = nkt < dmad::kHeadMajorMinTiles;  // block order (common.h)
-  pq.xcd_order = nqt < dmad::kHeadMajorMinTiles;
+  // grids and block order from the launch plan (128 keys / queries per workgroup)
+  const BwdPlan plan = plan_bwd(dtype, full, tgrad, B, H, Lq, Lk, D);
+  if (plan.grid_kv >= ((int64_t)1 << 31) || plan.grid_dq >= ((int64_t)1 << 31))
+    return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
+  p.xcd_order = plan.xcd_kv;  // block order (common.h)
+  pq.xcd_order = plan.xcd_dq;
   mark(0, false, s);
-  if ((e = fn(p, (int)(nkt * BH), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  if ((e = fn(p, (int)plan.grid_kv, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   mark(0, true, s);
   mark(1, false, s);
-  if (nqt > 0 && (e = fq(pq, (int)(nqt * BH), s)) != hipSuccess)
+  if (plan.grid_dq > 0 && (e = fq(pq, (int)plan.grid_dq, s)) != hipSuccess)
     return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
   mark(1, true, s);
   if (tgrad) {
@@ -719,7 +802,7 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     pt.dk = dtk;
     pt.dv = dtv;
     mark(2, false, s);
-    if ((e = fn_a(pt, (int)(nkt * BH), s)) != hipSuccess)
+    if ((e = fn_a(pt, (int)plan.grid_kv, s)) != hipSuccess)
       return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
     mark(2, true, s);
     dmad::DqParams pqt = pq;
@@ -729,7 +812,7 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     pqt.dq = dtq;
     if (fq_a != nullptr) {
       mark(3, false, s);
-      if (nqt > 0 && (e = fq_a(pqt, (int)(nqt * BH), s)) != hipSuccess)
+      if (plan.grid_dq > 0 && (e = fq_a(pqt, (int)plan.grid_dq, s)) != hipSuccess)
         return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
       mark(3, true, s);
     }
@@ -802,6 +885,50 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
                            workspace_bytes, stream);
 }
 
+int dmad_attn_fwd_plan(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                       int64_t Dqk, int64_t Dv, dmad_plan* out) {
+  if (out == nullptr) return fail(DMAD_ERR_INVALID, "plan: null pointer");
+  if (dtype != DMAD_BF16 && dtype != DMAD_F16 && dtype != DMAD_F32)
+    return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+  if (mode < DMAD_FWD_PLAIN || mode > DMAD_FWD_JVP_KV_TANGENT_ZERO) return fail(DMAD_ERR_INVALID, "unknown mode %d", mode);
+  if (magi_tasks >= 0 && mode == DMAD_FWD_PLAIN) return fail(DMAD_ERR_INVALID, "the block-sparse forward has JVP modes only");
+  if (B < 0 || H < 0 || Lq < 0 || Lk < 0 || !head_dim_ok(Dqk) || !head_dim_ok(Dv)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  const FwdPlan pl = plan_fwd(dtype, mode, magi_tasks, B, H, Lq, Lk, Dqk, Dv);
+  *out = dmad_plan{};
+  out->kernel = pl.kernel;
+  out->grid = pl.grid;
+  out->xcd_order = pl.xcd_order;
+  out->chunks = (int32_t)pl.chunks;
+  out->transposed_copies = pl.copies;
+  out->workspace_bytes = pl.ws;
+  return ok();
+}
+int dmad_attn_bwd_plan(int dtype, int full, int tangent_grads, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                       dmad_plan* out) {
+  if (out == nullptr) return fail(DMAD_ERR_INVALID, "plan: null pointer");
+  if (dtype != DMAD_BF16 && dtype != DMAD_F16 && dtype != DMAD_F32)
+    return fail(DMAD_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+  if ((full != 0 && full != 1) || (tangent_grads != 0 && tangent_grads != 1))
+    return fail(DMAD_ERR_INVALID, "full and tangent_grads must be 0 or 1");
+  if (tangent_grads && !full) return fail(DMAD_ERR_INVALID, "tangent gradients need the cotangent dto");
+  if (B < 0 || H < 0 || Lq < 0 || Lk < 0 || !head_dim_ok(D)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  if (full && D > 128) return fail(DMAD_ERR_UNSUPPORTED, "the full backward supports head dims up to 128");
+  if (full && dtype == DMAD_F32) return fail(DMAD_ERR_UNSUPPORTED, "the full backward takes bf16 or fp16 operands");
+  const BwdPlan pl = plan_bwd(dtype, full != 0, tangent_grads != 0, B, H, Lq, Lk, D);
+  *out = dmad_plan{};
+  out->kernel = pl.kv;
+  out->kernel2 = pl.dq;
+  out->kernel3 = pl.kv_t;
+  out->kernel4 = pl.dq_t;
+  out->grid = pl.grid_kv;
+  out->grid2 = pl.grid_dq;
+  out->xcd_order = pl.xcd_kv;
+  out->xcd_order2 = pl.xcd_dq;
+  out->chunks = 1;
+  out->transposed_copies = pl.copies;
+  out->workspace_bytes = pl.ws;
+  return ok();
+}
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes) {
   if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
   if (full < 0 || full > 2) return fail(DMAD_ERR_INVALID, "full must be 0, 1 or 2");

@@ -24,13 +24,10 @@ static_assert(fwd_simple_dvc(kFwdJvp, 256) * fwd_generic_chunks(kFwdJvp, 256, 25
 
 template <typename T, int DQK, int DV, int MODE>
 static hipError_t fwd_launch(const FwdParams& p, int grid, hipStream_t s) {
-  // registers spill on the other kernels for these (see fwd_generic_uses_halves;
-  // the K/V-tangent-free mode with 256-wide Q/K and 128-wide V as well)
-  if constexpr (fwd_generic_uses_halves(MODE, DQK, DV, false) || (MODE == kFwdJvpQOnly && DQK == 256 && DV == 128))
-    hipLaunchKernelGGL((attn_fwd_simple_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(256), 0, s, p);
-  else if constexpr (FwdStreamCfg<DQK, DV, MODE>::OK)
+  constexpr GenericFwd kind = generic_fwd_kind<DQK, DV, MODE>();  // launch.h
+  if constexpr (kind == GenericFwd::kStream)
     hipLaunchKernelGGL((attn_fwd_stream_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(512), 0, s, p);
-  else if constexpr (FwdCfg<DQK, DV, MODE>::FITS)
+  else if constexpr (kind == GenericFwd::kTiled)
     hipLaunchKernelGGL((attn_fwd_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(512), 0, s, p);
   else
     hipLaunchKernelGGL((attn_fwd_simple_kernel<T, DQK, DV, MODE>), dim3(grid), dim3(256), 0, s, p);

@@ -167,5 +167,85 @@ hipError_t launch_rmsnorm_rope(const PrologueParams& p, int dtype, hipStream_t s
 hipError_t launch_transpose_pad(const TransposeParams& p, int BH, hipStream_t s);
 hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s);
 
+// ---------------------------------------------------------------- kernel choice per shape
+// The generic forward kernels (transposed V) by (Dqk, Dv, mode): fwd_inst.hip
+// launches, and the launch-plan query names, the kernel this returns.
+enum class GenericFwd { kSimple, kStream, kTiled };
+template <int DQK, int DV, int MODE>
+constexpr GenericFwd generic_fwd_kind() {
+  // registers spill on the other kernels for these (the JVP modes with a
+  // 256-wide V, and the K, V tangent-free mode with 256-wide Q, K and 128-wide V)
+  if constexpr (fwd_generic_uses_halves(MODE, DQK, DV, false) || (MODE == kFwdJvpQOnly && DQK == 256 && DV == 128))
+    return GenericFwd::kSimple;
+  else if constexpr (FwdStreamCfg<DQK, DV, MODE>::OK) return GenericFwd::kStream;
+  else if constexpr (FwdCfg<DQK, DV, MODE>::FITS) return GenericFwd::kTiled;
+  else return GenericFwd::kSimple;
+}
+template <int DQK, int DV>
+inline GenericFwd generic_fwd_kind_of_mode(int mode) {
+  return mode == kFwdPlain ? generic_fwd_kind<DQK, DV, kFwdPlain>()
+         : mode == kFwdJvp ? generic_fwd_kind<DQK, DV, kFwdJvp>()
+                           : generic_fwd_kind<DQK, DV, kFwdJvpQOnly>();
+}
+template <int DQK>
+inline GenericFwd generic_fwd_kind_of(int dv, int mode) {
+  switch (dv) {
+    case 16: return generic_fwd_kind_of_mode<DQK, 16>(mode);
+    case 32: return generic_fwd_kind_of_mode<DQK, 32>(mode);
+    case 64: return generic_fwd_kind_of_mode<DQK, 64>(mode);
+    case 128: return generic_fwd_kind_of_mode<DQK, 128>(mode);
+    default: return generic_fwd_kind_of_mode<DQK, 256>(mode);
+  }
+}
+inline const char* generic_fwd_name(int dqk, int dv, int mode) {
+  GenericFwd k = GenericFwd::kSimple;
+  switch (dqk) {
+    case 16: k = generic_fwd_kind_of<16>(dv, mode); break;
+    case 32: k = generic_fwd_kind_of<32>(dv, mode); break;
+    case 64: k = generic_fwd_kind_of<64>(dv, mode); break;
+    case 128: k = generic_fwd_kind_of<128>(dv, mode); break;
+    default: k = generic_fwd_kind_of<256>(dv, mode); break;
+  }
+  return k == GenericFwd::kStream ? "attn_fwd_stream_kernel" : k == GenericFwd::kTiled ? "attn_fwd_kernel"
+                                                                                       : "attn_fwd_simple_kernel";
+}
+
+// The dO-only backward passes by head dim: bwd_inst.hip launches, and the
+// launch-plan query names, these kernels.
+template <int D>
+constexpr bool kv_dout_only_rows() { return KvTrCfg<D, kKvTrBmq>::FITS; }
+template <int D>
+constexpr bool kv_dout_only_pipe() { return !kv_dout_only_rows<D>() && KvPipeCfg<D, kv_pipe_bmq<D>()>::FITS; }
+template <int D>
+constexpr bool dq_dout_only_rows() { return DqTrCfg<D>::FITS; }
+template <int D>
+constexpr bool dq_dout_only_pipe() { return !dq_dout_only_rows<D>() && DqPipeCfg<D>::FITS; }
+template <int D>
+inline const char* kv_dout_only_name_of() {
+  return kv_dout_only_rows<D>() ? "attn_bwd_kv_tr_kernel" : kv_dout_only_pipe<D>() ? "attn_bwd_kv_pipe_kernel" : "attn_bwd_kernel";
+}
+template <int D>
+inline const char* dq_dout_only_name_of() {
+  return dq_dout_only_rows<D>() ? "attn_bwd_dq_tr_kernel" : dq_dout_only_pipe<D>() ? "attn_bwd_dq_pipe_kernel"
+                                                                                   : "attn_bwd_dq_kernel";
+}
+inline const char* kv_dout_only_name(int d) {
+  switch (d) {
+    case 16: return kv_dout_only_name_of<16>();
+    case 32: return kv_dout_only_name_of<32>();
+    case 64: return kv_dout_only_name_of<64>();
+    case 128: return kv_dout_only_name_of<128>();
+    default: return kv_dout_only_name_of<256>();
+  }
+}
+inline const char* dq_dout_only_name(int d) {
+  switch (d) {
+    case 16: return dq_dout_only_name_of<16>();
+    case 32: return dq_dout_only_name_of<32>();
+    case 64: return dq_dout_only_name_of<64>();
+    case 128: return dq_dout_only_name_of<128>();
+    default: return dq_dout_only_name_of<256>();
+  }
+}
 
 }  // namespace dmad

@@ -200,6 +200,37 @@ int dmad_rmsnorm_rope_jvp(int dtype, int64_t rows, int64_t L, int64_t H, int64_t
                           int64_t out_stride, void* stream);
 
 /*
+ * Launch plan of a call (host only: needs no GPU). The library chooses its
+ * kernels from a fixed per-shape table -- the dtype, the mode, the mask, Lq,
+ * Lk and the head dims -- where the reference autotunes its Triton forward
+ * over 48 configs keyed on (SEQ_LEN_Q, SEQ_LEN_KV, HEAD_DIM_QK, HEAD_DIM_V)
+ * (train/wan/rcm/utils/flash_attention_jvp_triton.py:98-107). The entry points
+ * launch what the plan reports. Kernel names are static strings.
+ */
+typedef struct dmad_plan {
+  const char* kernel;        /* forward kernel; backward: key-stationary pass (dK, dV) */
+  const char* kernel2;       /* backward: query-stationary pass (dQ [, dQd]); forward: NULL */
+  const char* kernel3;       /* backward with tangent gradients: key pass on (dOd, rho) for dKd, dVd; else NULL */
+  const char* kernel4;       /* ... and its query pass for dQd where kernel2 does not give it; else NULL */
+  int64_t grid;              /* workgroups of `kernel` (and of kernel3) */
+  int64_t grid2;             /* workgroups of `kernel2` (and of kernel4); 0 for the forward */
+  int32_t xcd_order;         /* 1: work items dealt contiguously per XCD; 0: head-major (of `kernel`) */
+  int32_t xcd_order2;        /* the same for `kernel2` */
+  int32_t chunks;            /* forward: workgroups per 128-query tile (column chunks of a wide V) */
+  int32_t transposed_copies; /* operands copied transposed into the workspace before the kernels */
+  int64_t workspace_bytes;   /* workspace the call needs */
+} dmad_plan;
+
+/* Plan of dmad_attn_jvp_fwd / dmad_attn_fwd (magi_tasks < 0) or of
+ * dmad_attn_jvp_fwd_magi with magi_tasks tasks; mode as there. */
+int dmad_attn_fwd_plan(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                       int64_t Dqk, int64_t Dv, dmad_plan* plan);
+
+/* Plan of dmad_attn_jvp_bwd; full and tangent_grads: 0 or 1 (dto and dtq/dtk/dtv given). */
+int dmad_attn_bwd_plan(int dtype, int full, int tangent_grads, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                       dmad_plan* plan);
+
+/*
  * Timing hook (no counterpart in the reference; for benchmarks and profilers
  * that time kernels live). `events` points to `count` hipEvent_t handles; while
  * set, every dmad_attn_jvp_fwd / dmad_attn_fwd / dmad_attn_jvp_bwd call on

@@ -1,0 +1,148 @@
+"""The per-shape launch table (dmad_attn_fwd_plan / dmad_attn_bwd_plan), on the CPU.
+
+The reference autotunes its Triton forward over 48 configs keyed on (SEQ_LEN_Q,
+SEQ_LEN_KV, HEAD_DIM_QK, HEAD_DIM_V) (train/wan/rcm/utils/flash_attention_jvp_triton.py:98-107).
+The library instead picks from a fixed table keyed on the dtype, the mode, the mask, Lq, Lk and
+the head dims; the entry points launch what the plan query reports (one function decides both).
+These tests pin the table: the Wan shapes, the reference's harness and test shapes, every head
+dim, fp32, the block-sparse forward, the backward passes, the workspace sizes (equal to the
+workspace queries) and the argument checks.
+"""
+import pytest
+
+from dmad_amd import _native as nat
+
+BF16, F16, F32 = nat.DMAD_BF16, nat.DMAD_F16, nat.DMAD_F32
+PLAIN, JVP, QONLY = nat.DMAD_FWD_PLAIN, nat.DMAD_FWD_JVP, nat.DMAD_FWD_JVP_KV_TANGENT_ZERO
+
+
+def test_wan_shapes():
+    # 14B self-attention: row-reading 32-query-wave kernel, head-major order (256 tiles per head), no workspace
+    p = nat.fwd_plan(BF16, JVP, 1, 40, 32760, 32760, 128, 128)
+    assert (p["kernel"], p["grid"], p["xcd_order"], p["chunks"], p["workspace_bytes"]) == \
+        ("attn_fwd32_kernel", 256 * 40, 0, 1, 0)
+    # text cross-attention (512 keys, Kd = Vd = 0), 14B and 1.3B: two workgroups per CU
+    for H in (40, 12):
+        p = nat.fwd_plan(BF16, QONLY, 1, H, 32760, 512, 128, 128)
+        assert (p["kernel"], p["grid"], p["transposed_copies"]) == ("attn_fwd32_x2_kernel", 256 * H, 0)
+    # 720p: 591 tiles per head
+    p = nat.fwd_plan(BF16, JVP, 1, 40, 75600, 75600, 128, 128)
+    assert (p["kernel"], p["grid"], p["xcd_order"]) == ("attn_fwd32_kernel", 591 * 40, 0)
+
+
+@pytest.mark.parametrize("Lk,kernel", [(1, "attn_fwd32_x2_kernel"), (2048, "attn_fwd32_x2_kernel"),
+                                       (2049, "attn_fwd32_kernel"), (32760, "attn_fwd32_kernel")])
+def test_short_key_kernel_is_keyed_on_lk(Lk, kernel):
+    """Kd = Vd = 0 with 128-wide heads: at most 64 key tiles run two workgroups per CU."""
+    for dt in (BF16, F16):
+        assert nat.fwd_plan(dt, QONLY, 1, 40, 32760, Lk, 128, 128)["kernel"] == kernel
+    # the other modes and head dims never take it
+    assert nat.fwd_plan(BF16, JVP, 1, 40, 32760, Lk, 128, 128)["kernel"] == "attn_fwd32_kernel"
+    assert nat.fwd_plan(BF16, PLAIN, 1, 40, 32760, Lk, 128, 128)["kernel"] == "attn_fwd32_kernel"
+    assert nat.fwd_plan(BF16, QONLY, 1, 40, 32760, Lk, 64, 64)["kernel"] == "attn_fwd32_kernel"
+
+
+@pytest.mark.parametrize("L,xcd", [(1024, 1), (4096, 1), (16384, 1), (32640, 1), (32768, 0)])
+@pytest.mark.parametrize("D", [64, 128])
+def test_block_order_is_keyed_on_query_tiles(L, xcd, D):
+    """The reference harness shape (B=4, H=32): fewer than 256 query tiles per head deal each
+    XCD a contiguous range of work items; from 256 on the order is head-major."""
+    p = nat.fwd_plan(F16, JVP, 4, 32, L, L, D, D)
+    assert (p["kernel"], p["grid"], p["xcd_order"]) == ("attn_fwd32_kernel", (L + 127) // 128 * 128, xcd)
+    b = nat.bwd_plan(F16, 4, 32, L, L, D)
+    assert (b["kernel"], b["kernel2"]) == ("attn_bwd_kv_tr_kernel", "attn_bwd_dq_tr_kernel")
+    assert (b["xcd_order"], b["xcd_order2"]) == (xcd, xcd)
+
+
+@pytest.mark.parametrize("D,kernel,chunks", [(16, "attn_fwd_simple_kernel", 1), (32, "attn_fwd_kernel", 1),
+                                             (256, "attn_fwd_simple_kernel", 2)])
+def test_generic_head_dims(D, kernel, chunks):
+    """Head dims the row-reading kernels do not take run on transposed copies of V (and Vd)."""
+    p = nat.fwd_plan(F16, JVP, 4, 32, 4096, 4096, D, D)
+    assert (p["kernel"], p["chunks"], p["transposed_copies"]) == (kernel, chunks, 2)
+    assert p["grid"] == 32 * 128 * chunks
+    assert p["workspace_bytes"] == nat.fwd_workspace_bytes(JVP, 4, 32, 4096, D, D) > 0
+    assert nat.fwd_plan(F16, PLAIN, 4, 32, 4096, 4096, D, D)["transposed_copies"] == 1
+
+
+def test_mixed_head_dims():
+    # Dqk != Dv: the reference's _test_jvp_ca shapes
+    p = nat.fwd_plan(F16, JVP, 1, 2, 1024, 512, 128, 64)
+    assert p["transposed_copies"] == 2 and p["kernel"] != "attn_fwd32_kernel"
+    assert nat.fwd_plan(F16, JVP, 1, 2, 1024, 512, 64, 64)["kernel"] == "attn_fwd32_kernel"
+
+
+def test_block_sparse_forward():
+    for D, kernel in ((128, "attn_fwd32_kernel"), (64, "attn_fwd32_kernel"), (32, "attn_fwd_simple_kernel")):
+        p = nat.fwd_plan(BF16, JVP, 1, 40, 24960, 32760, D, D, magi_tasks=198)
+        assert (p["kernel"], p["grid"], p["xcd_order"]) == (kernel, 198 * 40, 1)
+    # Kd = Vd = 0 with a mask stays on the block-sparse kernel
+    assert nat.fwd_plan(BF16, QONLY, 1, 40, 24960, 512, 128, 128, magi_tasks=198)["kernel"] == "attn_fwd32_kernel"
+    with pytest.raises(ValueError):
+        nat.fwd_plan(BF16, PLAIN, 1, 40, 24960, 512, 128, 128, magi_tasks=198)
+
+
+@pytest.mark.parametrize("Dqk,Dv,chunks", [(64, 64, 1), (128, 128, 1), (256, 256, 4), (128, 256, 2), (16, 32, 1)])
+def test_fp32_forward(Dqk, Dv, chunks):
+    p = nat.fwd_plan(F32, JVP, 4, 32, 4096, 4096, Dqk, Dv)
+    assert (p["kernel"], p["chunks"], p["grid"], p["transposed_copies"], p["workspace_bytes"]) == \
+        ("attn_f32_fwd_kernel", chunks, 32 * 128 * chunks, 0, 0)
+
+
+def test_backward_passes():
+    # dO-only, 64- and 128-wide heads: row-reading passes, statistics only
+    for D in (64, 128):
+        b = nat.bwd_plan(BF16, 1, 40, 32760, 32760, D)
+        assert (b["kernel"], b["kernel2"], b["kernel3"], b["kernel4"]) == \
+            ("attn_bwd_kv_tr_kernel", "attn_bwd_dq_tr_kernel", None, None)
+        assert (b["grid"], b["grid2"], b["transposed_copies"]) == (256 * 40, 256 * 40, 0)
+    # the full derivative of 128-wide heads (its query pass gives dQd)
+    b = nat.bwd_plan(BF16, 1, 40, 32760, 32760, 128, full=True, tangent_grads=True)
+    assert (b["kernel"], b["kernel2"], b["kernel3"], b["kernel4"]) == \
+        ("attn_bwd_kv_full_kernel", "attn_bwd_dq_full_kernel", "attn_bwd_kv_tr_kernel", None)
+    assert b["transposed_copies"] == 0
+    # the full derivative of the other head dims: generic passes on six transposed copies
+    b = nat.bwd_plan(F16, 1, 2, 1024, 1024, 64, full=True, tangent_grads=True)
+    assert (b["kernel"], b["kernel2"], b["kernel3"], b["kernel4"]) == \
+        ("attn_bwd_kernel", "attn_bwd_dq_kernel", "attn_bwd_kv_tr_kernel", "attn_bwd_dq_tr_kernel")
+    assert b["transposed_copies"] == 6
+    # dO-only for the generic head dims: Q^T, dO^T and K^T copies
+    assert nat.bwd_plan(F16, 4, 32, 4096, 4096, 32)["kernel"] == "attn_bwd_kv_pipe_kernel"
+    assert nat.bwd_plan(F16, 4, 32, 4096, 4096, 32)["kernel2"] == "attn_bwd_dq_pipe_kernel"
+    for D in (16, 256):
+        b = nat.bwd_plan(F16, 4, 32, 4096, 4096, D)
+        assert (b["kernel"], b["kernel2"], b["transposed_copies"]) == ("attn_bwd_kernel", "attn_bwd_dq_kernel", 3)
+    # fp32 (dO only): 64-key / 64-query workgroups at D = 256, 128 otherwise
+    b = nat.bwd_plan(F32, 4, 32, 4096, 4096, 256)
+    assert (b["kernel"], b["kernel2"], b["grid"], b["grid2"]) == \
+        ("attn_f32_bwd_kv_kernel", "attn_f32_bwd_dq_kernel", 64 * 128, 64 * 128)
+    assert nat.bwd_plan(F32, 4, 32, 4096, 4096, 128)["grid"] == 32 * 128
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("Lq,Lk", [(999, 515), (32760, 512), (1, 1)])
+def test_workspace_matches_the_queries(D, Lq, Lk):
+    for mode in (PLAIN, JVP, QONLY):
+        assert nat.fwd_plan(BF16, mode, 2, 3, Lq, Lk, D, D)["workspace_bytes"] == \
+            nat.fwd_workspace_bytes(mode, 2, 3, Lk, D, D)
+    fulls = ((0, False), (1, False), (2, True)) if D <= 128 else ((0, False),)
+    for full, tg in fulls:
+        assert nat.bwd_plan(BF16, 2, 3, Lq, Lk, D, full=full > 0, tangent_grads=tg)["workspace_bytes"] == \
+            nat.bwd_workspace_bytes(full, 2, 3, Lq, Lk, D)
+
+
+def test_argument_checks():
+    with pytest.raises(ValueError):
+        nat.fwd_plan(BF16, JVP, 1, 2, 64, 64, 96, 96)  # head dim outside {16, 32, 64, 128, 256}
+    with pytest.raises(ValueError):
+        nat.fwd_plan(BF16, 7, 1, 2, 64, 64, 64, 64)
+    with pytest.raises(ValueError):
+        nat.fwd_plan(BF16, JVP, -1, 2, 64, 64, 64, 64)
+    with pytest.raises(NotImplementedError):
+        nat.fwd_plan(9, JVP, 1, 2, 64, 64, 64, 64)
+    with pytest.raises(NotImplementedError):
+        nat.bwd_plan(BF16, 1, 2, 64, 64, 256, full=True)
+    with pytest.raises(NotImplementedError):
+        nat.bwd_plan(F32, 1, 2, 64, 64, 64, full=True)
+    with pytest.raises(ValueError):
+        nat.bwd_plan(BF16, 1, 2, 64, 64, 64, tangent_grads=True)
