@@ -108,3 +108,45 @@ def test_nonfinite_input_stays_in_its_slice(gpu, D, dtype, where, val):
         assert n_bad["o"] > 0 and n_bad["dk"] > 0
     if where in ("q", "k"):  # dV = P^T dO does not involve V
         assert n_bad["dv"] > 0
+
+
+@pytest.mark.parametrize("where", ["q", "k", "v", "tq"])
+@pytest.mark.parametrize("val", [math.nan, math.inf])
+def test_nonfinite_kv_tangent_free_forward(gpu, where, val):
+    """The same contract for the K, V tangent-free forward (Kd = Vd = 0, 128-wide heads, short key
+    sequences: the two-workgroups-per-CU kernel): O, Od, LSE and mu of the other slices bitwise
+    clean, the poisoned slice non-finite exactly where float64 math is."""
+    from dmad_amd.jvp_attention import jvp_attention_forward
+
+    print(f"case nonfinite kv-tangent-free {where}={val}", flush=True)
+    x = _inputs(128, seed=11, dtype=torch.bfloat16)
+
+    def run(inp):
+        g = {n: t.to(gpu) for n, t in inp.items()}
+        o, to, lse, mu = jvp_attention_forward(g["q"], g["k"], g["v"], g["tq"], None, None, 128 ** -0.5)
+        torch.cuda.synchronize()
+        return {"o": o.cpu(), "to": to.cpu(), "lse": lse.cpu(), "mu": mu.cpu()}
+
+    clean = run(x)
+    y = _poison(x, where, val)
+    got = run(y)
+    for name, t in got.items():
+        for b in range(B):
+            for h in range(H):
+                if (b, h) != (1, 0):
+                    assert torch.equal(t[b, h], clean[name][b, h]), (name, b, h)
+    if where == "tq":
+        for name in ("o", "lse"):
+            assert torch.equal(got[name][1, 0], clean[name][1, 0]), name
+    sl = {n: t[1:2, 0:1].double() for n, t in y.items()}
+    zk, zv = torch.zeros_like(sl["k"]), torch.zeros_like(sl["v"])
+    ro, rto, _, _ = orc.jvp_closed_form(sl["q"], sl["k"], sl["v"], sl["tq"], zk, zv)
+    for name, r in (("o", ro), ("to", rto)):
+        gv, rv = got[name][1, 0].double(), r[0, 0]
+        fin_g, fin_r = torch.isfinite(gv), torch.isfinite(rv)
+        assert torch.equal(fin_g, fin_r), (name, int((~fin_g).sum()), int((~fin_r).sum()))
+        both = fin_g & fin_r
+        if both.any():
+            assert orc.rel_l2(gv[both], rv[both]) <= 1e-2, name
+        if name == "to" or where != "tq":
+            assert (~fin_r).any(), name
