@@ -395,16 +395,18 @@ def main():
 
     def step(record):
         if record:
-            tf, tb = _native.KernelTimer(1), _native.KernelTimer(2)
-            timers.append((tf, tb))
+            tf, tb, tc = _native.KernelTimer(1), _native.KernelTimer(2), _native.KernelTimer(1)
+            timers.append((tf, tb, tc))
             with tf:
                 o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
             with tb:
                 jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
+            with tc:
+                jvp_attention_forward(q, kc, vc, tq, None, None, s)
         else:
             o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
             jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
-        jvp_attention_forward(q, kc, vc, tq, None, None, s)
+            jvp_attention_forward(q, kc, vc, tq, None, None, s)
 
     for _ in range(args.warmup):
         step(False)
@@ -420,19 +422,20 @@ def main():
     wall = time.perf_counter() - t0
     w1 = time.time()
     ms_step = e0.elapsed_time(e1) / args.steps
-    k_ms = {"fwd": 0.0, "bwd_dkdv": 0.0, "bwd_dq": 0.0}
-    for tf, tb in timers:
+    k_ms = {"fwd": 0.0, "bwd_dkdv": 0.0, "bwd_dq": 0.0, "cross": 0.0}
+    for tf, tb, tc in timers:
         k_ms["fwd"] += tf.elapsed()[0] / len(timers)
         b = tb.elapsed()
         k_ms["bwd_dkdv"] += b[0] / len(timers)
         k_ms["bwd_dq"] += b[1] / len(timers)
+        k_ms["cross"] += tc.elapsed()[0] / len(timers)
     value = f_step / (ms_step * 1e-3) / 1e12
 
     # algorithmic flops of each main kernel (GEMM flops it must do, counting the
     # S and dP recomputation of the dQ pass)
-    k_flops = {"fwd": f_fwd, "bwd_dkdv": 8.0 * H * L * L * D, "bwd_dq": 6.0 * H * L * L * D}
+    k_flops = {"fwd": f_fwd, "bwd_dkdv": 8.0 * H * L * L * D, "bwd_dq": 6.0 * H * L * L * D, "cross": f_cross}
     k_names = {"fwd": "attn_fwd32_kernel<bf16,jvp>", "bwd_dkdv": "attn_bwd_kv_tr_kernel<bf16,128>",
-               "bwd_dq": "attn_bwd_dq_tr_kernel<bf16,128>"}
+               "bwd_dq": "attn_bwd_dq_tr_kernel<bf16,128>", "cross": "attn_fwd32_x2_kernel<bf16>"}
     dom = max(k_ms, key=k_ms.get)
     dom_flops, dom_name = k_flops[dom], k_names[dom]
     achieved = dom_flops / (k_ms[dom] * 1e-3) / 1e12
@@ -460,6 +463,7 @@ def main():
         "ms_self_fwd_jvp_kernel": round(k_ms["fwd"], 3),
         "ms_self_bwd_dkdv_kernel": round(k_ms["bwd_dkdv"], 3),
         "ms_self_bwd_dq_kernel": round(k_ms["bwd_dq"], 3),
+        "ms_cross_fwd_jvp_kernel": round(k_ms["cross"], 4),
         "kernel_pct_peak": {n: round(100 * k_flops[n] / (k_ms[n] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
                             for n in k_ms},
         "roofline": {
