@@ -95,12 +95,23 @@ def _full_backward_unavailable(dqk: int, dv: int, dtype: torch.dtype) -> bool:
     return False
 
 
+_strides_ok: dict = {}
+
+
 def _kernel_ready(t: torch.Tensor) -> bool:
-    """Unit inner stride, 16-byte aligned rows (what the kernels load from)."""
-    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
-        return False
-    per16 = 16 // t.element_size()
-    return all(s % per16 == 0 for s in t.stride()[:-1])
+    """Unit inner stride, 16-byte aligned rows (what the kernels load from). The stride
+    part is a function of the stride tuple and element size, decided once per pair (this
+    sits on every call's host path)."""
+    st = t.stride()
+    key = (st, t.element_size())
+    ok = _strides_ok.get(key)
+    if ok is None:
+        per16 = 16 // key[1]
+        ok = st[-1] == 1 and all(x % per16 == 0 for x in st[:-1])
+        if len(_strides_ok) > 4096:
+            _strides_ok.clear()
+        _strides_ok[key] = ok
+    return ok and t.data_ptr() % 16 == 0
 
 
 def _prep(*ts):
