@@ -26,8 +26,10 @@
 //   request tile i+2 into the stage step i-1 read;
 //   phase A  S^T, Sd^T of tile i (K slices from the ring, Q from registers,
 //            Qd slices from the wave's region);
-//   softmax of tile i on the VALU (V^T operands of phase B read meanwhile);
-//   phase B  O~^T += V^T P~^T, C~^T += V^T H~^T.
+//   softmax of tile i's first 16-key chunk on the VALU (V^T operands of phase B
+//            read meanwhile);
+//   phase B  O~^T += V^T P~^T, C~^T += V^T H~^T, the second chunk's softmax
+//            beside the first chunk's MFMAs.
 #pragma once
 #include "attn_fwd32.h"
 
@@ -166,14 +168,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   }
   float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
 
-  // online softmax of one tile (log2 domain; lanes l and l^32 share a query):
+  // Online softmax of one tile (log2 domain; lanes l and l^32 share a query):
   // value v of the score tile is key 16 (v >> 3) + 8 half + (v & 7); P~, H~ are
-  // packed as the B operands of the two 16-key chunks. Each pair of values is
-  // finished (exp, sums, pack) before the next starts, with scheduling barriers
-  // between pairs and the running sums pinned after each: the compiler would
-  // otherwise raise all 16 exps first, or sink the sums to the end of the step,
-  // and hold every value live at once.
-  auto softmax = [&](const f32x16_t& sc, const f32x16_t& tc, i32x4_t (&pk)[2], i32x4_t (&hk)[2]) {
+  // packed as the B operands of the two 16-key chunks. soft_head takes the row
+  // max and the lazy-rescale decision (and rescales O~, C~ before any of the
+  // tile's MFMAs), soft_pair finishes one pair of values (exps, running sums,
+  // packs). The running sums are re-defined after each pair (an empty asm):
+  // the compiler would otherwise sink them to the end of the step and keep all
+  // 32 values live.
+  float neg_m = 0.f;
+  auto soft_head = [&](const f32x16_t& sc) -> float {
     float a = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     float b2 = fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]));
     float c2 = fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11]));
@@ -184,26 +188,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
     const float m_new = moved ? fmaxf(m_i, mx) : m_i;
     const float alpha = fast_exp2(m_i - m_new);
     m_i = m_new;
-    const float neg_m = -m_new;
-    float ls = 0.f, rs = 0.f;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      const float p0 = fast_exp2(fmaf(sc[v], p.scale_log2, neg_m));
-      const float p1 = fast_exp2(fmaf(sc[v + 1], p.scale_log2, neg_m));
-      ls += p0;
-      const float h0 = p0 * (tc[v] * p.scale);
-      rs += h0;
-      ls += p1;
-      const float h1 = p1 * (tc[v + 1] * p.scale);
-      rs += h1;
-      pk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(p0, p1);
-      hk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(h0, h1);
-      asm volatile("" : "+v"(ls), "+v"(rs));  // the sums here, not sunk to their use
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    l_i = l_i * alpha + ls;
-    r_i = r_i * alpha + rs;
+    neg_m = -m_new;
     if (moved) {  // rare with the slack
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
@@ -214,6 +199,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
         }
       }
     }
+    return alpha;
+  };
+  auto soft_pair = [&](int v, const f32x16_t& sc, const f32x16_t& tc, i32x4_t (&pk)[2], i32x4_t (&hk)[2], float& ls,
+                       float& rs) {
+    const float p0 = fast_exp2(fmaf(sc[v], p.scale_log2, neg_m));
+    const float p1 = fast_exp2(fmaf(sc[v + 1], p.scale_log2, neg_m));
+    ls += p0;
+    const float h0 = p0 * (tc[v] * p.scale);
+    rs += h0;
+    ls += p1;
+    const float h1 = p1 * (tc[v + 1] * p.scale);
+    rs += h1;
+    pk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(p0, p1);
+    hk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(h0, h1);
+    asm volatile("" : "+v"(ls), "+v"(rs));
   };
 
   constexpr int PFA = 2;  // phase-A operand pairs (K slice, Qd slice) read ahead
@@ -268,10 +268,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
     i32x4_t vb[PFB];
 #pragma unroll
     for (int j = 0; j < PFB; ++j) vb[j] = load_vt(j);
+    // softmax of the first 16-key chunk (two pairs per scheduling group)
     i32x4_t pk[2], hk[2];
-    softmax(sc, tc, pk, hk);
+    float ls = 0.f, rs = 0.f;
+    const float alpha = soft_head(sc);
     __builtin_amdgcn_sched_barrier(0);
-    // phase B: O~^T += V^T P~^T, C~^T += V^T H~^T (per 16-key chunk t, block db)
+#pragma unroll
+    for (int v = 0; v < 8; v += 2) {
+      soft_pair(v, sc, tc, pk, hk, ls, rs);
+      if (v & 2) __builtin_amdgcn_sched_barrier(0);
+    }
+    // phase B: O~^T += V^T P~^T, C~^T += V^T H~^T (per 16-key chunk t, block db);
+    // the second chunk's values are computed beside the first chunk's MFMAs
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int t = j / DB, db = j % DB;
@@ -279,8 +287,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
       if (j + PFB < NB) vb[j % PFB] = load_vt(j + PFB);
       oacc[db] = mfma32(a, pk[t], oacc[db], T());
       cacc[db] = mfma32(a, hk[t], cacc[db], T());
+      if (j < DB) soft_pair(8 + 2 * j, sc, tc, pk, hk, ls, rs);
       __builtin_amdgcn_sched_barrier(0);
     }
+    l_i = l_i * alpha + ls;
+    r_i = r_i * alpha + rs;
   };
 
   // ---- prologue: key tiles 0, 1 (behind the Q and Qd requests)
