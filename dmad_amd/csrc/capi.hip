@@ -356,7 +356,7 @@ BwdPlan plan_bwd(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int64_t
   const int64_t BH = B * H;
   if (dtype == DMAD_F32) {
     // fp32 operands (dO only): fp32-MFMA passes, head-major order
-    const int64_t bk = D > 128 ? 64 : 128, bm = D > 128 ? 64 : 128;
+    const int64_t bk = dmad::f32_kv_block((int)D), bm = dmad::f32_dq_block((int)D);
     pl.kv = "attn_f32_bwd_kv_kernel";
     pl.dq = "attn_f32_bwd_dq_kernel";
     pl.grid_kv = (Lk + bk - 1) / bk * BH;

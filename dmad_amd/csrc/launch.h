@@ -210,6 +210,26 @@ inline const char* generic_fwd_name(int dqk, int dv, int mode) {
                                                                                        : "attn_fwd_simple_kernel";
 }
 
+// Keys (queries) per workgroup of the fp32 dK/dV (dQ) pass for head dim d.
+inline int f32_kv_block(int d) {
+  switch (d) {
+    case 16: return F32KvCfg<16>::BK;
+    case 32: return F32KvCfg<32>::BK;
+    case 64: return F32KvCfg<64>::BK;
+    case 128: return F32KvCfg<128>::BK;
+    default: return F32KvCfg<256>::BK;
+  }
+}
+inline int f32_dq_block(int d) {
+  switch (d) {
+    case 16: return F32DqCfg<16>::BM;
+    case 32: return F32DqCfg<32>::BM;
+    case 64: return F32DqCfg<64>::BM;
+    case 128: return F32DqCfg<128>::BM;
+    default: return F32DqCfg<256>::BM;
+  }
+}
+
 // The dO-only backward passes by head dim: bwd_inst.hip launches, and the
 // launch-plan query names, these kernels.
 template <int D>
