@@ -37,7 +37,9 @@ def _hipcc() -> str:
 
 
 # Packed fp32 VALU instructions are switched off for all device code. No kernel
-# produces or tests NaNs, so fmaxf needs no operand canonicalisation.
+# branches on a NaN test, so fmaxf needs no operand canonicalisation; a NaN or
+# an Inf in the inputs still reaches every output row it touches and no other
+# (batch, head) slice (tests/test_nonfinite_gpu.py holds that contract).
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
