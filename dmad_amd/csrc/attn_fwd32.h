@@ -105,8 +105,13 @@ __device__ __forceinline__ void stage_store(const lds_char_t* region, int k, int
 // range starting at a 32-key boundary below its first key, and keys outside the
 // current range score -inf (the reference's n_mask, :338-343). Only the tile's
 // rows inside the group's query range are stored (:386-409).
+//
+// Waves per SIMD: one at D = 128 (the JVP modes hold ~460 registers); two at
+// D = 64, four for its dense plain forward (128 registers, 32 KiB of LDS per
+// workgroup; 1-2% faster than two, bitwise equal).
 template <typename T, int MODE, bool MAGI = false, int DH = 128>
-__global__ __launch_bounds__(256, DH == 64 ? 2 : 1) void attn_fwd32_kernel(FwdParams p) {
+__global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2) : 1) void attn_fwd32_kernel(
+    FwdParams p) {
   using C = Fwd32Cfg<MODE, DH>;
   constexpr int D = C::D, BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
   constexpr int NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
