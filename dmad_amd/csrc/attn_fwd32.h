@@ -1,4 +1,4 @@
-// Forward(+JVP) kernel for 128- and 64-wide heads on 32x32x16 MFMAs.
+// Forward(+JVP) kernel for 64-, 128- and (dense) 256-wide heads on 32x32x16 MFMAs.
 //
 // Same semantics as attn_fwd_kernel (the reference kernel `_attn_fwd`,
 // train/wan/rcm/utils/flash_attention_jvp_triton.py:107-232): log2-domain
@@ -11,7 +11,8 @@
 // 32x32 score tile gives each lane 16 keys of its own query and the row
 // statistics are per-lane scalars (the other 16 keys sit in lane l^32).
 // K, Kd, V, Vd stream as row-major 32-key tiles through a four-stage LDS ring
-// filled by buffer->LDS requests three steps ahead. K rows are read in perm32
+// filled by buffer->LDS requests three steps ahead (three stages, two steps
+// ahead, where four stages do not fit: 256-wide heads with Kd, Vd). K rows are read in perm32
 // order (A operand), so P~ and H~ leave the score tile already in the
 // B-operand layout of O^T += V^T P^T; V^T is read from the row-major V tile
 // with ds_read_b64_tr_b16, so V needs no transposed copy.
@@ -25,41 +26,62 @@
 //            softmax of tile i on the VALU between them
 //   (rescale of O~, C~ when some row's running max moved)
 //   phase B  O~^T += V^T P~^T, C~^T += V^T H~^T + Vd^T P~^T of tile i, with
-//            the requests for tile i+3 spread between the MFMAs
+//            the requests for tile i+3 (i+2) spread between the MFMAs
 // Every MFMA's LDS operand is read four operands ahead.
 #pragma once
 #include "attn_fwd.h"
 
 namespace dmad {
 
+// 256-wide heads in the JVP modes split V (and Vd, O, Od) into two 128-column
+// chunks, one per workgroup (the O~ and C~ accumulators of 256 columns do not
+// fit beside Q, Qd): each chunk's workgroup computes the full 256-wide scores
+// (S, Sd twice over per query tile) and the 128 output columns of its chunk.
+// K, Kd rows are then 512 bytes and V, Vd rows 256 bytes in the ring; with Kd,
+// Vd a stage is 48 KiB, so the ring has three stages. The plain forward keeps
+// all 256 columns in one workgroup (512-byte V rows, four stages).
 template <int MODE, int DH = 128>
 struct Fwd32Cfg {
-  static constexpr int D = DH;
+  static constexpr int D = DH;  // Q, K width
+  static constexpr int DVC = DH == 256 && MODE != kFwdPlain ? 128 : DH;  // V, O columns per workgroup
+  static constexpr int CHUNKS = D / DVC;
   static constexpr int NW = 4;        // waves per workgroup
   static constexpr int BM = 32 * NW;  // query rows per workgroup
   static constexpr int BN = 32;       // keys per pipeline step
   static constexpr int KS = D / 16;   // 16-wide k slices of Q K^T
-  static constexpr int DB = D / 32;   // 32-row blocks of O^T
-  static constexpr int CR = D / 8;    // 16-byte chunks per row
+  static constexpr int DB = DVC / 32;  // 32-row blocks of O^T
+  static constexpr int CR = D / 8;    // 16-byte chunks per K row
+  static constexpr int CRV = DVC / 8;  // 16-byte chunks per V row (its chunk)
   static constexpr int ROWB = D * 2;
-  static constexpr int TILE = BN * ROWB;
+  static constexpr int ROWBV = DVC * 2;
+  static constexpr int TILE = BN * ROWB;    // K (Kd) tile
+  static constexpr int TILEV = BN * ROWBV;  // V (Vd) tile
   static constexpr bool JVP = MODE != kFwdPlain;
   static constexpr bool KVT = MODE == kFwdJvp;
   static constexpr int NTILE = KVT ? 4 : 2;  // row tiles per stage: K, V [, Kd, Vd]
-  static constexpr int OFF_K = 0, OFF_V = TILE, OFF_KT = 2 * TILE, OFF_VT = 3 * TILE;
-  static constexpr int STAGE = NTILE * TILE;
-  static constexpr int NSTAGE = 4;
-  static constexpr int RPW = BN * CR / 64 / NW;       // 1 KiB requests per tile per wave
-  static constexpr int LOADS = NTILE * RPW;           // requests per wave per step
+  static constexpr int OFF_K = 0, OFF_V = TILE, OFF_KT = TILE + TILEV, OFF_VT = 2 * TILE + TILEV;
+  static constexpr int STAGE = (KVT ? 2 : 1) * (TILE + TILEV);
+  static constexpr int NSTAGE = 4 * STAGE <= 160 * 1024 ? 4 : 3;
+  static constexpr int RPW = BN * CR / 64 / NW;    // 1 KiB requests per K tile per wave
+  static constexpr int RPWV = BN * CRV / 64 / NW;  // 1 KiB requests per V tile per wave
+  static constexpr int LOADS = (KVT ? 2 : 1) * (RPW + RPWV);  // requests per wave per step
   static constexpr int NOPA = KS * (KVT ? 2 : 1);     // LDS operands of phase A
   static constexpr int NOPB = 2 * DB * (KVT ? 2 : 1);  // LDS operands of phase B
-  static_assert(BN * CR % (64 * NW) == 0, "tile requests split evenly over the waves");
+  static_assert(BN * CRV % (64 * NW) == 0, "tile requests split evenly over the waves");
   static_assert(NSTAGE * STAGE <= 160 * 1024, "ring exceeds the LDS");
 };
 
 // Head shapes served by attn_fwd32_kernel (the others use attn_fwd_kernel and
 // its variants, which read a transposed copy of V).
 constexpr bool fwd32_supported(int dqk, int dv) { return (dqk == 128 && dv == 128) || (dqk == 64 && dv == 64); }
+// 256-wide heads (dense launches only).
+constexpr bool fwd32_wide_supported(int dqk, int dv) { return dqk == 256 && dv == 256; }
+// Workgroups per query tile (column chunks of V).
+constexpr int fwd32_chunks(int mode, int d) { return d == 256 && mode != kFwdPlain ? 2 : 1; }
+static_assert(fwd32_chunks(kFwdJvp, 256) == Fwd32Cfg<kFwdJvp, 256>::CHUNKS &&
+                  fwd32_chunks(kFwdJvpQOnly, 256) == Fwd32Cfg<kFwdJvpQOnly, 256>::CHUNKS &&
+                  fwd32_chunks(kFwdPlain, 256) == Fwd32Cfg<kFwdPlain, 256>::CHUNKS,
+              "chunk counts of the launch plan");
 
 // ---------------------------------------------------------------- row-staged stores
 // One wave's 32 x D output tile, held in the MFMA C layout (lane: row `col`,
@@ -106,26 +128,28 @@ __device__ __forceinline__ void stage_store(const lds_char_t* region, int k, int
 // current range score -inf (the reference's n_mask, :338-343). Only the tile's
 // rows inside the group's query range are stored (:386-409).
 //
-// Waves per SIMD: one at D = 128 (the JVP modes hold ~460 registers); two at
-// D = 64, four for its dense plain forward (128 registers, 32 KiB of LDS per
-// workgroup; 1-2% faster than two, bitwise equal).
+// Waves per SIMD: one at D = 128 and 256 (the JVP modes hold 416-468
+// registers); two at D = 64, four for its dense plain forward (128 registers,
+// 32 KiB of LDS per workgroup; 1-2% faster than two, bitwise equal).
 template <typename T, int MODE, bool MAGI = false, int DH = 128>
 __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2) : 1) void attn_fwd32_kernel(
     FwdParams p) {
   using C = Fwd32Cfg<MODE, DH>;
   constexpr int D = C::D, BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
+  constexpr int DVC = C::DVC, CRV = C::CRV, ROWBV = C::ROWBV, NSTAGE = C::NSTAGE;
   constexpr int NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
   constexpr float kSlack = RescaleSlack<T>::value;
+  static_assert(!MAGI || C::CHUNKS == 1, "the block-sparse forward takes 64- and 128-wide heads");
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg3[NSTAGE == 4 ? C::STAGE : 16];
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 31, half = lane >> 5;
 
-  int bh, qt, ntiles;
+  int bh, qt, ntiles, chunk = 0;
   int q_lo = 0, q_hi = p.Lq;  // rows this workgroup stores
   int r_beg = 0, r_end = 0;   // key ranges of the group (MAGI)
   if constexpr (MAGI) {
@@ -144,7 +168,11 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     }
   } else {
     const int nqt = (p.Lq + C::BM - 1) / C::BM;
-    const int work = work_item(p.xcd_order);  // block order (common.h)
+    int work = work_item(p.xcd_order);  // block order (common.h)
+    if constexpr (C::CHUNKS > 1) {
+      chunk = work % C::CHUNKS;  // the chunks of one query tile are adjacent work items
+      work /= C::CHUNKS;
+    }
     bh = work / nqt;
     qt = work - bh * nqt;
     ntiles = (p.Lk + BN - 1) / BN;
@@ -172,7 +200,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // softmax. This unit is compiled with MFMAs in VGPR form
   // (-amdgpu-mfma-vgpr-form). 64-wide heads keep everything in VGPRs, two waves
   // per SIMD.
-  if constexpr (DH == 128) {
+  if constexpr (DH >= 128) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       asm volatile("" : "+a"(qreg[s]));
@@ -182,8 +210,9 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
 
   // ---- key-side resources and per-lane request offsets (tile independent)
   const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
-  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
-  const int64_t khead = b * p.k_sb + h * p.k_sh, vhead = b * p.v_sb + h * p.v_sh;
+  // V (Vd) resources start at this workgroup's column chunk
+  const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + DVC) * 2);
+  const int64_t khead = b * p.k_sb + h * p.k_sh, vhead = b * p.v_sb + h * p.v_sh + chunk * DVC;
   const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + khead * 2, k_bytes);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc((const char*)p.v + vhead * 2, v_bytes);
   __amdgpu_buffer_rsrc_t rtk = rk, rtv = rv;
@@ -191,21 +220,30 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     rtk = make_rsrc((const char*)p.tk + khead * 2, k_bytes);
     rtv = make_rsrc((const char*)p.tv + vhead * 2, v_bytes);
   }
-  constexpr int RPW = C::RPW;
-  uint32_t roff_k[RPW], roff_v[RPW];
+  constexpr int RPW = C::RPW, RPWV = C::RPWV;
+  uint32_t roff_k[RPW], roff_v[RPWV];
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const int pch = (wave + j * C::NW) * 64 + lane;
     const int row = pch / CR, phys = pch % CR;
     const int logical = phys ^ trswz<CR>(row & 15);
     roff_k[j] = (uint32_t)((int64_t)row * p.k_sl * 2) + logical * 16;
-    roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
+    if constexpr (RPWV == RPW) roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
+  }
+  if constexpr (RPWV != RPW) {
+#pragma unroll
+    for (int j = 0; j < RPWV; ++j) {
+      const int pch = (wave + j * C::NW) * 64 + lane;
+      const int row = pch / CRV, phys = pch % CRV;
+      const int logical = phys ^ trswz<CRV>(row & 15);
+      roff_v[j] = (uint32_t)((int64_t)row * p.v_sl * 2) + logical * 16;
+    }
   }
   const uint32_t k_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
   const uint32_t v_step = (uint32_t)((int64_t)BN * p.v_sl * 2);
 
   auto stage = [&](auto kk) -> lds_char_t* {
-    constexpr int k = decltype(kk)::value & 3;
+    constexpr int k = decltype(kk)::value % NSTAGE;
     if constexpr (k == 0) return (lds_char_t*)stg0;
     else if constexpr (k == 1) return (lds_char_t*)stg1;
     else if constexpr (k == 2) return (lds_char_t*)stg2;
@@ -215,7 +253,20 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // whose first key row is kt); tiles at or beyond the end read zeros or
   // in-range rows into a stage nobody reads again
   auto issue_load = [&](lds_char_t* st, int kt, int li) {
-    const int t = li % C::NTILE, jj = li / C::NTILE, i = wave + jj * C::NW;
+    // request li: tile t, 1 KiB slot jj of this wave. Equal K and V rows: the
+    // tiles interleave; otherwise K's requests, then Kd's, then V's and Vd's
+    int t = li % C::NTILE, jj = li / C::NTILE;
+    if constexpr (RPWV != RPW) {
+      constexpr int NK = (C::KVT ? 2 : 1) * RPW;
+      if (li < NK) {
+        t = C::KVT ? 2 * (li / RPW) : 0;
+        jj = li % RPW;
+      } else {
+        t = 1 + (C::KVT ? 2 * ((li - NK) / RPWV) : 0);
+        jj = (li - NK) % RPWV;
+      }
+    }
+    const int i = wave + jj * C::NW;
     uint32_t ks, vs;
     if constexpr (MAGI) {
       ks = (uint32_t)kt * (uint32_t)(p.k_sl * 2);
@@ -232,12 +283,19 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
 
   // ---- LDS read offsets: K rows (row perm32(col), chunk 2s + half) and V^T
   // through lds_read_tr16 (block db, keys 16 t + 8 (g >> 1) + (0..3 | 4..7))
-  int sx[KS];
+  // 256-wide heads keep only slice 0's offset: slice s of a 512-byte row sits
+  // at sx[0] ^ 32 s (the row bits lie above the XOR), rebuilt at each read
+  constexpr int NSX = D == 256 ? 1 : KS;
+  int sx[NSX];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
+  for (int s = 0; s < NSX; ++s) {
     const int r = perm32(col);
     sx[s] = r * ROWB + (((2 * s + half) ^ trswz<CR>(r & 15)) << 4);
   }
+  auto sxo = [&](int s) -> int {
+    if constexpr (NSX == 1) return sx[0] ^ (32 * s);
+    else return sx[s];
+  };
   int tx[DB][2];
   {
     const int g = lane >> 4, r = (lane & 15) >> 2, c = lane & 3;
@@ -246,8 +304,8 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int row = 8 * (g >> 1) + 4 * hh + r;  // plus 16 t
-        const int chunk = 4 * db + 2 * (g & 1) + (c >> 1);
-        tx[db][hh] = row * ROWB + ((chunk ^ trswz<CR>(row & 15)) << 4) + 8 * (c & 1);
+        const int ch = 4 * db + 2 * (g & 1) + (c >> 1);
+        tx[db][hh] = row * ROWBV + ((ch ^ trswz<CRV>(row & 15)) << 4) + 8 * (c & 1);
       }
     }
   }
@@ -255,7 +313,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // offset folds into the LDS instructions' immediate per step.
   auto pin_offsets = [&]() {
 #pragma unroll
-    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(sx[s]));
+    for (int s = 0; s < NSX; ++s) asm volatile("" : "+v"(sx[s]));
 #pragma unroll
     for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(tx[db][0]), "+v"(tx[db][1]));
   };
@@ -282,10 +340,10 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     if (o < NOPA) {
       const int s = C::KVT ? o >> 1 : o;
       const int off = (C::KVT && (o & 1)) ? C::OFF_KT : C::OFF_K;
-      return *(lds_i32x4_t*)(s_next + off + sx[s]);
+      return *(lds_i32x4_t*)(s_next + off + sxo(s));
     }
     const OpB ob = op_b(o - NOPA);
-    const lds_char_t* base = s_cur + (ob.vd ? C::OFF_VT : C::OFF_V) + ob.t * 16 * ROWB;
+    const lds_char_t* base = s_cur + (ob.vd ? C::OFF_VT : C::OFF_V) + ob.t * 16 * ROWBV;
     const u32x2_t lo = lds_read_tr16(base + tx[ob.db][0]);
     const u32x2_t hi = lds_read_tr16(base + tx[ob.db][1]);
     return i32x4_t{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
@@ -308,7 +366,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // Wan2.1-14B shape); the plain forward keeps them in VGPRs, where it fits two
   // waves per SIMD. Code that touches AGPR accumulators with the VALU (the
   // rescale, the epilogue) waits for the MFMAs first.
-  constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI && DH == 128 && !__is_same(T, _Float16);
+  constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI && ((DH == 128 && !__is_same(T, _Float16)) || DH == 256);
   auto acc_mfma = [&](f32x16_t& c, i32x4_t a, i32x4_t b) {
     if constexpr (kAccAgpr) mfma32_acc(c, a, b, T());
     else c = mfma32(a, b, c, T());
@@ -382,12 +440,26 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     }
   };
   auto rescale = [&](float alpha) {
+    if constexpr (C::CHUNKS > 1 && kAccAgpr) {
+      // 256-wide heads (all AGPRs taken): one 16-value block at a time, so the
+      // copies through VGPRs need 16 of them rather than all 128
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
+      for (int d = 0; d < 2 * DB; ++d) {
+        f32x16_t& a = d < DB ? oacc[d] : cacc[d - DB];
+        asm volatile("" : "+a"(a));  // read after the previous block's write-back
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        oacc[d][v] *= alpha;
-        if constexpr (C::JVP) cacc[d][v] *= alpha;
+        for (int v = 0; v < 16; ++v) a[v] *= alpha;
+        asm volatile("" : "+a"(a));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          oacc[d][v] *= alpha;
+          if constexpr (C::JVP) cacc[d][v] *= alpha;
+        }
       }
     }
   };
@@ -407,11 +479,12 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // tile i (sc, tc); phase B on tile i's V; requests tile i+3
   auto step = [&](auto kk, int i, const f32x16_t& sc, const f32x16_t& tc, f32x16_t& sn, f32x16_t& tn) {
     constexpr int k = decltype(kk)::value;
-    ring_sync<C::LOADS>();  // tile i+1 has landed (tile i+2 may be in flight)
+    // tile i+1 has landed (four stages: tile i+2 may be in flight)
+    ring_sync<(NSTAGE - 3) * C::LOADS>();
     pin_offsets();
     const lds_char_t* s_next = stage(IC<k + 1>{});
     const lds_char_t* s_cur = stage(IC<k>{});
-    lds_char_t* s_req = stage(IC<k + 3>{});
+    lds_char_t* s_req = stage(IC<k + NSTAGE - 1>{});
     i32x4_t opr[PF];
 #pragma unroll
     for (int o = 0; o < PF; ++o) opr[o] = load_op(s_next, s_cur, o);
@@ -446,7 +519,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
       if (o + PF < NOP) opr[o % PF] = load_op(s_next, s_cur, o + PF);
 #pragma unroll
       for (int li = 0; li < C::LOADS; ++li) {
-        if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, MAGI ? ci.start : i + 3, li);
+        if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, MAGI ? ci.start : i + NSTAGE - 1, li);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -492,10 +565,12 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
 #pragma unroll
     for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+    if constexpr (NSTAGE == 4) {
 #pragma unroll
-    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+      for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+    }
   }
-  ring_sync<2 * C::LOADS>();  // Q slices and tile 0
+  ring_sync<(NSTAGE - 2) * C::LOADS>();  // Q slices and tile 0
   f32x16_t sa, ta, sb, tb;
   {
     const lds_char_t* s0 = stage(IC<0>{});
@@ -504,20 +579,45 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     for (int o = 0; o < NOPA; ++o) mfma_op(o, load_op(s0, s0, o), sa, ta, none, none);
   }
   int i = 0;
-  for (; i + 4 < ntiles; i += 4) {
-    step(IC<0>{}, i, sa, ta, sb, tb);
-    step(IC<1>{}, i + 1, sb, tb, sa, ta);
-    step(IC<2>{}, i + 2, sa, ta, sb, tb);
-    step(IC<3>{}, i + 3, sb, tb, sa, ta);
+  if constexpr (NSTAGE == 4) {
+    for (; i + 4 < ntiles; i += 4) {
+      step(IC<0>{}, i, sa, ta, sb, tb);
+      step(IC<1>{}, i + 1, sb, tb, sa, ta);
+      step(IC<2>{}, i + 2, sa, ta, sb, tb);
+      step(IC<3>{}, i + 3, sb, tb, sa, ta);
+    }
+    const int rest = ntiles - i;  // 1..4 tiles left
+    if (rest >= 2) step(IC<0>{}, i, sa, ta, sb, tb);
+    if (rest >= 3) step(IC<1>{}, i + 1, sb, tb, sa, ta);
+    if (rest >= 4) step(IC<2>{}, i + 2, sa, ta, sb, tb);
+    if (rest == 1) last_step(IC<0>{}, i, sa, ta);
+    else if (rest == 2) last_step(IC<1>{}, i + 1, sb, tb);
+    else if (rest == 3) last_step(IC<2>{}, i + 2, sa, ta);
+    else last_step(IC<3>{}, i + 3, sb, tb);
+  } else {
+    // three stages: six steps per pass keep both the stage (k % 3) and the
+    // score-tile pair (k % 2) compile-time
+    for (; i + 6 < ntiles; i += 6) {
+      step(IC<0>{}, i, sa, ta, sb, tb);
+      step(IC<1>{}, i + 1, sb, tb, sa, ta);
+      step(IC<2>{}, i + 2, sa, ta, sb, tb);
+      step(IC<3>{}, i + 3, sb, tb, sa, ta);
+      step(IC<4>{}, i + 4, sa, ta, sb, tb);
+      step(IC<5>{}, i + 5, sb, tb, sa, ta);
+    }
+    const int rest = ntiles - i;  // 1..6 tiles left
+    if (rest >= 2) step(IC<0>{}, i, sa, ta, sb, tb);
+    if (rest >= 3) step(IC<1>{}, i + 1, sb, tb, sa, ta);
+    if (rest >= 4) step(IC<2>{}, i + 2, sa, ta, sb, tb);
+    if (rest >= 5) step(IC<3>{}, i + 3, sb, tb, sa, ta);
+    if (rest >= 6) step(IC<4>{}, i + 4, sa, ta, sb, tb);
+    if (rest == 1) last_step(IC<0>{}, i, sa, ta);
+    else if (rest == 2) last_step(IC<1>{}, i + 1, sb, tb);
+    else if (rest == 3) last_step(IC<2>{}, i + 2, sa, ta);
+    else if (rest == 4) last_step(IC<3>{}, i + 3, sb, tb);
+    else if (rest == 5) last_step(IC<4>{}, i + 4, sa, ta);
+    else last_step(IC<5>{}, i + 5, sb, tb);
   }
-  const int rest = ntiles - i;  // 1..4 tiles left
-  if (rest >= 2) step(IC<0>{}, i, sa, ta, sb, tb);
-  if (rest >= 3) step(IC<1>{}, i + 1, sb, tb, sa, ta);
-  if (rest >= 4) step(IC<2>{}, i + 2, sa, ta, sb, tb);
-  if (rest == 1) last_step(IC<0>{}, i, sa, ta);
-  else if (rest == 2) last_step(IC<1>{}, i + 1, sb, tb);
-  else if (rest == 3) last_step(IC<2>{}, i + 2, sa, ta);
-  else last_step(IC<3>{}, i + 3, sb, tb);
   wait_vmem();  // no requests beyond the last tile stay in flight
   if constexpr (kAccAgpr) mfma_acc_drain();
 
@@ -526,8 +626,9 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   const float inv_l = 1.0f / l;
   float mu = 0.f;
   if constexpr (C::JVP) mu = (r_i + other_half(r_i)) * inv_l;
-  const int64_t obase = b * p.o_sb + h * p.o_sh;
-  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + D) * 2);
+  // O (Od) resources start at this workgroup's column chunk
+  const int64_t obase = b * p.o_sb + h * p.o_sh + chunk * DVC;
+  const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + DVC) * 2);
   const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
   __amdgpu_buffer_rsrc_t rto = ro;
   if constexpr (C::JVP) rto = make_rsrc((char*)p.to + obase * 2, o_bytes);
@@ -535,11 +636,15 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // its last step the ring is free, and wave w stages its 32 rows in ring bytes
   // [w WST, (w + 1) WST)
   ring_sync<0>();
-  constexpr int WST = (C::JVP ? 2 : 1) * RowStage<D>::BYTES;
-  static_assert(C::STAGE % WST == 0 && C::NW * WST <= C::NSTAGE * C::STAGE, "staging fits the ring");
-  const int wst_stage = wave * WST / C::STAGE;
+  // (regions that do not pack into a stage take one stage per wave)
+  constexpr int WST = (C::JVP ? 2 : 1) * RowStage<DVC>::BYTES;
+  constexpr bool kPacked = C::STAGE % WST == 0;
+  static_assert(kPacked ? C::NW * WST <= NSTAGE * C::STAGE : WST <= C::STAGE && C::NW <= NSTAGE,
+                "staging fits the ring");
+  const int wst_stage = kPacked ? wave * WST / C::STAGE : wave;
   lds_char_t* const region = (wst_stage == 0 ? stage(IC<0>{}) : wst_stage == 1 ? stage(IC<1>{})
-                              : wst_stage == 2 ? stage(IC<2>{}) : stage(IC<3>{})) + (wave * WST) % C::STAGE;
+                              : wst_stage == 2 ? stage(IC<2>{}) : stage(IC<3>{})) +
+                             (kPacked ? (wave * WST) % C::STAGE : 0);
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -550,11 +655,12 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
         ov[e] = oacc[d][4 * jj + e] * inv_l;
         if constexpr (C::JVP) tv[e] = cacc[d][4 * jj + e] * inv_l - mu * ov[e];
       }
-      stage_put<D>(region, col, half, d, jj, u32x2_t{Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])});
+      stage_put<DVC>(region, col, half, d, jj, u32x2_t{Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])});
       if constexpr (C::JVP)
-        stage_put<D>(region + RowStage<D>::BYTES, col, half, d, jj,
+        stage_put<DVC>(region + RowStage<DVC>::BYTES, col, half, d, jj,
                      u32x2_t{Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])});
     }
+    if constexpr (C::CHUNKS > 1 && kAccAgpr) __builtin_amdgcn_sched_barrier(0);  // one block's copies at a time
   }
   // rows >= Lq fall outside the resource; MAGI stores only the group's rows
   const bool keep = !MAGI || (query >= q_lo && query < q_hi);
@@ -565,11 +671,12 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     return ok ? (uint32_t)((int64_t)qrow * p.o_sl * 2) : o_bytes;
   };
 #pragma unroll
-  for (int kk = 0; kk < RowStage<D>::NST; ++kk) {
-    stage_store<D>(region, kk, lane, ro, row_off);
-    if constexpr (C::JVP) stage_store<D>(region + RowStage<D>::BYTES, kk, lane, rto, row_off);
+  for (int kk = 0; kk < RowStage<DVC>::NST; ++kk) {
+    stage_store<DVC>(region, kk, lane, ro, row_off);
+    if constexpr (C::JVP) stage_store<DVC>(region + RowStage<DVC>::BYTES, kk, lane, rto, row_off);
   }
-  if (half == 0 && query < p.Lq && keep) {
+  // every chunk's workgroup holds the same statistics; chunk 0 stores them
+  if (half == 0 && query < p.Lq && keep && chunk == 0) {
     const int64_t si = (int64_t)bh * p.Lq + query;
     p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
     if constexpr (C::JVP) p.mu[si] = mu;

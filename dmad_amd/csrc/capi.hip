@@ -237,6 +237,11 @@ FwdPlan plan_fwd(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, 
     pl.family = FwdFamily::kRows;
     pl.kernel = "attn_fwd32_kernel";
     pl.chunks = 1;
+  } else if (!magi && dmad::fwd32_wide_supported((int)Dqk, (int)Dv)) {
+    // 256-wide heads: the same kernel; the JVP modes run one workgroup per 128-column chunk of V
+    pl.family = FwdFamily::kRows;
+    pl.kernel = "attn_fwd32_kernel";
+    pl.chunks = dmad::fwd32_chunks(mode, 256);
   } else {
     // the other head dims: generic kernels on transposed copies of V (and Vd)
     pl.family = FwdFamily::kGeneric;
@@ -248,7 +253,8 @@ FwdPlan plan_fwd(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, 
   pl.grid = units * B * H * pl.chunks;
   // block order (common.h): the block-sparse kernels always deal contiguous work items per XCD
   pl.xcd_order = magi ? 1 : units < dmad::kHeadMajorMinTiles;
-  pl.ws = pl.family == FwdFamily::kF32 ? 0 : fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv);
+  // the row-reading kernels read V in place; the generic ones need the copies
+  pl.ws = pl.family == FwdFamily::kGeneric ? fwd_ws_bytes(mode, B, H, Lk, Dqk, Dv) : 0;
   return pl;
 }
 

@@ -213,10 +213,12 @@ __device__ __forceinline__ int trswz16(int r) { return ((r & 3) << 2) | ((r >> 2
 // aligned chunks) do too. Bits: r0 ^ r2, r3, r1 (found by exhaustive search
 // against both access patterns).
 __device__ __forceinline__ int trswz8(int r) { return ((r ^ (r >> 2)) & 1) | ((r >> 2) & 2) | ((r << 1) & 4); }
+// Rows of 32 chunks (512 bytes, read row-wise only) take trswz16: a row starts
+// on a 256-byte boundary and the XOR stays inside its 16-chunk half.
 template <int CR>
 __device__ __forceinline__ int trswz(int r) {
-  static_assert(CR == 16 || CR == 8, "row tiles of 16 or 8 chunks");
-  if constexpr (CR == 16) return trswz16(r);
+  static_assert(CR == 32 || CR == 16 || CR == 8, "row tiles of 32, 16 or 8 chunks");
+  if constexpr (CR >= 16) return trswz16(r);
   else return trswz8(r);
 }
 

@@ -1,4 +1,4 @@
-// Instantiates attn_fwd32_kernel (64- and 128-wide heads) for one element type: compiled once per type
+// Instantiates attn_fwd32_kernel (64-, 128- and 256-wide heads) for one element type: compiled once per type
 // with -DDMAD_T=<0 bf16 | 1 f16> and MFMAs in VGPR form, so that the
 // accumulators and score tiles take the VGPRs and Q, Qd the AGPRs.
 #include "launch.h"
@@ -66,7 +66,7 @@ FwdLaunchFn fwd32x2_select<Elt>(int mode, int d) {
 
 template <>
 FwdLaunchFn fwd32_select<Elt>(int mode, int d) {
-  return d == 64 ? fwd32_mode<64>(mode) : d == 128 ? fwd32_mode<128>(mode) : nullptr;
+  return d == 64 ? fwd32_mode<64>(mode) : d == 128 ? fwd32_mode<128>(mode) : d == 256 ? fwd32_mode<256>(mode) : nullptr;
 }
 
 }  // namespace dmad

@@ -86,7 +86,9 @@ FwdLaunchFn fwd_select<Elt, DMAD_D>(int dv, int mode) {
     case 128:
       if constexpr (fwd32_supported(DMAD_D, 128)) return fwd32_select<Elt>(mode, 128);
       else return fwd_mode<Elt, DMAD_D, 128>(mode);
-    case 256: return fwd_mode<Elt, DMAD_D, 256>(mode);
+    case 256:
+      if constexpr (fwd32_wide_supported(DMAD_D, 256)) return fwd32_select<Elt>(mode, 256);
+      else return fwd_mode<Elt, DMAD_D, 256>(mode);
     default: return nullptr;
   }
 }

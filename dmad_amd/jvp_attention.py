@@ -130,8 +130,24 @@ def _pair(x, tx):
 
 
 def _fwd_ws_bytes(dtype, mode, B, H, Lk, Dqk, Dv) -> int:
-    """Forward workspace: transposed V copies of the bf16/fp16 kernels for some head dims; none for fp32."""
+    """Workspace of any forward entry (the block-sparse one included): transposed V copies of
+    the bf16/fp16 kernels for some head dims; none for fp32."""
     return 0 if dtype == torch.float32 else nat.fwd_workspace_bytes(mode, B, H, Lk, Dqk, Dv)
+
+
+_dense_needs_ws: dict = {}
+
+
+def _fwd_dense_ws_bytes(dtype, mode, B, H, Lk, Dqk, Dv) -> int:
+    """Workspace of the dense forward: the launch plan says whether its kernel reads V in
+    place (asked once per dtype, mode and head dims; then none is allocated)."""
+    key = (dtype, mode, Dqk, Dv)
+    need = _dense_needs_ws.get(key)
+    if need is None:
+        need = dtype != torch.float32 and \
+            nat.fwd_plan(nat.dtype_code(dtype), mode, 1, 1, 128, 128, Dqk, Dv)["workspace_bytes"] > 0
+        _dense_needs_ws[key] = need
+    return _fwd_ws_bytes(dtype, mode, B, H, Lk, Dqk, Dv) if need else 0
 
 
 def _check_device(*ts):
@@ -170,7 +186,7 @@ def jvp_attention_forward(q, k, v, tq, tk, tv, sm_scale, need_mu=True):
     lse = torch.empty((B, H, Lq), device=dev, dtype=torch.float32)
     mu = torch.empty_like(lse) if tq is not None else None
     lib = nat.lib()
-    ws_ptr, ws_size, ws = nat.workspace(_fwd_ws_bytes(q.dtype, mode, B, H, Lk, Dqk, Dv), dev)
+    ws_ptr, ws_size, ws = nat.workspace(_fwd_dense_ws_bytes(q.dtype, mode, B, H, Lk, Dqk, Dv), dev)
     nat.check(
         lib.dmad_attn_jvp_fwd(
             code, mode, B, H, Lq, Lk, Dqk, Dv,

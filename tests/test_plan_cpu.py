@@ -54,8 +54,7 @@ def test_block_order_is_keyed_on_query_tiles(L, xcd, D):
     assert (b["xcd_order"], b["xcd_order2"]) == (xcd, xcd)
 
 
-@pytest.mark.parametrize("D,kernel,chunks", [(16, "attn_fwd_simple_kernel", 1), (32, "attn_fwd_kernel", 1),
-                                             (256, "attn_fwd_simple_kernel", 2)])
+@pytest.mark.parametrize("D,kernel,chunks", [(16, "attn_fwd_simple_kernel", 1), (32, "attn_fwd_kernel", 1)])
 def test_generic_head_dims(D, kernel, chunks):
     """Head dims the row-reading kernels do not take run on transposed copies of V (and Vd)."""
     p = nat.fwd_plan(F16, JVP, 4, 32, 4096, 4096, D, D)
@@ -63,6 +62,27 @@ def test_generic_head_dims(D, kernel, chunks):
     assert p["grid"] == 32 * 128 * chunks
     assert p["workspace_bytes"] == nat.fwd_workspace_bytes(JVP, 4, 32, 4096, D, D) > 0
     assert nat.fwd_plan(F16, PLAIN, 4, 32, 4096, 4096, D, D)["transposed_copies"] == 1
+
+
+@pytest.mark.parametrize("mode", [PLAIN, JVP, QONLY])
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_wide_heads_on_the_row_kernel(mode, dt):
+    """Dense 256-wide heads: the row-reading kernel (JVP modes: one workgroup per 128-column
+    chunk of V), V read in place (no workspace, though the workspace query still sizes the copies the
+    block-sparse forward needs at this head dim)."""
+    p = nat.fwd_plan(dt, mode, 4, 32, 4096, 4096, 256, 256)
+    chunks = 1 if mode == PLAIN else 2  # the plain forward keeps all 256 columns in one workgroup
+    assert (p["kernel"], p["chunks"], p["transposed_copies"], p["workspace_bytes"]) == \
+        ("attn_fwd32_kernel", chunks, 0, 0)
+    assert p["grid"] == (4096 // 128) * 4 * 32 * chunks  # query tiles x B x H x chunks
+    assert nat.fwd_workspace_bytes(mode, 4, 32, 4096, 256, 256) > 0
+    if mode != PLAIN:
+        pm = nat.fwd_plan(dt, mode, 1, 2, 1000, 1000, 256, 256, magi_tasks=20)
+        assert (pm["kernel"], pm["transposed_copies"]) == ("attn_fwd_simple_kernel", 2 if mode == JVP else 1)
+        assert pm["workspace_bytes"] == nat.fwd_workspace_bytes(mode, 1, 2, 1000, 256, 256) > 0
+    # mixed widths stay on the generic kernels
+    assert nat.fwd_plan(dt, mode, 1, 2, 1000, 1000, 128, 256)["kernel"] != "attn_fwd32_kernel"
+    assert nat.fwd_plan(dt, mode, 1, 2, 1000, 1000, 256, 128)["kernel"] != "attn_fwd32_kernel"
 
 
 def test_mixed_head_dims():
@@ -123,8 +143,9 @@ def test_backward_passes():
 @pytest.mark.parametrize("Lq,Lk", [(999, 515), (32760, 512), (1, 1)])
 def test_workspace_matches_the_queries(D, Lq, Lk):
     for mode in (PLAIN, JVP, QONLY):
-        assert nat.fwd_plan(BF16, mode, 2, 3, Lq, Lk, D, D)["workspace_bytes"] == \
-            nat.fwd_workspace_bytes(mode, 2, 3, Lk, D, D)
+        # the query covers every forward entry; the dense row kernel at D = 256 needs none of it
+        want = 0 if D == 256 else nat.fwd_workspace_bytes(mode, 2, 3, Lk, D, D)
+        assert nat.fwd_plan(BF16, mode, 2, 3, Lq, Lk, D, D)["workspace_bytes"] == want
     fulls = ((0, False), (1, False), (2, True)) if D <= 128 else ((0, False),)
     for full, tg in fulls:
         assert nat.bwd_plan(BF16, 2, 3, Lq, Lk, D, full=full > 0, tangent_grads=tg)["workspace_bytes"] == \
