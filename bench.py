@@ -527,7 +527,8 @@ def main():
         out["magi_fwd_jvp"] = magi_timing(H, D, dev)
     if args.harness:
         out["reference_harness"] = [harness_timing(dev, D=d) for d in (64, 128)]
-        # the head dims the reference also accepts (:471-472), on the generic kernels
+        # the other head dims the reference accepts (:471-472): 16 and 32 on the generic kernels, 256 on the
+        # row-reading forward and the generic backward
         out["other_head_dims"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384)) for d in (16, 32, 256)]
         out["fp32_harness"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384), dtype=torch.float32)
                                for d in (64, 128)]
