@@ -144,3 +144,50 @@ def test_wide_rescale_at_every_step(gpu, dtype, mode):
     assert float((lse.double() - rlse).abs().max()) <= 2e-3 * max(1.0, float(rlse.abs().max()))
     # the logits really did rise across the tiles
     assert float(rlse.mean()) > rise * (Lk // 32 - 2) / 1.4426950408889634 / 2
+
+
+def _oracle_head(q, k, v, tq, tk, tv, h, s, chunk=2048):
+    """Oracle (O, Od, LSE, mu) of head h, float32 on the device, chunked over query rows (rows are independent)."""
+    f = lambda x: x[0, h].float().contiguous()  # noqa: E731
+    kh, vh = f(k), f(v)
+    tkh = torch.zeros_like(kh) if tk is None else f(tk)
+    tvh = torch.zeros_like(vh) if tv is None else f(tv)
+    qh, tqh = f(q), f(tq)
+    outs = [[], [], [], []]
+    for c in range(0, qh.shape[0], chunk):
+        for o, r in zip(outs, orc.jvp_closed_form(qh[c:c + chunk], kh, vh, tqh[c:c + chunk], tkh, tvh, sm_scale=s)):
+            o.append(r)
+    return [torch.cat(o, 0) for o in outs]
+
+
+@pytest.mark.parametrize("H,L,mode", [(3, 16384, "jvp"), (1, 32768, "jvp"), (2, 16384, "qonly")])
+def test_wide_row_kernel_long_sequences(gpu, H, L, mode):
+    """128 query tiles per head (work items dealt contiguously per XCD) and 256 (head-major order):
+    every row of two heads against the oracle in float32 on the GPU, sampled rows against float64."""
+    from dmad_amd.jvp_attention import jvp_attention_forward
+
+    print(f"case D=256 long H={H} L={L} {mode}", flush=True)
+    dtype = torch.bfloat16
+    g = torch.Generator(device=gpu).manual_seed(L + H)
+    r = lambda std: (torch.randn((1, H, L, D), device=gpu, generator=g) * std).to(dtype)  # noqa: E731
+    q, k, v, tq = r(1.0), r(1.0), r(1.0), r(0.1)
+    tk, tv = (r(0.1), r(0.1)) if mode == "jvp" else (None, None)
+    s = D ** -0.5
+    o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+    torch.cuda.synchronize()
+    for h in sorted({0, H - 1}):
+        ro, rto, rlse, rmu = _oracle_head(q, k, v, tq, tk, tv, h, s)
+        e_o, e_to, e_mu = orc.rel_l2(o[0, h], ro), orc.rel_l2(to[0, h], rto), orc.rel_l2(mu[0, h], rmu)
+        dl = float((lse[0, h] - rlse).abs().max())
+        print(f"  head {h}: rel-L2 O {e_o:.2e} Od {e_to:.2e} mu {e_mu:.2e} max|dLSE| {dl:.2e}", flush=True)
+        assert max(e_o, e_to, e_mu) <= 1e-2 and dl <= 2e-3
+    rows = torch.tensor([0, 1, 127, 128, L // 2, L - 129, L - 1], device=gpu)
+    h = H - 1
+    sub = lambda x: None if x is None else x[:, h:h + 1].cpu()  # noqa: E731
+    qs, tqs = q[:, h:h + 1, rows].cpu(), tq[:, h:h + 1, rows].cpu()
+    kh, vh, tkh, tvh = sub(k), sub(v), sub(tk), sub(tv)
+    tkh = torch.zeros_like(kh) if tkh is None else tkh
+    tvh = torch.zeros_like(vh) if tvh is None else tvh
+    ref_o, ref_to, _, _ = orc.jvp_closed_form(*(x.double() for x in (qs, kh, vh, tqs, tkh, tvh)), sm_scale=s)
+    assert orc.rel_l2(o[:, h:h + 1, rows].cpu(), ref_o) <= 1e-2
+    assert orc.rel_l2(to[:, h:h + 1, rows].cpu(), ref_to) <= 1e-2
