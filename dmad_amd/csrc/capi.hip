@@ -136,7 +136,9 @@ dmad::F32BwdFns pick_bwd_f32(int64_t d) {
 }
 
 // Bytes of the transposed, key-padded V (and Vd) copies the generic forward
-// kernels read; the kernels for 64- and 128-wide heads read V in place.
+// kernels read; the kernels for 64- and 128-wide heads read V in place. At
+// 256 the dense forward reads it in place too, the block-sparse one does not:
+// this is the bound over both (plan_fwd gives one launch's size).
 int64_t fwd_ws_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv) {
   if (dmad::fwd32_supported((int)Dqk, (int)Dv)) return 0;
   const int64_t dvp = Dv < 32 ? 32 : Dv;
@@ -443,8 +445,8 @@ int fwd_impl(int dtype, int mode, int64_t B, int64_t H, int64_t Lq, int64_t Lk, 
   const int BH = (int)(B * H);
   char* ws = (char*)workspace;
   const int64_t vt_bytes = round_up(B * H * dvp * lkp * 2, 256);
-  // kernels for 64- and 128-wide heads transpose V on the LDS read; the others
-  // read a transposed, key-padded copy made here
+  // the row-reading kernels transpose V on the LDS read; the others read a
+  // transposed, key-padded copy made here
   const bool need_vt = plan.copies > 0;
   hipError_t e = hipSuccess;
   dmad::TransposeParams tp{v, ws, v_strides[0], v_strides[1], v_strides[2], (int)H, (int)Lk, (int)Dv, (int)lkp, (int)dvp};
