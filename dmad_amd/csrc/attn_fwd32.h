@@ -363,7 +363,10 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // accumulators stay in AGPRs through inline MFMAs, which frees the VGPRs for
   // the score tiles and the softmax (0.6-1% faster). Measured slower for the
   // block-sparse variant (3%) and for fp16 (6%: 59.8 against 56.3 ms at the
-  // Wan2.1-14B shape); the plain forward keeps them in VGPRs, where it fits two
+  // Wan2.1-14B shape; still 8% with the rescale done block by block and no
+  // spills: 51.5 against 47.5 ms at B=4, H=32, L=16384 -- fp16 MFMAs writing
+  // AGPRs cost more than the copies they save); 256-wide heads need them for
+  // every type. The plain forward keeps them in VGPRs, where it fits two
   // waves per SIMD. Code that touches AGPR accumulators with the VALU (the
   // rescale, the epilogue) waits for the MFMAs first.
   constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI && ((DH == 128 && !__is_same(T, _Float16)) || DH == 256);
@@ -440,9 +443,10 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     }
   };
   auto rescale = [&](float alpha) {
-    if constexpr (C::CHUNKS > 1 && kAccAgpr) {
-      // 256-wide heads (all AGPRs taken): one 16-value block at a time, so the
-      // copies through VGPRs need 16 of them rather than all 128
+    if constexpr (kAccAgpr) {
+      // one 16-value block at a time, so the copies through VGPRs need 16 of
+      // them rather than all 128 (which spilled: 256-wide heads leave no AGPR
+      // free; 128-wide ones spilled 5 registers and ran 0.3% slower)
 #pragma unroll
       for (int d = 0; d < 2 * DB; ++d) {
         f32x16_t& a = d < DB ? oacc[d] : cacc[d - DB];
@@ -660,7 +664,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
         stage_put<DVC>(region + RowStage<DVC>::BYTES, col, half, d, jj,
                      u32x2_t{Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])});
     }
-    if constexpr (C::CHUNKS > 1 && kAccAgpr) __builtin_amdgcn_sched_barrier(0);  // one block's copies at a time
+    if constexpr (kAccAgpr) __builtin_amdgcn_sched_barrier(0);  // one block's copies at a time
   }
   // rows >= Lq fall outside the resource; MAGI stores only the group's rows
   const bool keep = !MAGI || (query >= q_lo && query < q_hi);
