@@ -537,10 +537,13 @@ struct DqTrCfg {
   static constexpr int NSTAGE = 4;
   static constexpr int NRI = BN * CR / 64;
   static constexpr int RPW = NRI / NW;
-  static constexpr bool FITS = (D == 128 || D == 64) && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
+  static constexpr bool FITS = (D == 128 || D == 64 || D == 256) && NRI % NW == 0 && NSTAGE * STAGE <= 160 * 1024;
   static constexpr int LOADS = 2 * RPW;
 };
 
+// D = 256: 512-byte K, V rows (32 KiB stages, one workgroup per CU), Q and dO
+// held in AGPRs (the dQ accumulators and score tiles take the VGPRs), one
+// K-slice offset kept (slice s at sx ^ 32 s).
 // D = 64 fits three waves per SIMD (168 VGPRs, 32 KiB of LDS per workgroup):
 // the third wave hides more of the 6 VALU instructions per MFMA (1% faster at
 // B=4, H=32, L=16384 than two waves at 172 VGPRs, with bitwise equal dQ).
@@ -579,6 +582,10 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void attn_bwd_dq_tr_kernel(Dq
       qreg[s] = buf_load16(rq, qo + s * 32);
       doreg[s] = buf_load16(rdo, oo + s * 32);
     }
+  }
+  if constexpr (D == 256) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) asm volatile("" : "+a"(qreg[s]), "+a"(doreg[s]));
   }
   float lse2 = __builtin_inff(), dlt = 0.f;
   if (query < p.LQP) {
@@ -623,12 +630,17 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void attn_bwd_dq_tr_kernel(Dq
 
   // ---- LDS read offsets: row-wise (K, V row perm32(col), chunk 2s + half) and
   // transposed (K^T block db, keys 16 t + 8 (g >> 1) + (0..3 | 4..7))
-  int sx[KS];
+  constexpr int NSX = D == 256 ? 1 : KS;
+  int sx[NSX];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
+  for (int s = 0; s < NSX; ++s) {
     const int r = perm32(col);
     sx[s] = r * ROWB + (((2 * s + half) ^ trswz<CR>(r & 15)) << 4);
   }
+  auto sxo = [&](int s) -> int {
+    if constexpr (NSX == 1) return sx[0] ^ (32 * s);
+    else return sx[s];
+  };
   int tx[DB][2];
   {
     const int g = lane >> 4, r = (lane & 15) >> 2, c = lane & 3;
@@ -644,7 +656,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void attn_bwd_dq_tr_kernel(Dq
   }
   auto pin_offsets = [&]() {
 #pragma unroll
-    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(sx[s]));
+    for (int s = 0; s < NSX; ++s) asm volatile("" : "+v"(sx[s]));
 #pragma unroll
     for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(tx[db][0]), "+v"(tx[db][1]));
   };
@@ -665,7 +677,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 1) void attn_bwd_dq_tr_kernel(Dq
   static_assert(VPS * NMA >= NVAL && VPS <= 2, "values ride in the score slots");
   const f32x16_t zero16 = {};
   auto load_op = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int m) -> i32x4_t {
-    if (m < NMA) return *(lds_i32x4_t*)(s_next + ((m & 1) ? C::OFF_V : C::OFF_K) + sx[m >> 1]);
+    if (m < NMA) return *(lds_i32x4_t*)(s_next + ((m & 1) ? C::OFF_V : C::OFF_K) + sxo(m >> 1));
     const int mm = m - NMA, t = mm / DB, db = mm % DB;
     const lds_char_t* base = s_cur + C::OFF_K + t * 16 * ROWB;
     const u32x2_t lo = lds_read_tr16(base + tx[db][0]);

@@ -1,8 +1,9 @@
-// Instantiates the dO-only dQ pass for 64- and 128-wide heads (attn_bwd_dq_tr_kernel)
-// for one element type (-DDMAD_T=<0 bf16 | 1 f16>). This unit is compiled with
-// MFMAs in VGPR form: the kernel then fits 256 VGPRs with no AGPRs, the score
-// tiles need no AGPR->VGPR copies before the softmax, and two workgroups share
-// a CU (64 KiB of LDS each).
+// Instantiates the dO-only dQ pass for 64-, 128- and 256-wide heads
+// (attn_bwd_dq_tr_kernel) for one element type (-DDMAD_T=<0 bf16 | 1 f16>). This
+// unit is compiled with MFMAs in VGPR form: at D = 128 the kernel then fits 256
+// VGPRs with no AGPRs, the score tiles need no AGPR->VGPR copies before the
+// softmax, and two workgroups share a CU (64 KiB of LDS each); D = 256 keeps Q
+// and dO in AGPRs, one workgroup per CU.
 #include "launch.h"
 
 #ifndef DMAD_T
@@ -30,6 +31,10 @@ DqLaunchFn dq_tr_select<Elt, 64>() {
 template <>
 DqLaunchFn dq_tr_select<Elt, 128>() {
   return &dq_tr_launch<Elt, 128>;
+}
+template <>
+DqLaunchFn dq_tr_select<Elt, 256>() {
+  return &dq_tr_launch<Elt, 256>;
 }
 
 }  // namespace dmad

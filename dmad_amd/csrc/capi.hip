@@ -337,9 +337,15 @@ BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) 
   BwdWs w{};
   // transposed copies of Q, dO (and Qd, dOd) and K (and Kd): the full derivative
   // and the dO-only passes of the head dims whose kernels read transposed copies
-  const bool copies = full != 0 ? !dmad::full_reads_rows((int)D) : !dmad::dout_only_reads_rows((int)D);
-  w.nq = copies ? (full ? 4 : 2) : 0;
-  w.nk = copies ? (full ? 2 : 1) : 0;
+  // (Q, dO for the dK/dV pass, K for the dQ pass)
+  if (full != 0) {
+    const bool copies = !dmad::full_reads_rows((int)D);
+    w.nq = copies ? 4 : 0;
+    w.nk = copies ? 2 : 0;
+  } else {
+    w.nq = dmad::kv_dout_only_reads_rows((int)D) ? 0 : 2;
+    w.nk = dmad::dq_dout_only_reads_rows((int)D) ? 0 : 1;
+  }
   w.tgrad = full == 2;
   w.trq = round_up(BH * dp * lqp * 2, 256);
   w.trk = round_up(BH * dp * lkp * 2, 256);
@@ -694,8 +700,9 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   // ones of some head dims, read transposed copies of Q, dO (and Qd, dOd) and K
   // (and Kd)
   const bool need_tr = w.nq > 0;
-  if (need_tr && ((e = tr(q, q_strides, trq, Lq, lqp)) != hipSuccess ||
-                  (e = tr(dout, do_strides, trdo, Lq, lqp)) != hipSuccess || (e = tr(k, k_strides, trk, Lk, lkp)) != hipSuccess))
+  if (need_tr && ((e = tr(q, q_strides, trq, Lq, lqp)) != hipSuccess || (e = tr(dout, do_strides, trdo, Lq, lqp)) != hipSuccess))
+    return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
+  if (w.nk > 0 && (e = tr(k, k_strides, trk, Lk, lkp)) != hipSuccess)
     return fail(DMAD_ERR_HIP, "transpose launch: %s", hipGetErrorString(e));
   if (need_tr && full && ((e = tr(tq, q_strides, trtq, Lq, lqp)) != hipSuccess || (e = tr(dto, do_strides, trdto, Lq, lqp)) != hipSuccess ||
                (e = tr(tk, k_strides, trtk, Lk, lkp)) != hipSuccess))

@@ -75,13 +75,15 @@ template <> BwdLaunchFn kv_tr_select<__bf16, 128>();
 template <> BwdLaunchFn kv_tr_select<_Float16, 64>();
 template <> BwdLaunchFn kv_tr_select<_Float16, 128>();
 
-// Launcher for the dO-only attn_bwd_dq_tr_kernel<T, D>, D = 64 or 128 (bwd_dq_inst.hip).
+// Launcher for the dO-only attn_bwd_dq_tr_kernel<T, D>, D = 64, 128 or 256 (bwd_dq_inst.hip).
 template <typename T, int D>
 DqLaunchFn dq_tr_select();
 template <> DqLaunchFn dq_tr_select<__bf16, 64>();
 template <> DqLaunchFn dq_tr_select<__bf16, 128>();
 template <> DqLaunchFn dq_tr_select<_Float16, 64>();
 template <> DqLaunchFn dq_tr_select<_Float16, 128>();
+template <> DqLaunchFn dq_tr_select<__bf16, 256>();
+template <> DqLaunchFn dq_tr_select<_Float16, 256>();
 
 // Full-derivative passes for 128-wide heads (bwd_full_inst.hip): the key pass
 // (dK, dV) and the query pass (dQ, and dQd when tangent_grads).
@@ -109,15 +111,25 @@ inline int bwd_bmq(int d, int mode) {
   }
 }
 
-// True when the dO-only backward kernels for head dim d read Q, dO and K
-// row-major (transposing on the LDS read), so they need no transposed copies.
-inline bool dout_only_reads_rows(int d) {
+// True when the dO-only dK/dV pass for head dim d reads Q, dO row-major
+// (transposing on the LDS read), so it needs no transposed copies of them.
+inline bool kv_dout_only_reads_rows(int d) {
   switch (d) {
-    case 16: return KvTrCfg<16, kKvTrBmq>::FITS && DqTrCfg<16>::FITS;
-    case 32: return KvTrCfg<32, kKvTrBmq>::FITS && DqTrCfg<32>::FITS;
-    case 64: return KvTrCfg<64, kKvTrBmq>::FITS && DqTrCfg<64>::FITS;
-    case 128: return KvTrCfg<128, kKvTrBmq>::FITS && DqTrCfg<128>::FITS;
-    default: return KvTrCfg<256, kKvTrBmq>::FITS && DqTrCfg<256>::FITS;
+    case 16: return KvTrCfg<16, kKvTrBmq>::FITS;
+    case 32: return KvTrCfg<32, kKvTrBmq>::FITS;
+    case 64: return KvTrCfg<64, kKvTrBmq>::FITS;
+    case 128: return KvTrCfg<128, kKvTrBmq>::FITS;
+    default: return KvTrCfg<256, kKvTrBmq>::FITS;
+  }
+}
+// The same for the dQ pass and K.
+inline bool dq_dout_only_reads_rows(int d) {
+  switch (d) {
+    case 16: return DqTrCfg<16>::FITS;
+    case 32: return DqTrCfg<32>::FITS;
+    case 64: return DqTrCfg<64>::FITS;
+    case 128: return DqTrCfg<128>::FITS;
+    default: return DqTrCfg<256>::FITS;
   }
 }
 
