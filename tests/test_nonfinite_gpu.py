@@ -13,7 +13,8 @@ poisoned element in sample 1, head 0:
     scores drop the key), dQ, dK, dV are non-finite at least there, and where
     both are finite they agree to the usual rel-L2 <= 1e-2;
   * a poisoned tangent leaves O, LSE and the dO-only gradients bitwise unchanged.
-bf16 on the 128- and 64-wide kernels, fp32 on the fp32 kernels.
+bf16 on the 128-, 64- and 256-wide kernels (at 256: two forward workgroups per query tile, one
+per 128-column chunk of V), fp32 on the fp32 kernels.
 """
 import math
 
@@ -62,8 +63,8 @@ def _poison(x, where, val):
     return y
 
 
-@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.bfloat16), (128, torch.float32),
-                                     (32, torch.float32)])
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.bfloat16), (256, torch.bfloat16),
+                                     (128, torch.float32), (32, torch.float32)])
 @pytest.mark.parametrize("where", ["q", "k", "v", "tq"])
 @pytest.mark.parametrize("val", [math.nan, math.inf])
 def test_nonfinite_input_stays_in_its_slice(gpu, D, dtype, where, val):
