@@ -359,17 +359,18 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     }
   }
   const f32x16_t zero16 = {};
-  // O~, C~ accumulation. In the dense bf16 JVP mode for 128-wide heads the
-  // accumulators stay in AGPRs through inline MFMAs, which frees the VGPRs for
-  // the score tiles and the softmax (0.6-1% faster). Measured slower for the
-  // block-sparse variant (3%) and for fp16 (6%: 59.8 against 56.3 ms at the
-  // Wan2.1-14B shape; still 8% with the rescale done block by block and no
-  // spills: 51.5 against 47.5 ms at B=4, H=32, L=16384 -- fp16 MFMAs writing
-  // AGPRs cost more than the copies they save); 256-wide heads need them for
-  // every type. The plain forward keeps them in VGPRs, where it fits two
-  // waves per SIMD. Code that touches AGPR accumulators with the VALU (the
+  // O~, C~ accumulation. In the bf16 JVP mode for 128-wide heads (dense and
+  // block-sparse) the accumulators stay in AGPRs through inline MFMAs, which
+  // frees the VGPRs for the score tiles and the softmax (0.6-1% faster dense,
+  // 0.4-0.6% block-sparse, once the rescale went block by block; before, the
+  // block-sparse kernel spilled and ran 3% slower). Measured slower for fp16
+  // (6%: 59.8 against 56.3 ms at the Wan2.1-14B shape; still 8% with the
+  // rescale done block by block and no spills: 51.5 against 47.5 ms at B=4,
+  // H=32, L=16384 -- fp16 MFMAs writing AGPRs cost more than the copies they
+  // save); 256-wide heads need them for every type. The plain forward keeps
+  // them in VGPRs, where it fits two waves per SIMD. Code that touches AGPR accumulators with the VALU (the
   // rescale, the epilogue) waits for the MFMAs first.
-  constexpr bool kAccAgpr = MODE == kFwdJvp && !MAGI && ((DH == 128 && !__is_same(T, _Float16)) || DH == 256);
+  constexpr bool kAccAgpr = MODE == kFwdJvp && ((DH == 128 && !__is_same(T, _Float16)) || DH == 256);
   auto acc_mfma = [&](f32x16_t& c, i32x4_t a, i32x4_t b) {
     if constexpr (kAccAgpr) mfma32_acc(c, a, b, T());
     else c = mfma32(a, b, c, T());
