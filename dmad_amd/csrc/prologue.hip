@@ -17,9 +17,12 @@
 // row, so every load and store instruction moves whole 1 KiB row segments.
 // Chunk c sits at position c mod (D/8) inside its head. When D/8 divides 64
 // (D = 8, 16, 32, 64, 128, 256, 512) that position is the same for all of a
-// lane's chunks, so each lane computes the sine and cosine of its 4 angles
-// once per row; for other head dims (D = 24, 40, 96, ...) the angles are
-// recomputed per chunk. HBM-bound: per row 2C (or 4C with the tangent) bytes
+// lane's chunks, so the sine and cosine of its 4 angles are computed once per
+// row; where 4 or more lanes share a position (D <= 128) each of them computes
+// one of the 4 and takes the others by cross-lane reads (sincosf takes its
+// full range reduction at RoPE's large angles: 4-5% of the kernel at the 14B
+// shape). For other head dims (D = 24, 40, 96, ...) the angles are recomputed
+// per chunk. HBM-bound: per row 2C (or 4C with the tangent) bytes
 // in and out, the weight and angles from cache.
 #include "launch.h"
 
@@ -83,7 +86,21 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(PrologueParams p) {
   };
   if constexpr (ROPE) {
     frow = p.freqs + (int64_t)(row % p.L) * (p.D >> 1);
-    angles(lane);
+    if (same_pos && cpd <= 16) {
+      // the 64 / cpd >= 4 lanes at one in-head position share its 4 angles:
+      // lane computes angle (lane / cpd) % 4 and takes the others from the
+      // lanes p + cpd k that computed them (same values, a quarter of the work)
+      const int pos = lane % cpd, own = (lane / cpd) & 3;
+      float s0, c0;
+      sincosf(frow[4 * pos + own], &s0, &c0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        sn[k] = __shfl(s0, pos + cpd * k);
+        cs[k] = __shfl(c0, pos + cpd * k);
+      }
+    } else {
+      angles(lane);
+    }
   }
 
   char* orow = (char*)p.out + row * p.o_stride * 2;
