@@ -64,7 +64,8 @@ struct F32FwdCfg {
   static constexpr int BM = 16 * NW;
   static constexpr int BN = 32;
   static constexpr int NB = BN / 16;
-  static constexpr int DVC = DV < (DQK > 128 ? 64 : 128) ? DV : (DQK > 128 ? 64 : 128);  // V columns per workgroup
+  static constexpr int DVW = DQK > 128 && MODE != kFwdPlain ? 64 : 128;  // widest V chunk that fits
+  static constexpr int DVC = DV < DVW ? DV : DVW;  // V columns per workgroup
   static constexpr int NCH = DV / DVC;             // workgroups per query tile
   static constexpr int KT = DQK / 16;              // 16-wide d chunks of the scores
   static constexpr int DB = DVC / 16;              // 16-row blocks of O^T

@@ -228,7 +228,7 @@ FwdPlan plan_fwd(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, 
     // fp32 operands: fp32-MFMA kernels, V in column chunks for wide heads
     pl.family = FwdFamily::kF32;
     pl.kernel = "attn_f32_fwd_kernel";
-    pl.chunks = dmad::f32_fwd_chunks((int)Dqk, (int)Dv);
+    pl.chunks = dmad::f32_fwd_chunks(mode, (int)Dqk, (int)Dv);
   } else if (!magi && dmad::fwd32x2_supported(mode, (int)Dqk, (int)Dv) && (Lk + 31) / 32 <= kX2MaxKeyTiles) {
     // short key sequences with Kd = Vd = 0 (the text cross-attention): two workgroups per CU
     pl.family = FwdFamily::kRowsX2;

@@ -9,9 +9,12 @@
 namespace dmad {
 
 static_assert(F32FwdCfg<DMAD_D, 16, kFwdJvp>::BM == kMagiBlockM, "block-sparse tasks are 128-query tiles");
-static_assert(F32FwdCfg<DMAD_D, 256, kFwdJvp>::NCH == f32_fwd_chunks(DMAD_D, 256) &&
-                  F32FwdCfg<DMAD_D, 128, kFwdJvp>::NCH == f32_fwd_chunks(DMAD_D, 128) &&
-                  F32FwdCfg<DMAD_D, 64, kFwdJvp>::NCH == f32_fwd_chunks(DMAD_D, 64),
+static_assert(F32FwdCfg<DMAD_D, 256, kFwdJvp>::NCH == f32_fwd_chunks(kFwdJvp, DMAD_D, 256) &&
+                  F32FwdCfg<DMAD_D, 128, kFwdJvp>::NCH == f32_fwd_chunks(kFwdJvp, DMAD_D, 128) &&
+                  F32FwdCfg<DMAD_D, 64, kFwdJvp>::NCH == f32_fwd_chunks(kFwdJvp, DMAD_D, 64) &&
+                  F32FwdCfg<DMAD_D, 256, kFwdJvpQOnly>::NCH == f32_fwd_chunks(kFwdJvpQOnly, DMAD_D, 256) &&
+                  F32FwdCfg<DMAD_D, 256, kFwdPlain>::NCH == f32_fwd_chunks(kFwdPlain, DMAD_D, 256) &&
+                  F32FwdCfg<DMAD_D, 128, kFwdPlain>::NCH == f32_fwd_chunks(kFwdPlain, DMAD_D, 128),
               "the launcher's grid matches the kernel's column chunks");
 
 template <int DQK, int DV, int MODE, bool MAGI>

@@ -107,6 +107,8 @@ def test_fp32_forward(Dqk, Dv, chunks):
     p = nat.fwd_plan(F32, JVP, 4, 32, 4096, 4096, Dqk, Dv)
     assert (p["kernel"], p["chunks"], p["grid"], p["transposed_copies"], p["workspace_bytes"]) == \
         ("attn_f32_fwd_kernel", chunks, 32 * 128 * chunks, 0, 0)
+    # the plain forward takes 128 V columns per workgroup at every Q, K width
+    assert nat.fwd_plan(F32, PLAIN, 4, 32, 4096, 4096, Dqk, Dv)["chunks"] == max(1, Dv // 128)
 
 
 def test_backward_passes():
