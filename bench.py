@@ -91,6 +91,8 @@ def _args():
     ap.add_argument("--harness", action="store_true",
                     help="also time the reference perf harness configuration (B=4, H=32, D=64 and 128, fp16), "
                          "and the same at head dims 16, 32 and 256")
+    ap.add_argument("--harness-dims", default="16,32,64,128,256",
+                    help="head dims the --harness timing covers (comma-separated; default all five)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one elementwise kernel that reads and writes this many MiB "
                          "(a known-size reference for HBM byte counters under a profiler)")
@@ -526,12 +528,14 @@ def main():
     if args.magi:
         out["magi_fwd_jvp"] = magi_timing(H, D, dev)
     if args.harness:
-        out["reference_harness"] = [harness_timing(dev, D=d) for d in (64, 128)]
+        dims = {int(d) for d in args.harness_dims.split(",") if d}
+        out["reference_harness"] = [harness_timing(dev, D=d) for d in (64, 128) if d in dims]
         # the other head dims the reference accepts (:471-472): 16 and 32 on the generic kernels, 256 on the
-        # row-reading forward and the generic backward
-        out["other_head_dims"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384)) for d in (16, 32, 256)]
+        # row-reading forward, the generic dK/dV pass and the row-reading dQ pass
+        out["other_head_dims"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384)) for d in (16, 32, 256)
+                                  if d in dims]
         out["fp32_harness"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384), dtype=torch.float32)
-                               for d in (64, 128)]
+                               for d in (64, 128) if d in dims]
     if args.calibration_copy_mib:
         n = args.calibration_copy_mib * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)
