@@ -62,9 +62,9 @@ def units():
         out.append(("bwd_kv_inst.hip", f"bwd_kv_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
         out.append(("bwd_full_inst.hip", f"bwd_full_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
         for d in HEAD_DIMS:
-            out.append(("fwd_inst.hip", f"fwd_{tname}_d{d}", [f"-DDMAD_T={t}", f"-DDMAD_D={d}"]))
+            out.append(("fwd_inst.hip", f"fwd_{tname}_d{d}", [f"-DDMAD_T={t}", f"-DDMAD_D={d}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
             if os.path.exists(os.path.join(CSRC, "bwd_inst.hip")):
-                out.append(("bwd_inst.hip", f"bwd_{tname}_d{d}", [f"-DDMAD_T={t}", f"-DDMAD_D={d}"]))
+                out.append(("bwd_inst.hip", f"bwd_{tname}_d{d}", [f"-DDMAD_T={t}", f"-DDMAD_D={d}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
     for d in HEAD_DIMS:
         out.append(("f32_inst.hip", f"f32_d{d}", [f"-DDMAD_D={d}"]))
     return out

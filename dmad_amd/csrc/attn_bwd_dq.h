@@ -227,8 +227,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(DqParams p) {
       }
     }
 
+    // ---- the last tile may hold keys >= Lk: their scores -> -inf (P = 0)
+    if ((kt + 1) * BN > p.Lk) {
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          if (kt * BN + kb * 32 + 16 * (v >> 3) + 8 * half + (v & 7) >= p.Lk) sacc[kb][v] = -__builtin_inff();
+        }
+      }
+    }
+
     // ---- dS (and dSd); value v of block kb is key kt*BN + kb*32 + 16t + 8*half + e (v = 8t + e)
-    const bool tail = (kt + 1) * BN > p.Lk;
     i32x4_t dsb[NB][2], tdsb[NB][2];
 #pragma unroll
     for (int kb = 0; kb < NB; ++kb) {
@@ -238,8 +248,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(DqParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int v = 8 * t + e;
-          float pe = fast_exp2(fmaf(sacc[kb][v], p.scale_log2, -lse2));
-          if (tail && kt * BN + kb * 32 + 16 * t + 8 * half + e >= p.Lk) pe = 0.f;
+          const float pe = fast_exp2(fmaf(sacc[kb][v], p.scale_log2, -lse2));
           if constexpr (!FULL) {
             dsv[e] = pe * (dpacc[kb][v] - dlt);
           } else {

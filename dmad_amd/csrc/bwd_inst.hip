@@ -1,5 +1,7 @@
 // Instantiates the backward kernels for one (element type, head dim) pair:
-// compiled once per pair with -DDMAD_T=<0 bf16 | 1 f16> -DDMAD_D=<D>.
+// compiled once per pair with -DDMAD_T=<0 bf16 | 1 f16> -DDMAD_D=<D> and
+// MFMAs in VGPR form (the score tiles feed P, dS on the VALU with no copies out
+// of AGPRs).
 #include "launch.h"
 
 #ifndef DMAD_T

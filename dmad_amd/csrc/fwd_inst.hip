@@ -1,5 +1,7 @@
 // Instantiates the forward kernels for one (element type, Dqk) pair:
-// compiled once per pair with -DDMAD_T=<0 bf16 | 1 f16> -DDMAD_D=<Dqk>.
+// compiled once per pair with -DDMAD_T=<0 bf16 | 1 f16> -DDMAD_D=<Dqk> and
+// MFMAs in VGPR form (their results feed the softmax's VALU work directly,
+// with no copies out of AGPRs).
 #include "launch.h"
 
 #ifndef DMAD_T
