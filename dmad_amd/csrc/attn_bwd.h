@@ -390,16 +390,25 @@ struct KvPipeCfg {
   static constexpr int NRI = BMQ * CR / 64;  // wave-wide 1 KiB loads per row tile
   static constexpr int NTI = D * CT / 64;    // ... per transposed tile
   static constexpr int ST_LANES = STAT_BYTES / 16 / NW;  // lanes per wave loading statistics
-  // every wave issues the same number of loads per tile (counted waits)
-  static constexpr bool FITS = D >= 32 && D <= 128 && NRI % NW == 0 && NTI % NW == 0 &&
+  // Requests per tile: the Q and dO row tiles (2 NRI), the Q^T and dO^T tiles
+  // (2 NTI) and one for the statistics. A wave's k-th row request is request
+  // (wave + NW k) of the row tiles taken together, so that every wave issues
+  // the same number of loads per tile (counted waits) also when a tile has
+  // fewer requests than there are waves.
+  static constexpr int RLOADS = 2 * NRI / NW;  // row requests per wave per tile
+  static constexpr int TLOADS = 2 * NTI / NW;  // transposed-tile requests per wave per tile
+  static constexpr bool FITS = D >= 32 && D <= 128 && 2 * NRI % NW == 0 && 2 * NTI % NW == 0 &&
                                NSTAGE * STAGE <= 160 * 1024;
-  static constexpr int LOADS = 2 * (NRI / NW) + 2 * (NTI / NW) + 1;  // per wave per tile
+  static constexpr int LOADS = RLOADS + TLOADS + 1;  // per wave per tile
 };
 
 // Query tile used by the dO-only dK/dV kernel for head dim D (the layout of the
-// backward statistics follows it).
+// backward statistics follows it). 32 queries per step: at D = 32 (the head dim
+// this kernel serves) the two score-tile sets then take 64 registers and the
+// kernel 188, so two waves share each SIMD (64-query steps took 328 registers,
+// one wave per SIMD, and ran 6% slower).
 template <int D>
-constexpr int kv_pipe_bmq() { return D >= 128 ? 32 : 64; }
+constexpr int kv_pipe_bmq() { return 32; }
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
@@ -452,19 +461,21 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   const __amdgpu_buffer_rsrc_t rqt = make_rsrc((const char*)p.qT + (int64_t)bh * tr_bytes, tr_bytes);
   const __amdgpu_buffer_rsrc_t rdot = make_rsrc((const char*)p.doT + (int64_t)bh * tr_bytes, tr_bytes);
   const __amdgpu_buffer_rsrc_t rst = make_rsrc((const char*)p.stats + (int64_t)bh * st_bytes, st_bytes);
-  constexpr int RPW = C::NRI / C::NW, TPW = C::NTI / C::NW;
-  uint32_t roff_q[RPW], roff_do[RPW], toff[TPW];
+  // request g of the row tiles: tensor g / NRI (Q, dO), 1 KiB block g % NRI
+  constexpr int RL = C::RLOADS, TL = C::TLOADS;
+  uint32_t roff[RL], toff[TL];
 #pragma unroll
-  for (int j = 0; j < RPW; ++j) {
-    const int pch = (wave + j * C::NW) * 64 + lane;
+  for (int j = 0; j < RL; ++j) {
+    const int g = wave + j * C::NW;
+    const int pch = (g % C::NRI) * 64 + lane;
     const int row = pch / CR, phys = pch % CR;
     const int logical = phys ^ swz<CR>(perm32(row & 31) & 15);
-    roff_q[j] = (uint32_t)((int64_t)row * p.q_sl * 2) + logical * 16;
-    roff_do[j] = (uint32_t)((int64_t)row * p.do_sl * 2) + logical * 16;
+    roff[j] = (uint32_t)((int64_t)row * (g < C::NRI ? p.q_sl : p.do_sl) * 2) + logical * 16;
   }
 #pragma unroll
-  for (int j = 0; j < TPW; ++j) {
-    const int pch = (wave + j * C::NW) * 64 + lane;
+  for (int j = 0; j < TL; ++j) {
+    const int g = wave + j * C::NW;
+    const int pch = (g % C::NTI) * 64 + lane;
     const int d = pch / CT, phys = pch % CT;
     const int logical = phys ^ swz<CT>(d & 15);
     toff[j] = (uint32_t)(d * p.LQP * 2) + logical * 16;
@@ -486,13 +497,13 @@ __global__ __launch_bounds__(256) void attn_bwd_kv_pipe_kernel(BwdParams p) {
   // the end read zeros or in-range rows (buffer range checks) into a stage
   // nobody reads again.
   auto issue_load = [&](lds_char_t* st, int qt, int li) {
-    if (li < 2 * RPW) {
-      const int jj = li >> 1, i = wave + jj * C::NW;
-      if (li & 1) buf_load16_lds(rdo, st + C::OFF_DO + i * 1024, roff_do[jj], (uint32_t)qt * do_step);
-      else buf_load16_lds(rq, st + C::OFF_Q + i * 1024, roff_q[jj], (uint32_t)qt * q_step);
-    } else if (li < 2 * RPW + 2 * TPW) {
-      const int jj = (li - 2 * RPW) >> 1, i = wave + jj * C::NW;
-      if (li & 1) buf_load16_lds(rdot, st + C::OFF_DOT + i * 1024, toff[jj], (uint32_t)qt * BMQ * 2);
+    if (li < RL) {
+      const int g = wave + li * C::NW, i = g % C::NRI;
+      if (g >= C::NRI) buf_load16_lds(rdo, st + C::OFF_DO + i * 1024, roff[li], (uint32_t)qt * do_step);
+      else buf_load16_lds(rq, st + C::OFF_Q + i * 1024, roff[li], (uint32_t)qt * q_step);
+    } else if (li < RL + TL) {
+      const int jj = li - RL, g = wave + jj * C::NW, i = g % C::NTI;
+      if (g >= C::NTI) buf_load16_lds(rdot, st + C::OFF_DOT + i * 1024, toff[jj], (uint32_t)qt * BMQ * 2);
       else buf_load16_lds(rqt, st + C::OFF_QT + i * 1024, toff[jj], (uint32_t)qt * BMQ * 2);
     } else {
       if (st_lane) buf_load16_lds(rst, st + C::OFF_ST, lane * 16, (uint32_t)qt * C::STAT_BYTES);
