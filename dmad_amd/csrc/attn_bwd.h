@@ -278,8 +278,9 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int v = 8 * t + e;
-          float pe = fast_exp2(fmaf(sacc[qb][v], p.scale_log2, -lse2[e]));
-          pe = key_ok ? pe : 0.f;
+          // no key mask: a lane's key >= Lk reads K = V = 0, and its dK, dV
+          // column (the only outputs its P, dS reach) is never stored
+          const float pe = fast_exp2(fmaf(sacc[qb][v], p.scale_log2, -lse2[e]));
           pv[e] = pe;
           if constexpr (!FULL) {
             dsv[e] = pe * (dpacc[qb][v] - dlt[e]);
