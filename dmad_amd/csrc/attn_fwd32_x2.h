@@ -247,6 +247,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
       qa[s] = load_qd(s);
     }
     __builtin_amdgcn_sched_barrier(0);
+    // the MFMA phases run at wave priority 1 and the softmax at 0, so that on a
+    // SIMD shared with another workgroup's wave the matrix unit goes to the wave
+    // in its MFMA phase and the other's softmax fills the gaps (0.8% faster)
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const i32x4_t a = ka[s % PFA], qd = qa[s % PFA];
@@ -258,6 +262,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
       tc = mfma32(a, qd, s == 0 ? zero16 : tc, T());
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     // the last tile may hold keys >= Lk
     if (i == ntiles - 1) {
 #pragma unroll
@@ -278,6 +284,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
       soft_pair(v, sc, tc, pk, hk, ls, rs);
       if (v & 2) __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(1);
     // phase B: O~^T += V^T P~^T, C~^T += V^T H~^T (per 16-key chunk t, block db);
     // the second chunk's values are computed beside the first chunk's MFMAs
 #pragma unroll
@@ -290,6 +297,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
       if (j < DB) soft_pair(8 + 2 * j, sc, tc, pk, hk, ls, rs);
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     l_i = l_i * alpha + ls;
     r_i = r_i * alpha + rs;
   };
