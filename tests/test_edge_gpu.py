@@ -75,7 +75,9 @@ def _check(xs, got, full, tol=1e-2):
     assert not bad, bad
 
 
-@pytest.mark.parametrize("D", [128, 64])
+# 16 and 32: the generic and pipelined passes (keys beyond Lk unmasked in the dK/dV
+# passes, the 32-wide dK/dV pass's statistics in 32-query tiles)
+@pytest.mark.parametrize("D", [128, 64, 32, 16])
 @pytest.mark.parametrize("Lq,Lk", [(1, 1), (1, 257), (257, 1), (33, 31), (129, 95), (64, 128)])
 @pytest.mark.parametrize("full", [False, True])
 def test_tiny_and_off_grid_lengths(gpu, D, Lq, Lk, full):
