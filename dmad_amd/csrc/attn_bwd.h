@@ -407,7 +407,7 @@ struct KvPipeCfg {
 // backward statistics follows it). 32 queries per step: at D = 32 (the head dim
 // this kernel serves) the two score-tile sets then take 64 registers and the
 // kernel 188, so two waves share each SIMD (64-query steps took 328 registers,
-// one wave per SIMD, and ran 6% slower).
+// one wave per SIMD: 14.4 against 11.4 ms at B=4, H=32, L=16384, fp16).
 template <int D>
 constexpr int kv_pipe_bmq() { return 32; }
 
