@@ -52,19 +52,27 @@ __device__ __forceinline__ void buf_store_f4(__amdgpu_buffer_rsrc_t r, f32x4_t v
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), r, (int)voff, 0, 0);
 }
 
+// Dense JVP modes with 256-wide Q, K: the one-wave-per-SIMD forward below.
+constexpr bool f32_fwd_wide(int mode, int dqk, bool magi) { return dqk > 128 && mode != kFwdPlain && !magi; }
+
 // ------------------------------------------------------------------ forward
 // 8 waves x 16 queries = 128-query tiles (the block-sparse task size), 32-key
 // steps. V is processed in column chunks (128 wide, 64 when Q and K are
 // 256 wide), each chunk by its own workgroup recomputing the scores, so Q, Qd
-// and the O~, C~ accumulators fit 256 registers without spills.
-template <int DQK, int DV, int MODE>
+// and the O~, C~ accumulators fit 256 registers without spills. The dense JVP
+// modes with 256-wide Q and K (f32_fwd_wide) run one wave per SIMD instead:
+// 4 waves x 16 queries, up to 512 registers, so that all of V fits one
+// workgroup and the 256-wide scores are computed once per query tile rather
+// than once per 64-column chunk.
+template <int DQK, int DV, int MODE, bool MAGI = false>
 struct F32FwdCfg {
-  static constexpr int NW = 8;
+  static constexpr bool WIDE = f32_fwd_wide(MODE, DQK, MAGI);
+  static constexpr int NW = WIDE ? 4 : 8;
   static constexpr int NT = 64 * NW;
   static constexpr int BM = 16 * NW;
   static constexpr int BN = 32;
   static constexpr int NB = BN / 16;
-  static constexpr int DVW = DQK > 128 && MODE != kFwdPlain ? 64 : 128;  // widest V chunk that fits
+  static constexpr int DVW = WIDE ? 256 : DQK > 128 && MODE != kFwdPlain ? 64 : 128;  // widest V chunk that fits
   static constexpr int DVC = DV < DVW ? DV : DVW;  // V columns per workgroup
   static constexpr int NCH = DV / DVC;             // workgroups per query tile
   static constexpr int KT = DQK / 16;              // 16-wide d chunks of the scores
@@ -82,13 +90,15 @@ struct F32FwdCfg {
   static constexpr int VPT = (VCH + NT - 1) / NT;
   // the next tile is prefetched into registers while this one is used, unless
   // that would push the wave past 256 registers
-  static constexpr bool PREFETCH = (KVT ? 2 : 1) * (KPT + VPT) * 4 + (JVP ? 2 : 1) * DQK / 4 + 2 * DVC / 4 <= 176;
+  static constexpr bool PREFETCH =
+      (KVT ? 2 : 1) * (KPT + VPT) * 4 + (JVP ? 2 : 1) * DQK / 4 + 2 * DVC / 4 <= (WIDE ? 352 : 176);
   static_assert(LDS_FLOATS * 4 <= 160 * 1024, "tile exceeds LDS");
 };
 
 template <int DQK, int DV, int MODE, bool MAGI>
-__global__ __launch_bounds__(512) void attn_f32_fwd_kernel(FwdParams p) {
-  using C = F32FwdCfg<DQK, DV, MODE>;
+__global__ __launch_bounds__(f32_fwd_wide(MODE, DQK, MAGI) ? 256 : 512) void attn_f32_fwd_kernel(FwdParams p) {
+  using C = F32FwdCfg<DQK, DV, MODE, MAGI>;
+  static_assert(C::NT == (f32_fwd_wide(MODE, DQK, MAGI) ? 256 : 512), "launch bounds match the workgroup");
   constexpr int BN = C::BN, NB = C::NB, KT = C::KT, DB = C::DB, KP = C::KP, VP = C::VP, DVC = C::DVC;
   __shared__ __attribute__((aligned(16))) float smem[C::LDS_FLOATS];
   float* const sk = smem;                   // K rows  [BN][KP]
@@ -173,7 +183,7 @@ __global__ __launch_bounds__(512) void attn_f32_fwd_kernel(FwdParams p) {
   // ---- one key tile: global -> registers -> LDS (K rows, V transposed);
   // keys at or beyond Lk read as zero (and are masked in the scores)
   f32x4_t kr[C::KPT], ktr[C::KPT], vr[C::VPT], vtr[C::VPT];
-  auto fetch = [&](int start) {
+  auto fetch_k = [&](int start) {
 #pragma unroll
     for (int j = 0; j < C::KPT; ++j) {
       const int c = tid + j * C::NT;
@@ -183,6 +193,8 @@ __global__ __launch_bounds__(512) void attn_f32_fwd_kernel(FwdParams p) {
       kr[j] = buf_load_f4(rk, off);
       if constexpr (C::KVT) ktr[j] = buf_load_f4(rtk, off);
     }
+  };
+  auto fetch_v = [&](int start) {
 #pragma unroll
     for (int j = 0; j < C::VPT; ++j) {
       const int c = tid + j * C::NT;
@@ -194,7 +206,7 @@ __global__ __launch_bounds__(512) void attn_f32_fwd_kernel(FwdParams p) {
       if constexpr (C::KVT) vtr[j] = buf_load_f4(rtv, off);
     }
   };
-  auto put = [&]() {
+  auto put_k = [&]() {
 #pragma unroll
     for (int j = 0; j < C::KPT; ++j) {
       const int c = tid + j * C::NT;
@@ -204,6 +216,8 @@ __global__ __launch_bounds__(512) void attn_f32_fwd_kernel(FwdParams p) {
         if constexpr (C::KVT) *(f32x4_t*)(skt + row * KP + 4 * c4) = ktr[j];
       }
     }
+  };
+  auto put_v = [&]() {
 #pragma unroll
     for (int j = 0; j < C::VPT; ++j) {
       const int c = tid + j * C::NT;
@@ -226,12 +240,24 @@ __global__ __launch_bounds__(512) void attn_f32_fwd_kernel(FwdParams p) {
   }
   float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
 
+  auto fetch = [&](int start) {
+    fetch_k(start);
+    fetch_v(start);
+  };
   if constexpr (C::PREFETCH) fetch(MAGI ? ci.start : 0);
   for (int kt = 0; kt < ntiles; ++kt) {
     const int start = MAGI ? cm.start : kt * BN;
     __syncthreads();  // every wave is done with the previous tile
-    if constexpr (!C::PREFETCH) fetch(start);
-    put();
+    if constexpr (C::WIDE && !C::PREFETCH) {  // K rows, then V: half the staging registers live at once
+      fetch_k(start);
+      put_k();
+      fetch_v(start);
+      put_v();
+    } else {
+      if constexpr (!C::PREFETCH) fetch(start);
+      put_k();
+      put_v();
+    }
     if constexpr (MAGI) ci.next(p, BN);
     if constexpr (C::PREFETCH) {
       if (kt + 1 < ntiles) fetch(MAGI ? ci.start : (kt + 1) * BN);

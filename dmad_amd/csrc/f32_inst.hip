@@ -8,19 +8,25 @@
 
 namespace dmad {
 
-static_assert(F32FwdCfg<DMAD_D, 16, kFwdJvp>::BM == kMagiBlockM, "block-sparse tasks are 128-query tiles");
-static_assert(F32FwdCfg<DMAD_D, 256, kFwdJvp>::NCH == f32_fwd_chunks(kFwdJvp, DMAD_D, 256) &&
-                  F32FwdCfg<DMAD_D, 128, kFwdJvp>::NCH == f32_fwd_chunks(kFwdJvp, DMAD_D, 128) &&
-                  F32FwdCfg<DMAD_D, 64, kFwdJvp>::NCH == f32_fwd_chunks(kFwdJvp, DMAD_D, 64) &&
-                  F32FwdCfg<DMAD_D, 256, kFwdJvpQOnly>::NCH == f32_fwd_chunks(kFwdJvpQOnly, DMAD_D, 256) &&
-                  F32FwdCfg<DMAD_D, 256, kFwdPlain>::NCH == f32_fwd_chunks(kFwdPlain, DMAD_D, 256) &&
-                  F32FwdCfg<DMAD_D, 128, kFwdPlain>::NCH == f32_fwd_chunks(kFwdPlain, DMAD_D, 128),
-              "the launcher's grid matches the kernel's column chunks");
+static_assert(F32FwdCfg<DMAD_D, 16, kFwdJvp, true>::BM == kMagiBlockM &&
+                  F32FwdCfg<DMAD_D, 256, kFwdJvpQOnly, true>::BM == kMagiBlockM,
+              "block-sparse tasks are 128-query tiles");
+// the launcher's grid matches the kernel's query tile and column chunks
+template <int DV, int MODE, bool MAGI>
+constexpr bool f32_grid_matches() {
+  using C = F32FwdCfg<DMAD_D, DV, MODE, MAGI>;
+  return C::NCH == f32_fwd_chunks(MODE, DMAD_D, DV, MAGI) && C::BM == f32_fwd_bm(MODE, DMAD_D, MAGI);
+}
+static_assert(f32_grid_matches<256, kFwdJvp, false>() && f32_grid_matches<256, kFwdJvp, true>() &&
+                  f32_grid_matches<128, kFwdJvp, false>() && f32_grid_matches<64, kFwdJvp, true>() &&
+                  f32_grid_matches<256, kFwdJvpQOnly, false>() && f32_grid_matches<256, kFwdJvpQOnly, true>() &&
+                  f32_grid_matches<256, kFwdPlain, false>() && f32_grid_matches<128, kFwdPlain, false>(),
+              "the launcher's grid matches the kernel's query tile and column chunks");
 
 template <int DQK, int DV, int MODE, bool MAGI>
 static hipError_t f32_fwd_launch(const FwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_f32_fwd_kernel<DQK, DV, MODE, MAGI>), dim3(grid), dim3(F32FwdCfg<DQK, DV, MODE>::NT), 0,
-                     s, p);
+  hipLaunchKernelGGL((attn_f32_fwd_kernel<DQK, DV, MODE, MAGI>), dim3(grid),
+                     dim3(F32FwdCfg<DQK, DV, MODE, MAGI>::NT), 0, s, p);
   return hipGetLastError();
 }
 

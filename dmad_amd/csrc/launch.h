@@ -135,7 +135,7 @@ inline bool dq_dout_only_reads_rows(int d) {
 
 // fp32 operands (attn_f32.h; f32_inst.hip, one compilation per head dim).
 // Forward launcher for (Dqk, Dv, mode), dense or block-sparse, or nullptr; the
-// grid is (query tiles or tasks) * B * H * f32_fwd_chunks(mode, Dqk, Dv) workgroups.
+// grid is (f32_fwd_bm-query tiles or tasks) * B * H * f32_fwd_chunks(mode, Dqk, Dv, magi) workgroups.
 template <int DQK>
 FwdLaunchFn f32_fwd_select(int dv, int mode, bool magi);
 template <> FwdLaunchFn f32_fwd_select<16>(int, int, bool);
@@ -143,12 +143,15 @@ template <> FwdLaunchFn f32_fwd_select<32>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<64>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<128>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<256>(int, int, bool);
-// V columns per workgroup: 128, or 64 in the JVP modes with 256-wide Q, K
-// (their Q, Qd slices and two accumulators would not fit 256 registers)
-constexpr int f32_fwd_chunks(int mode, int dqk, int dv) {
-  const int dvc = dqk > 128 && mode != kFwdPlain ? 64 : 128;
+// V columns per workgroup: 128, or 64 in the block-sparse JVP modes with
+// 256-wide Q, K (their Q, Qd slices and two accumulators would not fit 256
+// registers); all of V in the dense ones (one wave per SIMD, f32_fwd_wide)
+constexpr int f32_fwd_chunks(int mode, int dqk, int dv, bool magi) {
+  const int dvc = f32_fwd_wide(mode, dqk, magi) ? 256 : dqk > 128 && mode != kFwdPlain ? 64 : 128;
   return dv > dvc ? dv / dvc : 1;
 }
+// Query rows per workgroup of the fp32 forward (and per task of its block-sparse form)
+constexpr int f32_fwd_bm(int mode, int dqk, bool magi) { return f32_fwd_wide(mode, dqk, magi) ? 64 : 128; }
 // dO-only backward: statistics, key pass, query pass (each sizes its own grid).
 struct F32BwdFns {
   hipError_t (*prep)(const F32PrepParams&, hipStream_t);

@@ -102,13 +102,22 @@ def test_block_sparse_forward():
         nat.fwd_plan(BF16, PLAIN, 1, 40, 24960, 512, 128, 128, magi_tasks=198)
 
 
-@pytest.mark.parametrize("Dqk,Dv,chunks", [(64, 64, 1), (128, 128, 1), (256, 256, 4), (128, 256, 2), (16, 32, 1)])
-def test_fp32_forward(Dqk, Dv, chunks):
-    p = nat.fwd_plan(F32, JVP, 4, 32, 4096, 4096, Dqk, Dv)
-    assert (p["kernel"], p["chunks"], p["grid"], p["transposed_copies"], p["workspace_bytes"]) == \
-        ("attn_f32_fwd_kernel", chunks, 32 * 128 * chunks, 0, 0)
+# (Dqk, Dv, V chunks, query rows per workgroup): 256-wide Q, K in the JVP modes run
+# four waves of 16 queries (one per SIMD) with all of V in one workgroup
+@pytest.mark.parametrize("Dqk,Dv,chunks,bm", [(64, 64, 1, 128), (128, 128, 1, 128), (256, 256, 1, 64),
+                                              (256, 128, 1, 64), (128, 256, 2, 128), (16, 32, 1, 128)])
+def test_fp32_forward(Dqk, Dv, chunks, bm):
+    for mode in (JVP, QONLY):
+        p = nat.fwd_plan(F32, mode, 4, 32, 4096, 4096, Dqk, Dv)
+        assert (p["kernel"], p["chunks"], p["grid"], p["transposed_copies"], p["workspace_bytes"]) == \
+            ("attn_f32_fwd_kernel", chunks, (4096 // bm) * 128 * chunks, 0, 0)
     # the plain forward takes 128 V columns per workgroup at every Q, K width
-    assert nat.fwd_plan(F32, PLAIN, 4, 32, 4096, 4096, Dqk, Dv)["chunks"] == max(1, Dv // 128)
+    p = nat.fwd_plan(F32, PLAIN, 4, 32, 4096, 4096, Dqk, Dv)
+    assert (p["chunks"], p["grid"]) == (max(1, Dv // 128), 32 * 128 * max(1, Dv // 128))
+    # block-sparse: 128-query tasks, V in 64-column chunks when Q, K are 256 wide
+    m = nat.fwd_plan(F32, JVP, 1, 40, 24960, 32760, Dqk, Dv, magi_tasks=198)
+    mc = Dv // 64 if Dqk > 128 else max(1, Dv // 128)
+    assert (m["chunks"], m["grid"]) == (mc, 198 * 40 * mc)
 
 
 def test_backward_passes():
