@@ -57,10 +57,12 @@ constexpr bool f32_fwd_wide(int mode, int dqk, bool magi) { return dqk > 128 && 
 
 // ------------------------------------------------------------------ forward
 // 8 waves x 16 queries = 128-query tiles (the block-sparse task size), 32-key
-// steps. V is processed in column chunks (128 wide, 64 when Q and K are
-// 256 wide), each chunk by its own workgroup recomputing the scores, so Q, Qd
-// and the O~, C~ accumulators fit 256 registers without spills. The dense JVP
-// modes with 256-wide Q and K (f32_fwd_wide) run one wave per SIMD instead:
+// steps. In the JVP modes V is processed in column chunks (128 wide, 64 when Q
+// and K are 256 wide), each chunk by its own workgroup recomputing the scores,
+// so Q, Qd and the O~, C~ accumulators fit 256 registers without spills; the
+// plain forward holds up to 256 columns of O~ in one workgroup (244 registers
+// at the widest). The dense JVP modes with 256-wide Q and K (f32_fwd_wide)
+// run one wave per SIMD instead:
 // 4 waves x 16 queries, up to 512 registers, so that all of V fits one
 // workgroup and the 256-wide scores are computed once per query tile rather
 // than once per 64-column chunk.
@@ -72,7 +74,7 @@ struct F32FwdCfg {
   static constexpr int BM = 16 * NW;
   static constexpr int BN = 32;
   static constexpr int NB = BN / 16;
-  static constexpr int DVW = WIDE ? 256 : DQK > 128 && MODE != kFwdPlain ? 64 : 128;  // widest V chunk that fits
+  static constexpr int DVW = WIDE || MODE == kFwdPlain ? 256 : DQK > 128 ? 64 : 128;  // widest V chunk that fits
   static constexpr int DVC = DV < DVW ? DV : DVW;  // V columns per workgroup
   static constexpr int NCH = DV / DVC;             // workgroups per query tile
   static constexpr int KT = DQK / 16;              // 16-wide d chunks of the scores

@@ -143,11 +143,12 @@ template <> FwdLaunchFn f32_fwd_select<32>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<64>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<128>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<256>(int, int, bool);
-// V columns per workgroup: 128, or 64 in the block-sparse JVP modes with
-// 256-wide Q, K (their Q, Qd slices and two accumulators would not fit 256
-// registers); all of V in the dense ones (one wave per SIMD, f32_fwd_wide)
+// V columns per workgroup in the JVP modes: 128, or 64 in the block-sparse ones
+// with 256-wide Q, K (their Q, Qd slices and two accumulators would not fit 256
+// registers), all of V in the dense ones (one wave per SIMD, f32_fwd_wide); the
+// plain forward takes up to 256 columns at every Q, K width
 constexpr int f32_fwd_chunks(int mode, int dqk, int dv, bool magi) {
-  const int dvc = f32_fwd_wide(mode, dqk, magi) ? 256 : dqk > 128 && mode != kFwdPlain ? 64 : 128;
+  const int dvc = f32_fwd_wide(mode, dqk, magi) || mode == kFwdPlain ? 256 : dqk > 128 ? 64 : 128;
   return dv > dvc ? dv / dvc : 1;
 }
 // Query rows per workgroup of the fp32 forward (and per task of its block-sparse form)

@@ -111,9 +111,9 @@ def test_fp32_forward(Dqk, Dv, chunks, bm):
         p = nat.fwd_plan(F32, mode, 4, 32, 4096, 4096, Dqk, Dv)
         assert (p["kernel"], p["chunks"], p["grid"], p["transposed_copies"], p["workspace_bytes"]) == \
             ("attn_f32_fwd_kernel", chunks, (4096 // bm) * 128 * chunks, 0, 0)
-    # the plain forward takes 128 V columns per workgroup at every Q, K width
+    # the plain forward takes all of V (up to 256 columns) in one workgroup at every Q, K width
     p = nat.fwd_plan(F32, PLAIN, 4, 32, 4096, 4096, Dqk, Dv)
-    assert (p["chunks"], p["grid"]) == (max(1, Dv // 128), 32 * 128 * max(1, Dv // 128))
+    assert (p["chunks"], p["grid"]) == (1, 32 * 128)
     # block-sparse: 128-query tasks, V in 64-column chunks when Q, K are 256 wide
     m = nat.fwd_plan(F32, JVP, 1, 40, 24960, 32760, Dqk, Dv, magi_tasks=198)
     mc = Dv // 64 if Dqk > 128 else max(1, Dv // 128)
