@@ -52,29 +52,31 @@ __device__ __forceinline__ void buf_store_f4(__amdgpu_buffer_rsrc_t r, f32x4_t v
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, v), r, (int)voff, 0, 0);
 }
 
-// Dense JVP modes with 256-wide Q, K: the one-wave-per-SIMD forward below.
-constexpr bool f32_fwd_wide(int mode, int dqk, bool magi) { return dqk > 128 && mode != kFwdPlain && !magi; }
+// JVP modes with 256-wide Q, K: the one-wave-per-SIMD forward below (a
+// block-sparse task's 128 query rows then take two workgroups of 64).
+constexpr bool f32_fwd_wide(int mode, int dqk) { return dqk > 128 && mode != kFwdPlain; }
 
 // ------------------------------------------------------------------ forward
 // 8 waves x 16 queries = 128-query tiles (the block-sparse task size), 32-key
-// steps. In the JVP modes V is processed in column chunks (128 wide, 64 when Q
-// and K are 256 wide), each chunk by its own workgroup recomputing the scores,
-// so Q, Qd and the O~, C~ accumulators fit 256 registers without spills; the
-// plain forward holds up to 256 columns of O~ in one workgroup (244 registers
-// at the widest). The dense JVP modes with 256-wide Q and K (f32_fwd_wide)
-// run one wave per SIMD instead:
+// steps. In the JVP modes a 256-wide V is processed in two 128-column chunks,
+// each by its own workgroup recomputing the scores, so Q, Qd and the O~, C~
+// accumulators fit 256 registers without spills; the plain forward holds up
+// to 256 columns of O~ in one workgroup (244 registers at the widest). The JVP
+// modes with 256-wide Q and K (f32_fwd_wide) run one wave per SIMD instead:
 // 4 waves x 16 queries, up to 512 registers, so that all of V fits one
 // workgroup and the 256-wide scores are computed once per query tile rather
-// than once per 64-column chunk.
+// than once per 64-column chunk (two such workgroups per block-sparse task).
 template <int DQK, int DV, int MODE, bool MAGI = false>
 struct F32FwdCfg {
-  static constexpr bool WIDE = f32_fwd_wide(MODE, DQK, MAGI);
+  static constexpr bool WIDE = f32_fwd_wide(MODE, DQK);
   static constexpr int NW = WIDE ? 4 : 8;
   static constexpr int NT = 64 * NW;
   static constexpr int BM = 16 * NW;
+  static constexpr int TASK_ROWS = 128;            // query rows of a block-sparse task
+  static constexpr int HALVES = TASK_ROWS / BM;     // workgroups per block-sparse task
   static constexpr int BN = 32;
   static constexpr int NB = BN / 16;
-  static constexpr int DVW = WIDE || MODE == kFwdPlain ? 256 : DQK > 128 ? 64 : 128;  // widest V chunk that fits
+  static constexpr int DVW = WIDE || MODE == kFwdPlain ? 256 : 128;  // widest V chunk that fits
   static constexpr int DVC = DV < DVW ? DV : DVW;  // V columns per workgroup
   static constexpr int NCH = DV / DVC;             // workgroups per query tile
   static constexpr int KT = DQK / 16;              // 16-wide d chunks of the scores
@@ -98,9 +100,10 @@ struct F32FwdCfg {
 };
 
 template <int DQK, int DV, int MODE, bool MAGI>
-__global__ __launch_bounds__(f32_fwd_wide(MODE, DQK, MAGI) ? 256 : 512) void attn_f32_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(f32_fwd_wide(MODE, DQK) ? 256 : 512) void attn_f32_fwd_kernel(FwdParams p) {
   using C = F32FwdCfg<DQK, DV, MODE, MAGI>;
-  static_assert(C::NT == (f32_fwd_wide(MODE, DQK, MAGI) ? 256 : 512), "launch bounds match the workgroup");
+  static_assert(C::NT == (f32_fwd_wide(MODE, DQK) ? 256 : 512), "launch bounds match the workgroup");
+  static_assert(C::HALVES * C::BM == C::TASK_ROWS, "a block-sparse task is a whole number of workgroup tiles");
   constexpr int BN = C::BN, NB = C::NB, KT = C::KT, DB = C::DB, KP = C::KP, VP = C::VP, DVC = C::DVC;
   __shared__ __attribute__((aligned(16))) float smem[C::LDS_FLOATS];
   float* const sk = smem;                   // K rows  [BN][KP]
@@ -117,18 +120,19 @@ __global__ __launch_bounds__(f32_fwd_wide(MODE, DQK, MAGI) ? 256 : 512) void att
   int q_lo = 0, q_hi = p.Lq;  // rows this workgroup stores
   MagiCursor cm{0, 0, 0, 0, 0};
   if constexpr (MAGI) {
-    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H * C::NCH);
+    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H * C::NCH * C::HALVES);
     chunk = work % C::NCH;
-    const int w2 = work / C::NCH;
+    const int half = (work / C::NCH) % C::HALVES;  // 64-row half of the task (one-wave-per-SIMD form)
+    const int w2 = work / (C::NCH * C::HALVES);
     bh = w2 / p.T;
-    const MagiTask t = magi_task(p, w2 - bh * p.T, C::BM);
-    row0 = t.row0;
+    const MagiTask t = magi_task(p, w2 - bh * p.T, C::TASK_ROWS);
+    row0 = t.row0 + half * C::BM;
     q_lo = t.q_lo;
     q_hi = t.q_hi;
     ntiles = magi_ntiles(p, t, BN);
     if (ntiles == 0) {  // uniform over the workgroup: the rows get O = Od = 0, LSE = -inf
       const int b = bh / p.H, h = bh - b * p.H;
-      const int lo = max(t.row0, t.q_lo), hi = min(t.row0 + C::BM, t.q_hi);
+      const int lo = max(row0, t.q_lo), hi = min(row0 + C::BM, t.q_hi);
       const int64_t obase = b * p.o_sb + h * p.o_sh;
       for (int idx = tid; idx < (hi - lo) * (DVC / 4); idx += C::NT) {
         const int r = lo + idx / (DVC / 4), c4 = idx % (DVC / 4);

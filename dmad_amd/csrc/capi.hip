@@ -224,13 +224,13 @@ FwdPlan plan_fwd(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, 
                  int64_t Dv) {
   const bool magi = magi_tasks >= 0;
   FwdPlan pl{};
-  int64_t bm = 128;  // query rows per workgroup (block-sparse tasks: always 128)
+  int64_t bm = 128;  // query rows per workgroup (a block-sparse task is 128 rows)
   if (dtype == DMAD_F32) {
     // fp32 operands: fp32-MFMA kernels, V in column chunks for wide heads
     pl.family = FwdFamily::kF32;
     pl.kernel = "attn_f32_fwd_kernel";
-    pl.chunks = dmad::f32_fwd_chunks(mode, (int)Dqk, (int)Dv, magi);
-    bm = dmad::f32_fwd_bm(mode, (int)Dqk, magi);
+    pl.chunks = dmad::f32_fwd_chunks(mode, (int)Dqk, (int)Dv);
+    bm = dmad::f32_fwd_bm(mode, (int)Dqk);
   } else if (!magi && dmad::fwd32x2_supported(mode, (int)Dqk, (int)Dv) && (Lk + 31) / 32 <= kX2MaxKeyTiles) {
     // short key sequences with Kd = Vd = 0 (the text cross-attention): two workgroups per CU
     pl.family = FwdFamily::kRowsX2;
@@ -253,7 +253,7 @@ FwdPlan plan_fwd(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, 
     pl.chunks = dmad::fwd_generic_chunks(mode, (int)Dqk, (int)Dv, magi);
     pl.copies = mode == DMAD_FWD_JVP ? 2 : 1;
   }
-  const int64_t units = magi ? magi_tasks : (Lq + bm - 1) / bm;  // query tiles or tasks
+  const int64_t units = magi ? magi_tasks * (dmad::kMagiBlockM / bm) : (Lq + bm - 1) / bm;  // query tiles
   pl.grid = units * B * H * pl.chunks;
   // block order (common.h): the block-sparse kernels always deal contiguous work items per XCD
   pl.xcd_order = magi ? 1 : units < dmad::kHeadMajorMinTiles;

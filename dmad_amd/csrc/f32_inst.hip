@@ -8,14 +8,12 @@
 
 namespace dmad {
 
-static_assert(F32FwdCfg<DMAD_D, 16, kFwdJvp, true>::BM == kMagiBlockM &&
-                  F32FwdCfg<DMAD_D, 256, kFwdJvpQOnly, true>::BM == kMagiBlockM,
-              "block-sparse tasks are 128-query tiles");
 // the launcher's grid matches the kernel's query tile and column chunks
 template <int DV, int MODE, bool MAGI>
 constexpr bool f32_grid_matches() {
   using C = F32FwdCfg<DMAD_D, DV, MODE, MAGI>;
-  return C::NCH == f32_fwd_chunks(MODE, DMAD_D, DV, MAGI) && C::BM == f32_fwd_bm(MODE, DMAD_D, MAGI);
+  return C::NCH == f32_fwd_chunks(MODE, DMAD_D, DV) && C::BM == f32_fwd_bm(MODE, DMAD_D) &&
+         C::TASK_ROWS == kMagiBlockM;
 }
 static_assert(f32_grid_matches<256, kFwdJvp, false>() && f32_grid_matches<256, kFwdJvp, true>() &&
                   f32_grid_matches<128, kFwdJvp, false>() && f32_grid_matches<64, kFwdJvp, true>() &&

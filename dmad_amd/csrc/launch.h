@@ -135,7 +135,8 @@ inline bool dq_dout_only_reads_rows(int d) {
 
 // fp32 operands (attn_f32.h; f32_inst.hip, one compilation per head dim).
 // Forward launcher for (Dqk, Dv, mode), dense or block-sparse, or nullptr; the
-// grid is (f32_fwd_bm-query tiles or tasks) * B * H * f32_fwd_chunks(mode, Dqk, Dv, magi) workgroups.
+// grid is (f32_fwd_bm-query tiles, or tasks * kMagiBlockM / f32_fwd_bm) * B * H * f32_fwd_chunks(mode, Dqk, Dv)
+// workgroups.
 template <int DQK>
 FwdLaunchFn f32_fwd_select(int dv, int mode, bool magi);
 template <> FwdLaunchFn f32_fwd_select<16>(int, int, bool);
@@ -143,16 +144,16 @@ template <> FwdLaunchFn f32_fwd_select<32>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<64>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<128>(int, int, bool);
 template <> FwdLaunchFn f32_fwd_select<256>(int, int, bool);
-// V columns per workgroup in the JVP modes: 128, or 64 in the block-sparse ones
-// with 256-wide Q, K (their Q, Qd slices and two accumulators would not fit 256
-// registers), all of V in the dense ones (one wave per SIMD, f32_fwd_wide); the
-// plain forward takes up to 256 columns at every Q, K width
-constexpr int f32_fwd_chunks(int mode, int dqk, int dv, bool magi) {
-  const int dvc = f32_fwd_wide(mode, dqk, magi) || mode == kFwdPlain ? 256 : dqk > 128 ? 64 : 128;
+// V columns per workgroup: 128 in the JVP modes, all of V with 256-wide Q, K
+// (one wave per SIMD, f32_fwd_wide); the plain forward takes up to 256 columns
+// at every Q, K width
+constexpr int f32_fwd_chunks(int mode, int dqk, int dv) {
+  const int dvc = f32_fwd_wide(mode, dqk) || mode == kFwdPlain ? 256 : 128;
   return dv > dvc ? dv / dvc : 1;
 }
-// Query rows per workgroup of the fp32 forward (and per task of its block-sparse form)
-constexpr int f32_fwd_bm(int mode, int dqk, bool magi) { return f32_fwd_wide(mode, dqk, magi) ? 64 : 128; }
+// Query rows per workgroup of the fp32 forward (a block-sparse task's 128 rows
+// take kMagiBlockM / f32_fwd_bm workgroups)
+constexpr int f32_fwd_bm(int mode, int dqk) { return f32_fwd_wide(mode, dqk) ? 64 : 128; }
 // dO-only backward: statistics, key pass, query pass (each sizes its own grid).
 struct F32BwdFns {
   hipError_t (*prep)(const F32PrepParams&, hipStream_t);

@@ -165,6 +165,9 @@ MAGI = [
     ("block_causal", 40, 4, 2, 1, 128, 128, True),
     ("teacher_forcing", 24, 3, 0, 0, 128, 128, False),
     ("teacher_forcing", 16, 6, 3, 1, 32, 256, False),
+    # 256-wide Q, K: two 64-row workgroups per 128-query task, all of V in each
+    ("block_causal", 24, 4, 2, 1, 256, 256, False),
+    ("teacher_forcing", 20, 3, 0, 0, 256, 128, True),
 ]
 
 

@@ -114,10 +114,9 @@ def test_fp32_forward(Dqk, Dv, chunks, bm):
     # the plain forward takes all of V (up to 256 columns) in one workgroup at every Q, K width
     p = nat.fwd_plan(F32, PLAIN, 4, 32, 4096, 4096, Dqk, Dv)
     assert (p["chunks"], p["grid"]) == (1, 32 * 128)
-    # block-sparse: 128-query tasks, V in 64-column chunks when Q, K are 256 wide
+    # block-sparse: 128-query tasks, each 128 // bm workgroups
     m = nat.fwd_plan(F32, JVP, 1, 40, 24960, 32760, Dqk, Dv, magi_tasks=198)
-    mc = Dv // 64 if Dqk > 128 else max(1, Dv // 128)
-    assert (m["chunks"], m["grid"]) == (mc, 198 * 40 * mc)
+    assert (m["chunks"], m["grid"]) == (chunks, 198 * (128 // bm) * 40 * chunks)
 
 
 def test_backward_passes():
