@@ -218,8 +218,9 @@ typedef struct dmad_plan {
   int64_t grid2;             /* workgroups of `kernel2` (and of kernel4); 0 for the forward */
   int32_t xcd_order;         /* 1: work items dealt contiguously per XCD; 0: head-major (of `kernel`) */
   int32_t xcd_order2;        /* the same for `kernel2` */
-  int32_t chunks;            /* forward: workgroups per query tile or task (column chunks of a wide V); the
-                                query tile is 128 rows, 64 for fp32 with 256-wide Q, K in the dense JVP modes */
+  int32_t chunks;            /* forward: workgroups per query tile (column chunks of a wide V); the query tile
+                                is 128 rows (a block-sparse task), 64 for fp32 with 256-wide Q, K in the JVP
+                                modes (two per task) */
   int32_t transposed_copies; /* operands copied transposed into the workspace before the kernels */
   int64_t workspace_bytes;   /* workspace the call needs */
 } dmad_plan;
