@@ -123,7 +123,8 @@ __device__ __forceinline__ void stage_store(const lds_char_t* region, int k, int
 
 // MAGI: the block-sparse variant (the reference's `_attn_fwd_magi`,
 // flash_attention_jvp_triton.py:242-409). The workgroup runs one (query group,
-// 128-query tile) task; its key tiles walk the group's key ranges in order, a
+// 128-query tile) task (256-wide heads in the JVP modes: one 128-column chunk of
+// V of it, two adjacent workgroups per task); its key tiles walk the group's key ranges in order, a
 // range starting at a 32-key boundary below its first key, and keys outside the
 // current range score -inf (the reference's n_mask, :338-343). Only the tile's
 // rows inside the group's query range are stored (:386-409).
@@ -139,7 +140,6 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   constexpr int DVC = C::DVC, CRV = C::CRV, ROWBV = C::ROWBV, NSTAGE = C::NSTAGE;
   constexpr int NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
   constexpr float kSlack = RescaleSlack<T>::value;
-  static_assert(!MAGI || C::CHUNKS == 1, "the block-sparse forward takes 64- and 128-wide heads");
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
@@ -153,7 +153,11 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   int q_lo = 0, q_hi = p.Lq;  // rows this workgroup stores
   int r_beg = 0, r_end = 0;   // key ranges of the group (MAGI)
   if constexpr (MAGI) {
-    const int work = xcd_remap(blockIdx.x, p.T * p.B * p.H);
+    int work = xcd_remap(blockIdx.x, p.T * p.B * p.H * C::CHUNKS);
+    if constexpr (C::CHUNKS > 1) {
+      chunk = work % C::CHUNKS;  // the chunks of one task are adjacent work items
+      work /= C::CHUNKS;
+    }
     bh = work / p.T;
     const MagiTask t = magi_task(p, work - bh * p.T, C::BM);
     qt = t.row0 / C::BM;
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     r_end = t.r_end;
     ntiles = magi_ntiles(p, t, BN);
     if (ntiles == 0) {  // uniform over the workgroup: nothing requested yet
-      magi_store_empty<T, D, C::JVP>(p, bh, t, C::BM);
+      if (chunk == 0) magi_store_empty<T, D, C::JVP>(p, bh, t, C::BM);  // every column of the rows
       return;
     }
   } else {
@@ -554,7 +558,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
     for (int o = NOPA; o < NOP; ++o) mfma_op(o, load_op(s_cur, s_cur, o), un_s, un_t, pk, hk);
   };
 
-  // ---- prologue: tiles 0..2 requested, scores of tile 0
+  // ---- prologue: tiles 0..NSTAGE-2 requested, scores of tile 0
   if constexpr (MAGI) {
 #pragma unroll
     for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), ci.start, li);
@@ -562,9 +566,11 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
 #pragma unroll
     for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), ci.start, li);
     ci.next(p, BN);
+    if constexpr (NSTAGE == 4) {
 #pragma unroll
-    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), ci.start, li);
-    ci.next(p, BN);
+      for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), ci.start, li);
+      ci.next(p, BN);
+    }
   } else {
 #pragma unroll
     for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);

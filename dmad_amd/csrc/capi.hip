@@ -140,7 +140,8 @@ dmad::F32BwdFns pick_bwd_f32(int64_t d) {
 // 256 the dense forward reads it in place too, the block-sparse one does not:
 // this is the bound over both (plan_fwd gives one launch's size).
 int64_t fwd_ws_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv) {
-  if (dmad::fwd32_supported((int)Dqk, (int)Dv)) return 0;
+  // the row-reading kernels (every forward of 64- and 128-wide heads, and of 256-wide ones) read V in place
+  if (dmad::fwd32_supported((int)Dqk, (int)Dv) || dmad::fwd32_wide_supported((int)Dqk, (int)Dv)) return 0;
   const int64_t dvp = Dv < 32 ? 32 : Dv;
   const int64_t one = B * H * dvp * round_up(Lk, kLkAlign) * 2;
   return round_up(one, 256) * (mode == DMAD_FWD_JVP ? 2 : 1);
@@ -241,8 +242,9 @@ FwdPlan plan_fwd(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, 
     pl.family = FwdFamily::kRows;
     pl.kernel = "attn_fwd32_kernel";
     pl.chunks = 1;
-  } else if (!magi && dmad::fwd32_wide_supported((int)Dqk, (int)Dv)) {
+  } else if (dmad::fwd32_wide_supported((int)Dqk, (int)Dv)) {
     // 256-wide heads: the same kernel; the JVP modes run one workgroup per 128-column chunk of V
+    // (per query tile, or per block-sparse task)
     pl.family = FwdFamily::kRows;
     pl.kernel = "attn_fwd32_kernel";
     pl.chunks = dmad::fwd32_chunks(mode, 256);

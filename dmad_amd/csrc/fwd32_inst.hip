@@ -56,7 +56,10 @@ static FwdLaunchFn fwd32_mode(int mode) {
 
 template <>
 FwdLaunchFn fwd32_magi_select<Elt>(int mode, int d) {
-  return d == 64 ? fwd32_magi_mode<64>(mode) : d == 128 ? fwd32_magi_mode<128>(mode) : nullptr;
+  return d == 64    ? fwd32_magi_mode<64>(mode)
+         : d == 128 ? fwd32_magi_mode<128>(mode)
+         : d == 256 ? fwd32_magi_mode<256>(mode)
+                    : nullptr;
 }
 
 template <>

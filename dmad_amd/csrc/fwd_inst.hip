@@ -72,7 +72,9 @@ FwdLaunchFn fwd_magi_select<Elt, DMAD_D>(int dv, int mode) {
     case 128:
       if constexpr (fwd32_supported(DMAD_D, 128)) return fwd32_magi_select<Elt>(mode, 128);
       else return fwd_magi_mode<Elt, DMAD_D, 128>(mode);
-    case 256: return fwd_magi_mode<Elt, DMAD_D, 256>(mode);
+    case 256:
+      if constexpr (fwd32_wide_supported(DMAD_D, 256)) return fwd32_magi_select<Elt>(mode, 256);
+      else return fwd_magi_mode<Elt, DMAD_D, 256>(mode);
     default: return nullptr;
   }
 }

@@ -58,11 +58,10 @@ int dmad_abi_version(void);
 const char* dmad_last_error(void);
 
 /* Bytes of workspace dmad_attn_jvp_fwd / dmad_attn_fwd / dmad_attn_jvp_fwd_magi need
- * for these sizes with bf16/fp16 operands: 0 for Dqk = Dv = 64 or 128 (V is read in
- * place; the workspace pointer may then be NULL), else room for transposed copies of
- * V (and Vd). fp32 operands need none. It covers every forward entry: the dense
- * entries at Dqk = Dv = 256 also read V in place and need none (dmad_attn_fwd_plan
- * gives the exact size of one launch). */
+ * for these sizes with bf16/fp16 operands: 0 for Dqk = Dv = 64, 128 or 256 (V is read
+ * in place; the workspace pointer may then be NULL), else room for transposed copies
+ * of V (and Vd). fp32 operands need none. It covers every forward entry
+ * (dmad_attn_fwd_plan gives the exact size of one launch). */
 int dmad_attn_fwd_workspace_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv, size_t* bytes);
 
 /*

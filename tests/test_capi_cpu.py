@@ -93,14 +93,14 @@ def test_kv_tangent_zero_mode_does_not_need_kv_tangents(nat):
 def test_workspace_query(nat):
     n = ctypes.c_size_t(0)
     q = nat.lib().dmad_attn_fwd_workspace_bytes
-    # 64- and 128-wide heads read V in place: no workspace
-    for d in (64, 128):
+    # 64-, 128- and 256-wide heads read V in place: no workspace
+    for d in (64, 128, 256):
         for mode in (0, 1, 2):
             assert q(mode, 1, 40, 32760, d, d, ctypes.byref(n)) == 0 and n.value == 0
     # other head dims (or Dqk != Dv): transposed, key-padded copies of V (and Vd in the full JVP mode)
     assert q(1, 1, 40, 32760, 64, 128, ctypes.byref(n)) == 0
     assert n.value == 2 * 40 * 128 * 32768 * 2
-    assert q(0, 1, 40, 32760, 256, 256, ctypes.byref(n)) == 0
+    assert q(0, 1, 40, 32760, 128, 256, ctypes.byref(n)) == 0
     assert n.value == 40 * 256 * 32768 * 2
     assert q(0, 1, 1, 10, 16, 16, ctypes.byref(n)) == 0
     assert n.value == 32 * 64 * 2  # Dv < 32 pads to 32 rows, keys pad to 64

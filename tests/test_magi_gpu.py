@@ -109,15 +109,17 @@ WIDE = [
 ]
 
 
+# D = 256: the row-reading kernel in two 128-column chunks of V per task
+@pytest.mark.parametrize("D", [128, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", WIDE)
-def test_wide_heads(gpu, case, dtype):
+def test_wide_heads(gpu, case, dtype, D):
     mode, ft, nb, first, chunk, local, sink, B, H = case
-    print(f"case {case} dtype={dtype}", flush=True)
+    print(f"case {case} dtype={dtype} D={D}", flush=True)
     spec, Q, KV, allow = _spec(mode, ft, nb, first, chunk, local, sink)
     qr, kr = mm.make_magi_ranges_full(spec, Q_real=Q, KV_real=KV, device=gpu)
     mask = mm.prepare_magi_csr_and_tasks(qr, kr, Q_real=Q, KV_real=KV)
-    _check(_inputs(B, H, Q, KV, 128, 128, dtype, seed=7), gpu, mask, allow, 128 ** -0.5, dtype)
+    _check(_inputs(B, H, Q, KV, D, D, dtype, seed=7), gpu, mask, allow, D ** -0.5, dtype)
 
 
 def _sweep(n, seed):
@@ -227,7 +229,7 @@ def _call_tables(gpu, xs, q_ranges, k_ranges, qk_map, tasks, sentinel):
     return o.cpu(), to.cpu(), lse.cpu(), mu.cpu()
 
 
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D", [128, 64, 256])
 def test_hand_made_tables(gpu, D):
     """Group 0 [0, 100): keys [-20, 50) and [90, 95) (clipped at 0);
     group 1 [100, 230): keys [250, 400) entirely past Lk = 240 -> no keys;
