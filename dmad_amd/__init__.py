@@ -13,7 +13,10 @@ and the attention helpers of train/wan/rcm/utils/jvp_helper.py):
 * ``MinimalA2AAttnOpWithT``, ``RopeCache`` -- RoPE-with-tangent then local attention (one-GPU branch)
 * ``apply_rope_with_tangent``       -- interleaved RoPE of a BSHD pair, differentiable
 """
-from .jvp_attention import _attention, attention, plain_attention, set_backward_mode, set_reference_backward  # noqa: F401
+from .jvp_attention import (  # noqa: F401
+    _attention, attention, backward_mode, current_backward_mode, plain_attention, set_backward_mode,
+    set_reference_backward,
+)
 from .jvp_helper import (  # noqa: F401
     FlexOrSdpaLocalAttentionWithT,
     MinimalA2AAttnOpWithT,

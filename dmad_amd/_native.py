@@ -204,6 +204,13 @@ def bwd_plan(dtype: int, B: int, H: int, Lq: int, Lk: int, D: int, full: bool = 
     return pl.as_dict()
 
 
+@functools.lru_cache(maxsize=1024)
+def bwd_workspace_bytes_of(dtype: int, mode: int, B: int, H: int, Lq: int, Lk: int, D: int) -> int:
+    """Workspace of a backward whose operands have dtype code ``dtype`` (``mode`` as in
+    ``bwd_workspace_bytes``): fp32 operands need only the per-row statistics."""
+    return int(bwd_plan(dtype, B, H, Lq, Lk, D, full=mode > 0, tangent_grads=mode == 2)["workspace_bytes"])
+
+
 def workspace(nbytes: int, device: torch.device):
     """(pointer, size) of a fresh workspace of ``nbytes`` (NULL, 0 when none is needed) and the
     tensor that owns it, which the caller keeps alive until the launch is queued."""

@@ -74,7 +74,7 @@ struct Fwd32Cfg {
 // Head shapes served by attn_fwd32_kernel (the others use attn_fwd_kernel and
 // its variants, which read a transposed copy of V).
 constexpr bool fwd32_supported(int dqk, int dv) { return (dqk == 128 && dv == 128) || (dqk == 64 && dv == 64); }
-// 256-wide heads (dense launches only).
+// 256-wide heads (Dqk = Dv = 256), dense and block-sparse launches.
 constexpr bool fwd32_wide_supported(int dqk, int dv) { return dqk == 256 && dv == 256; }
 // Workgroups per query tile (column chunks of V).
 constexpr int fwd32_chunks(int mode, int d) { return d == 256 && mode != kFwdPlain ? 2 : 1; }

@@ -136,11 +136,10 @@ dmad::F32BwdFns pick_bwd_f32(int64_t d) {
 }
 
 // Bytes of the transposed, key-padded V (and Vd) copies the generic forward
-// kernels read; the kernels for 64- and 128-wide heads read V in place. At
-// 256 the dense forward reads it in place too, the block-sparse one does not:
-// this is the bound over both (plan_fwd gives one launch's size).
+// kernels read. The row-reading kernel serves every bf16/fp16 forward of 64-
+// and 128-wide heads and of Dqk = Dv = 256 heads, dense and block-sparse, and
+// reads V in place: those need no workspace (plan_fwd gives one launch's size).
 int64_t fwd_ws_bytes(int mode, int64_t B, int64_t H, int64_t Lk, int64_t Dqk, int64_t Dv) {
-  // the row-reading kernels (every forward of 64- and 128-wide heads, and of 256-wide ones) read V in place
   if (dmad::fwd32_supported((int)Dqk, (int)Dv) || dmad::fwd32_wide_supported((int)Dqk, (int)Dv)) return 0;
   const int64_t dvp = Dv < 32 ? 32 : Dv;
   const int64_t one = B * H * dvp * round_up(Lk, kLkAlign) * 2;
@@ -359,6 +358,17 @@ BwdWs bwd_ws(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) 
   return w;
 }
 
+// Workspace of a backward with operands of the given dtype. The fp32 passes
+// (dO only) make no transposed copies and keep only the log2 LSE and D
+// statistics, [BH][LQP] floats each.
+BwdWs bwd_ws_of(int dtype, int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) {
+  if (dtype != DMAD_F32) return bwd_ws(full, B, H, Lq, Lk, D);
+  BwdWs w{};
+  w.stats = round_up(B * H * round_up(Lq, 64) * 2 * 4, 256);
+  w.total = w.stats;
+  return w;
+}
+
 // Backward plan: the key-stationary pass (dK, dV), the query-stationary pass
 // (dQ [, dQd]), and with tangent gradients the dO-only passes run on (dOd, rho)
 // (the query one only where the full query pass does not give dQd).
@@ -379,7 +389,7 @@ BwdPlan plan_bwd(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int64_t
     pl.dq = "attn_f32_bwd_dq_kernel";
     pl.grid_kv = (Lk + bk - 1) / bk * BH;
     pl.grid_dq = (Lq + bm - 1) / bm * BH;
-    pl.ws = bwd_ws(0, B, H, Lq, Lk, D).total;
+    pl.ws = bwd_ws_of(DMAD_F32, 0, B, H, Lq, Lk, D).total;
     return pl;
   }
   const bool rows = full && dmad::full_reads_rows((int)D);
@@ -614,7 +624,7 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     if ((rc = check_operand("dtv", dtv, dv_strides, Lk, D, esz))) return rc;
   }
   const int fl = full ? (tgrad ? 2 : 1) : 0;
-  const BwdWs w = bwd_ws(fl, B, H, Lq, Lk, D);
+  const BwdWs w = bwd_ws_of(dtype, fl, B, H, Lq, Lk, D);
   if (use_scratch) {
     if (w.total > (int64_t)DMAD_BWD_SCRATCH_BYTES)
       return fail(DMAD_ERR_UNSUPPORTED,
@@ -631,8 +641,8 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   const int64_t dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign), BH = B * H;
   if (dp * lqp * 2 >= kMaxHeadBytes || dp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "sequence too long");
   if (f32) {
-    // fp32 (dO only): statistics [BH][LQP] (log2 LSE, then D) at the start of
-    // the workspace, which the query sizes for the bf16 path and so always holds them
+    // fp32 (dO only): the workspace holds just the statistics [BH][LQP]
+    // (log2 LSE, then D)
     const dmad::F32BwdFns f = pick_bwd_f32(D);
     if (f.prep == nullptr || f.kv == nullptr || f.dq == nullptr)
       return fail(DMAD_ERR_UNSUPPORTED, "no fp32 backward kernel for D=%lld", (long long)D);

@@ -15,7 +15,8 @@ torch's current stream. There is no CPU or PyTorch fallback.
 Differences from the reference, all additive:
   * ``tk``/``tv`` may be ``None`` (tangents of K and V known to be zero, as in
     Wan cross-attention): the forward then skips the two GEMMs they feed.
-  * backward (``set_backward_mode``): by default the reference's dO-only
+  * backward (``backward_mode`` for a scope, ``set_backward_mode`` for the
+    process default): by default the reference's dO-only
     gradients, with the reference's saved tensors (q, k, v, o, LSE; the
     cotangent of ``to`` is ignored, :535), unless a tangent requires grad: then
     the full derivative, including the cotangent of ``to`` and gradients for
@@ -28,18 +29,52 @@ Differences from the reference, all additive:
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple
+import contextlib
+import contextvars
+from typing import Iterator, Optional, Tuple
 
 import torch
 
 from . import _native as nat
 
 _BACKWARD_MODES = ("auto", "reference", "full")
-_BACKWARD_MODE = "auto"
+# process-wide default, and the mode of the innermost ``backward_mode`` scope of
+# the calling thread or task (None outside any scope)
+_DEFAULT_BACKWARD_MODE = "auto"
+_SCOPED_BACKWARD_MODE: contextvars.ContextVar = contextvars.ContextVar("dmad_backward_mode", default=None)
+
+
+def _check_backward_mode(mode: str) -> None:
+    if mode not in _BACKWARD_MODES:
+        raise ValueError(f"backward mode must be one of {_BACKWARD_MODES}, got {mode!r}")
+
+
+def current_backward_mode() -> str:
+    """The mode a forward called here would record: the innermost ``backward_mode``
+    scope of this thread or task, else the process default."""
+    m = _SCOPED_BACKWARD_MODE.get()
+    return _DEFAULT_BACKWARD_MODE if m is None else m
+
+
+@contextlib.contextmanager
+def backward_mode(mode: str) -> Iterator[None]:
+    """Scope in which forwards record ``mode`` for their backward (modes as in
+    ``set_backward_mode``). The scope belongs to the calling thread or asyncio
+    task (a ``contextvars`` variable): other threads keep their own mode, and
+    scopes nest. The mode is read when the forward runs and kept on the autograd
+    node, so a backward run after the scope has closed still follows it.
+    """
+    _check_backward_mode(mode)
+    token = _SCOPED_BACKWARD_MODE.set(mode)
+    try:
+        yield
+    finally:
+        _SCOPED_BACKWARD_MODE.reset(token)
 
 
 def set_backward_mode(mode: str) -> None:
-    """How ``attention``'s backward treats the cotangent of ``to``.
+    """Process-wide default of how ``attention``'s backward treats the cotangent
+    of ``to`` (``backward_mode`` overrides it for a scope):
 
     "auto" (default): as the reference (dO-only gradients; only q, k, v, o and
         the LSE are kept for the backward) unless a tangent requires grad; then
@@ -48,10 +83,9 @@ def set_backward_mode(mode: str) -> None:
     "full": the full derivative whenever the cotangent of ``to`` reaches the op
         (the tangents, ``to`` and mu are then kept for the backward too).
     """
-    global _BACKWARD_MODE
-    if mode not in _BACKWARD_MODES:
-        raise ValueError(f"backward mode must be one of {_BACKWARD_MODES}, got {mode!r}")
-    _BACKWARD_MODE = mode
+    global _DEFAULT_BACKWARD_MODE
+    _check_backward_mode(mode)
+    _DEFAULT_BACKWARD_MODE = mode
 
 
 def set_reference_backward(flag: bool) -> None:
@@ -66,7 +100,7 @@ FULL_BWD_MAX_HEAD_DIM = 128
 _warned_full_fallback = False
 
 
-def _full_backward_unavailable(dqk: int, dv: int, dtype: torch.dtype) -> bool:
+def _full_backward_unavailable(mode: str, dqk: int, dv: int, dtype: torch.dtype) -> bool:
     """Backward mode for inputs the full derivative does not cover (head dims
     above 128, fp32 operands).
 
@@ -78,9 +112,9 @@ def _full_backward_unavailable(dqk: int, dv: int, dtype: torch.dtype) -> bool:
     global _warned_full_fallback
     what = (f"head dims up to {FULL_BWD_MAX_HEAD_DIM} (got Dqk={dqk}, Dv={dv})" if max(dqk, dv) > FULL_BWD_MAX_HEAD_DIM
             else f"bfloat16 and float16 operands (got {dtype})")
-    if _BACKWARD_MODE == "full":
+    if mode == "full":
         raise NotImplementedError(
-            f"the full-derivative backward supports {what}; use set_backward_mode('auto') or ('reference') "
+            f"the full-derivative backward supports {what}; use backward mode 'auto' or 'reference' "
             "for the reference's dO-only gradients"
         )
     if not _warned_full_fallback:
@@ -95,28 +129,44 @@ def _full_backward_unavailable(dqk: int, dv: int, dtype: torch.dtype) -> bool:
     return False
 
 
-_strides_ok: dict = {}
+_layout_ok: dict = {}
+
+# The kernels address one (batch, head) slice with 32-bit byte offsets: the rows
+# a slice spans, plus 256 rows of slack for tile overrun, must stay under 2 GiB.
+MAX_SLICE_BYTES = 1 << 31
+
+
+def slice_fits(rows: int, row_stride: int, head_dim: int, elem_size: int) -> bool:
+    """Whether a [rows, head_dim] slice with this row stride (elements) fits the kernels'
+    32-bit offsets. Wan's BSHD views have row stride H*D, so one head of a 14B layer
+    (H=40, D=128, bf16) stops fitting at about 209k tokens; a contiguous BHSD copy (row
+    stride D) fits up to about 8.4M."""
+    return ((rows + 256) * row_stride + head_dim) * elem_size < MAX_SLICE_BYTES
 
 
 def _kernel_ready(t: torch.Tensor) -> bool:
-    """Unit inner stride, 16-byte aligned rows (what the kernels load from). The stride
-    part is a function of the stride tuple and element size, decided once per pair (this
-    sits on every call's host path)."""
+    """Unit inner stride, 16-byte aligned rows and a (batch, head) slice within the 32-bit
+    offsets (what the kernels load from). The layout part is a function of the strides, the
+    element size and the last two sizes, decided once per key (this sits on every call's
+    host path)."""
     st = t.stride()
-    key = (st, t.element_size())
-    ok = _strides_ok.get(key)
+    key = (st, t.element_size(), t.shape[-2], t.shape[-1])
+    ok = _layout_ok.get(key)
     if ok is None:
         per16 = 16 // key[1]
         ok = st[-1] == 1 and all(x % per16 == 0 for x in st[:-1])
-        if len(_strides_ok) > 4096:
-            _strides_ok.clear()
-        _strides_ok[key] = ok
+        ok = ok and slice_fits(key[2], st[-2], key[3], key[1])
+        if len(_layout_ok) > 4096:
+            _layout_ok.clear()
+        _layout_ok[key] = ok
     return ok and t.data_ptr() % 16 == 0
 
 
 def _prep(*ts):
-    """Copy operands whose layout the kernels cannot read; tangents stay
-    stride-identical to their primals because both go through the same rule."""
+    """Copy operands whose layout the kernels cannot read (among them views whose
+    (batch, head) slice spans 2 GiB or more: the copy is contiguous BHSD, whose slice is
+    only L*D elements); tangents stay stride-identical to their primals because both go
+    through the same rule."""
     return tuple(None if t is None else (t if _kernel_ready(t) else t.contiguous()) for t in ts)
 
 
@@ -288,7 +338,7 @@ def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_sc
     dtv = torch.empty_like(dv) if tgrads else None
     lib = nat.lib()
     ws_mode = (2 if tgrads else 1) if full else 0
-    ws_ptr, ws_size, ws = nat.workspace(nat.bwd_workspace_bytes(ws_mode, B, H, Lq, Lk, D), q.device)
+    ws_ptr, ws_size, ws = nat.workspace(nat.bwd_workspace_bytes_of(code, ws_mode, B, H, Lq, Lk, D), q.device)
     nat.check(
         lib.dmad_attn_jvp_bwd(
             code, B, H, Lq, Lk, D,
@@ -344,10 +394,11 @@ class _attention(torch.autograd.Function):
         # the full derivative needs the tangent side; otherwise keep only what the
         # reference keeps (q, k, v, o, LSE: :500-502), so tangent activations and
         # `to` are not held until the backward
-        full = _BACKWARD_MODE == "full" or (_BACKWARD_MODE == "auto" and tangent_grad)
+        mode = current_backward_mode()
+        full = mode == "full" or (mode == "auto" and tangent_grad)
         if full and (is_grad or tangent_grad) and (max(HEAD_DIM_QK, HEAD_DIM_V) > FULL_BWD_MAX_HEAD_DIM
                                                    or q.dtype == torch.float32):
-            full = _full_backward_unavailable(HEAD_DIM_QK, HEAD_DIM_V, q.dtype)
+            full = _full_backward_unavailable(mode, HEAD_DIM_QK, HEAD_DIM_V, q.dtype)
         # an output that does not reach the loss arrives in backward as None
         # (not zeros), so an unused `to` keeps the dO-only kernel
         ctx.set_materialize_grads(False)

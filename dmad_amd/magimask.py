@@ -262,9 +262,11 @@ def prepare_magi_csr_and_tasks(q_ranges: torch.Tensor, k_ranges: torch.Tensor, Q
     q_ranges, k_ranges = merge_k_ranges(q_ranges, k_ranges, KV_real=KV_real)
     q_unique, k_flat, qk_map = group_q_ranges_csr(q_ranges, k_ranges)
     qu = _host(q_unique)
-    assert len(qu) > 0 and qu[0, 0] == 0 and qu[-1, 1] == Q_real, "q_unique does not cover [0,Q_real)."
+    assert len(qu) > 0 and qu[0, 0] == 0 and qu[-1, 1] == Q_real, \
+        f"the query groups must start at row 0 and end at row {Q_real} (Q_real)"
     for i in range(len(qu) - 1):
-        assert qu[i, 1] == qu[i + 1, 0], f"q_unique has gap/overlap at i={i}: {qu[i]} vs {qu[i + 1]}"
+        assert qu[i, 1] == qu[i + 1, 0], \
+            f"query groups {i} and {i + 1} do not meet: {qu[i].tolist()} then {qu[i + 1].tolist()}"
     task_group, task_qtile = build_qtile_tasks(q_unique, Q_real=Q_real, BLOCK_M=BLOCK_M)
     return MagiMask(q_unique=q_unique.contiguous(), k_flat=k_flat.contiguous(), qk_map=qk_map.contiguous(),
                     task_group=task_group, task_qtile=task_qtile, G=int(qu.shape[0]), T=int(task_group.numel()),

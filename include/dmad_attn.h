@@ -121,7 +121,9 @@ int dmad_attn_fwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64
  * (dto, dtq, dtk, dtv given). The per-row statistics always; transposed copies
  * of Q, dO, K (and the tangents) for the full derivative of head dims other
  * than 128 and for the dO-only gradients of head dims other than 64 and 128.
- * The size holds for every dtype (fp32 uses only the statistics part). */
+ * The size is that of bf16/fp16 operands and bounds every dtype: fp32 operands
+ * need only the statistics, round_up(B*H*round_up(Lq,64)*8, 256) bytes
+ * (dmad_attn_bwd_plan reports the exact figure for each dtype). */
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes);
 
 /*
@@ -158,8 +160,8 @@ int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, i
  * errors as dmad_attn_jvp_bwd without the workspace: the per-row statistics
  * (and any transposed copies) go to a static device array of
  * DMAD_BWD_SCRATCH_BYTES in the library, one copy per GPU, held until the
- * process ends. Problems whose dmad_attn_bwd_workspace_bytes exceeds that size
- * fail with DMAD_ERR_UNSUPPORTED (e.g. the dO-only backward of 64- and 128-wide
+ * process ends. Problems whose workspace (dmad_attn_bwd_plan's workspace_bytes
+ * for the dtype) exceeds that size fail with DMAD_ERR_UNSUPPORTED (e.g. the dO-only backward of 64- and 128-wide
  * heads fits up to B*H*Lq ~ 8.4M rows: Wan2.1-14B at 720p needs 24 MB; the full
  * derivative of 128-wide heads with tangent gradients up to ~2.8M rows). The
  * call allocates nothing; the first call on a device looks up that device's

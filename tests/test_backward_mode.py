@@ -66,3 +66,62 @@ def test_wide_heads_raise_in_forward_in_full_mode():
     with pytest.raises(NotImplementedError, match="head dims up to 128"):
         _saved_d(256, False)
     assert _saved_d(128, False) == (10, True)
+
+
+def test_scoped_mode_overrides_the_default_and_nests():
+    from dmad_amd import backward_mode, current_backward_mode
+
+    assert current_backward_mode() == "auto"
+    with backward_mode("full"):
+        assert _saved(False) == (10, True)
+        with backward_mode("reference"):
+            assert _saved(True) == (5, False)
+        assert current_backward_mode() == "full"
+    assert current_backward_mode() == "auto"
+    assert _saved(False) == (5, False)
+    # a scope wins over the process default while it is open
+    set_backward_mode("full")
+    with backward_mode("auto"):
+        assert _saved(False) == (5, False)
+    assert _saved(False) == (10, True)
+    with pytest.raises(ValueError, match="backward mode"):
+        with backward_mode("exact"):
+            pass
+
+
+def test_scoped_mode_is_local_to_its_thread():
+    """A scope opened in one thread leaves the forwards of another thread on the
+    process default."""
+    import threading
+
+    from dmad_amd import backward_mode
+
+    entered, release = threading.Event(), threading.Event()
+    seen = {}
+
+    def worker():
+        with backward_mode("full"):
+            seen["worker"] = _saved(False)
+            entered.set()
+            release.wait(10)
+
+    t = threading.Thread(target=worker)
+    t.start()
+    assert entered.wait(10)
+    seen["main"] = _saved(False)
+    release.set()
+    t.join(10)
+    assert seen == {"worker": (10, True), "main": (5, False)}
+
+
+def test_mode_is_recorded_by_the_forward():
+    """The node keeps the mode of the scope its forward ran in."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from dmad_amd import backward_mode
+
+    with FakeTensorMode():
+        xs = [torch.empty(1, 2, 64, 32, dtype=torch.bfloat16).requires_grad_(i < 3) for i in range(6)]
+        with backward_mode("full"):
+            o, _ = _attention.apply(*xs)
+        assert o.grad_fn.full is True

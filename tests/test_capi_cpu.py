@@ -305,6 +305,20 @@ def test_bwd_noalloc_rejects_problems_beyond_its_scratch(nat):
     assert n.value <= nat.BWD_SCRATCH_BYTES
 
 
+def test_bwd_noalloc_sizes_fp32_by_its_statistics(nat):
+    """fp32 operands need only the per-row statistics (B=1, H=32, L=2048: 512 KiB), so the
+    size gate of the allocation-free backward passes a 256-wide fp32 problem that the
+    bf16 sizing (transposed Q, dO copies) would refuse. Without a GPU the call then stops
+    at the device lookup, never at the scratch size."""
+    st = _strides(32 * 2048 * 256, 2048 * 256, 256, 1)
+    rc = _bwd_noalloc(nat, dtype=2, B=1, H=32, Lq=2048, Lk=2048, D=256, qs=st, ks=st, vs=st, os=st, dos=st, dqs=st,
+                      dks=st, dvs=st)
+    assert "static scratch" not in nat.lib().dmad_last_error().decode()
+    assert rc in (0, 4)
+    assert nat.bwd_plan(nat.DMAD_F32, 1, 32, 2048, 2048, 256)["workspace_bytes"] == 32 * 2048 * 8
+    assert nat.bwd_workspace_bytes(0, 1, 32, 2048, 2048, 256) > nat.BWD_SCRATCH_BYTES
+
+
 @pytest.mark.parametrize("over,code,needle", [(dict(dtype=7), 2, "dtype"), (dict(q=0), 1, "q: null"),
                                               (dict(D=48), 2, "head dim")])
 def test_bwd_noalloc_rejects_bad_arguments(nat, over, code, needle):

@@ -251,9 +251,10 @@ def test_wan13b_cross_attention_full_size(gpu):
 
 
 def test_wan14b_cross_attention_full_size(gpu):
-    """Wan2.1-14B text cross-attention: H=40, 32760 queries over 512 keys, Kd = Vd = 0."""
-    print("case wan14b cross fwd+JVP", flush=True)
-    x = make_inputs(1, 40, 32760, 512, 128, seed=1, device=gpu, gen_device=gpu)
+    """Wan2.1-14B text cross-attention: H=40, 32760 queries over 512 keys, Kd = Vd = 0, on
+    the tensors the benchmark times (the CPU generator seeded 1)."""
+    print("case wan14b cross fwd+JVP (benchmark inputs)", flush=True)
+    x = make_inputs(1, 40, 32760, 512, 128, seed=1, device=gpu)
     (o, to, lse, mu), _, s = _run(x, tangents=False)
     _check_fwd(o, to, lse, mu, x["q"], x["k"], x["v"], x["tq"], None, None, heads=(0, 17, 39), sm_scale=s)
 
@@ -270,11 +271,42 @@ def test_wan14b_720p_self_attention_full_size(gpu):
     _check_bwd(dq, dk, dv, x["q"], x["k"], x["v"], x["do"], heads=(0, 26), sm_scale=s)
 
 
-def test_wan14b_self_attention_bench_shape(gpu):
-    """The benchmark workload itself (H=40, L=32760): one head against the oracle, identities on all."""
-    print("case wan14b self fwd+JVP+bwd", flush=True)
-    x = make_inputs(1, 40, 32760, 32760, 128, seed=0, device=gpu, grid=(21, 30, 52), with_grads=True, gen_device=gpu)
+@pytest.fixture(scope="module")
+def bench_inputs(gpu):
+    """The exact tensors the benchmark step times: B=1, H=40, L=32760, D=128, bf16, drawn on
+    the CPU generator seeded 0 in the order Q, K, V, Qd, Kd, Vd, dO, dOd, Q and K
+    RMS-normalised and rotated with 3D RoPE over the 21x30x52 latent grid."""
+    print("drawing the benchmark inputs on the CPU generator", flush=True)
+    x = make_inputs(1, 40, 32760, 32760, 128, seed=0, device=gpu, grid=(21, 30, 52), with_grads=True)
+    yield x
+    del x
+    torch.cuda.empty_cache()
+
+
+def test_wan14b_self_attention_bench_shape(gpu, bench_inputs):
+    """The benchmark workload on the benchmark's own inputs (H=40, L=32760): forward+JVP and
+    the dO-only backward, two heads against the oracle, the identities on all 40."""
+    print("case wan14b self fwd+JVP+bwd (benchmark inputs)", flush=True)
+    x = bench_inputs
     (o, to, lse, mu), (dq, dk, dv), s = _run(x, backward=True)
     args = (x["q"], x["k"], x["v"], x["tq"], x["tk"], x["tv"])
-    _check_fwd(o, to, lse, mu, *args, heads=(39,), sm_scale=s)
-    _check_bwd(dq, dk, dv, x["q"], x["k"], x["v"], x["do"], heads=(20,), sm_scale=s)
+    _check_fwd(o, to, lse, mu, *args, heads=(0, 39), sm_scale=s)
+    _check_rows_against_cpu(o, to, *args, h=21, rows=[0, 1, 2047, 16380, 32758, 32759], sm_scale=s)
+    _check_bwd(dq, dk, dv, x["q"], x["k"], x["v"], x["do"], heads=(20, 39), sm_scale=s)
+
+
+def test_wan14b_self_attention_full_derivative_bench_inputs(gpu, bench_inputs):
+    """The full derivative (all six gradients, as the benchmark's full-derivative field
+    times it) at the 14B head count on the benchmark's inputs: two heads against the
+    oracle, the identities on all 40."""
+    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+
+    print("case wan14b self fwd+JVP+full bwd (benchmark inputs)", flush=True)
+    x = bench_inputs
+    q, k, v, tq, tk, tv = (x[n] for n in ("q", "k", "v", "tq", "tk", "tv"))
+    s = 128 ** -0.5
+    o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
+    grads = jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, x["do"], x["dto"], s, True)
+    torch.cuda.synchronize()
+    assert all(g is not None for g in grads)
+    _check_bwd_full(grads, x, heads=(7, 33), sm_scale=s)

@@ -152,6 +152,17 @@ def test_backward_passes():
 
 
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+def test_fp32_backward_workspace_is_the_statistics(D):
+    # fp32 passes read Q, dO, K in place: the workspace holds only the log2 LSE and D per
+    # query row, [B*H][round_up(Lq, 64)] floats each (4 MiB at B=4, H=32, L=4096)
+    b = nat.bwd_plan(F32, 4, 32, 4096, 4096, D)
+    assert (b["workspace_bytes"], b["transposed_copies"]) == (4 * 32 * 4096 * 2 * 4, 0)
+    assert nat.bwd_plan(F32, 1, 3, 999, 515, D)["workspace_bytes"] == (3 * 1024 * 8 + 255) // 256 * 256
+    # the dtype-free query bounds it (it sizes bf16/fp16 operands)
+    assert b["workspace_bytes"] <= nat.bwd_workspace_bytes(0, 4, 32, 4096, 4096, D)
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("Lq,Lk", [(999, 515), (32760, 512), (1, 1)])
 def test_workspace_matches_the_queries(D, Lq, Lk):
     for mode in (PLAIN, JVP, QONLY):

@@ -3,7 +3,7 @@ static device scratch, called through the C ABI, against dmad_attn_jvp_bwd
 with a caller workspace on the same inputs. Same kernels, same statistics:
 the gradients must be bitwise equal. Two calls in a row, the second smaller
 than the first (the scratch keeps the first call's contents), then the first
-shape again, and an fp32 call (its statistics in the same scratch)."""
+shape again, and fp32 calls (their statistics in the same scratch)."""
 import ctypes
 
 import pytest
@@ -55,6 +55,8 @@ CALLS = [
     (1, 2, 300, 64, False, torch.bfloat16),
     (2, 3, 700, 128, True, torch.bfloat16),
     (1, 2, 257, 32, False, torch.float32),
+    # fp32 with 256-wide heads needs only its statistics (512 KiB here), well inside the scratch
+    (1, 32, 2048, 256, False, torch.float32),
 ]
 
 
