@@ -93,6 +93,8 @@ def _args():
                          "and the same at head dims 16, 32 and 256")
     ap.add_argument("--harness-dims", default="16,32,64,128,256",
                     help="head dims the --harness timing covers (comma-separated; default all five)")
+    ap.add_argument("--no-ceiling", dest="ceiling", action="store_false",
+                    help="skip the MFMA ceiling probe after the timed steps (extra field)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run one elementwise kernel that reads and writes this many MiB "
                          "(a known-size reference for HBM byte counters under a profiler)")
@@ -261,12 +263,18 @@ def full_bwd_timing(q, k, v, tq, tk, tv, do, dto):
     return res
 
 
-def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384), dtype=None):
+def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384), dtype=None, as_reference=False):
     """The configuration of the reference's own perf_report harness
     (flash_attention_jvp_triton.py:662-725): B=4, H=32, fp16, L = 1024..16384,
     forward+JVP and its backward, with the harness's flop convention (12 and 10
     units of B*H*L^2*D). The reference publishes no result for it. With
-    dtype=float32 the same on the fp32 kernels, against the fp32 MFMA peak."""
+    dtype=float32 the same on the fp32 kernels, against the fp32 MFMA peak.
+
+    By default Q, K, V, the tangents and dO are N(0,1) and sm_scale = D^-0.5.
+    as_reference=True takes the harness's own values (:686-698): Q, K, V, dO
+    ~ N(0,1), zero tangent tensors (the full six-GEMM forward still runs) and
+    sm_scale = 1.3, whose logits are about 10x larger, so the online softmax
+    raises its running maximum, and rescales, far more often."""
     import torch
 
     from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
@@ -280,6 +288,9 @@ def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384), dtype=Non
         q, k, v, tq, tk, tv, do = (torch.randn((B, H, L, D), device=dev, dtype=dtype, generator=g)
                                    for _ in range(7))
         s = D ** -0.5
+        if as_reference:
+            tq, tk, tv = (torch.zeros_like(x) for x in (q, k, v))
+            s = 1.3
         o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
         jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, None, s, False)
         torch.cuda.synchronize()
@@ -302,7 +313,39 @@ def harness_timing(dev, D=64, lengths=(1024, 2048, 4096, 8192, 16384), dtype=Non
                      "bwd_TFLOPs": round(tf_b, 1), "bwd_pct_peak": round(100 * tf_b / peak, 1)})
         del q, k, v, tq, tk, tv, do, o, to, lse, mu
     return {"B": 4, "H": 32, "D": D, "dtype": "fp32" if dtype == torch.float32 else "fp16", "peak_TFLOPs": peak,
+            "sm_scale": 1.3 if as_reference else "D^-0.5", "tangents": "zeros" if as_reference else "N(0,1)",
             "rows": rows}
+
+
+def mfma_ceiling(dev, kernel_tflops):
+    """The board's practical MFMA rate, measured right after the timed steps: the
+    library's probe kernel (dmad_probe_mfma) runs back-to-back bf16 32x32x16 MFMAs,
+    one workgroup of four waves per CU, about 3.5 ms per launch, under the same
+    power limit as the attention kernels. Reported with each main kernel's rate as
+    a fraction of it."""
+    import torch
+
+    from dmad_amd import _native
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    per_wave = 256 * 750  # 192000 MFMAs: ~3.3 ms at 1.86 GHz
+    sink = torch.empty(cus * 256, device=dev, dtype=torch.float32)
+    stream = _native.stream_ptr(dev)
+    lib = _native.lib()
+    for _ in range(3):
+        _native.check(lib.dmad_probe_mfma(_native.DMAD_BF16, cus, per_wave, _native.ptr(sink), stream))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    e0.record()
+    for _ in range(reps):
+        _native.check(lib.dmad_probe_mfma(_native.DMAD_BF16, cus, per_wave, _native.ptr(sink), stream))
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    tflops = cus * 4 * per_wave * 32768.0 / (ms * 1e-3) / 1e12
+    return {"kernel": "mfma_probe_kernel<bf16>", "cus": cus, "ms_per_launch": round(ms, 3),
+            "TFLOPs": round(tflops, 1), "pct_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+            "kernels_pct_of_ceiling": {n: round(100 * t / tflops, 1) for n, t in kernel_tflops.items()}}
 
 
 def magi_timing(H, D, dev):
@@ -517,6 +560,8 @@ def main():
         # skip the first 0.5 s of each window: the clock settles after a change of load
         out["power"] = {name: _power_summary(power_file, a + 0.5, b) for name, (a, b) in windows.items()}
         os.unlink(power_file)
+    if args.ceiling:
+        out["mfma_ceiling"] = mfma_ceiling(dev, {n: k_flops[n] / (k_ms[n] * 1e-3) / 1e12 for n in k_ms})
     if args.full_bwd:
         out["full_derivative_bwd"] = full_bwd_timing(q, k, v, tq, tk, tv, do, x["dto"])
     # fused RMSNorm(+JVP) + RoPE prologue that produces q and k for this layer,
@@ -530,6 +575,9 @@ def main():
     if args.harness:
         dims = {int(d) for d in args.harness_dims.split(",") if d}
         out["reference_harness"] = [harness_timing(dev, D=d) for d in (64, 128) if d in dims]
+        # the harness's own inputs: sm_scale = 1.3, zero tangents (:686-698)
+        out["reference_harness_as_written"] = [harness_timing(dev, D=d, as_reference=True) for d in (64, 128)
+                                               if d in dims]
         # the other head dims the reference accepts (:471-472): 16 and 32 on the generic kernels, 256 on the
         # row-reading forward, the generic dK/dV pass and the row-reading dQ pass
         out["other_head_dims"] = [harness_timing(dev, D=d, lengths=(1024, 4096, 16384)) for d in (16, 32, 256)

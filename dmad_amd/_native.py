@@ -81,6 +81,7 @@ SIGNATURES = {
     "dmad_attn_fwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P,
                              _I64P, _I64P, _I64P, _P, _I64P, _P, _F, _P, _SZ, _P]),
     "dmad_set_kernel_events": (_INT, [ctypes.POINTER(ctypes.c_void_p), _INT]),
+    "dmad_probe_mfma": (_INT, [_INT, _I64, _I64, _P, _P]),
     "dmad_rmsnorm_rope_jvp": (_INT, [_INT, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _FP, _F, _P, _P, _I64, _P]),
     "dmad_attn_bwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _SZP]),
     "dmad_attn_fwd_plan": (_INT, [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.POINTER(Plan)]),

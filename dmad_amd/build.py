@@ -55,7 +55,8 @@ COMMON_FLAGS = [
 
 def units():
     """(source, object name, extra flags) for every compilation unit."""
-    out = [("capi.hip", "capi", []), ("aux.hip", "aux", []), ("prologue.hip", "prologue", [])]
+    out = [("capi.hip", "capi", []), ("aux.hip", "aux", []), ("prologue.hip", "prologue", []),
+           ("probe.hip", "probe", [])]
     for t, tname in ((0, "bf16"), (1, "f16")):
         out.append(("fwd32_inst.hip", f"fwd32_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))
         out.append(("bwd_dq_inst.hip", f"bwd_dq_{tname}", [f"-DDMAD_T={t}", "-mllvm", "-amdgpu-mfma-vgpr-form"]))

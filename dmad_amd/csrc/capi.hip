@@ -1038,4 +1038,16 @@ int dmad_rmsnorm_rope_jvp(int dtype, int64_t rows, int64_t L, int64_t H, int64_t
   return ok();
 }
 
+int dmad_probe_mfma(int dtype, int64_t blocks, int64_t mfmas_per_wave, float* sink, void* stream) {
+  if (dtype != DMAD_BF16 && dtype != DMAD_F16) return fail(DMAD_ERR_UNSUPPORTED, "the MFMA probe takes bf16 or fp16");
+  if (blocks < 1 || blocks > (1 << 20)) return fail(DMAD_ERR_INVALID, "blocks must be in [1, 2^20]");
+  if (mfmas_per_wave < 256 || mfmas_per_wave % 256 != 0 || mfmas_per_wave > ((int64_t)1 << 30))
+    return fail(DMAD_ERR_INVALID, "mfmas_per_wave must be a positive multiple of 256 up to 2^30");
+  if (sink == nullptr) return fail(DMAD_ERR_INVALID, "sink: null pointer");
+  const hipError_t e = dmad::launch_mfma_probe(dtype == DMAD_F16, (int)blocks, (int)(mfmas_per_wave / 256), sink,
+                                               (hipStream_t)stream);
+  if (e != hipSuccess) return fail(DMAD_ERR_HIP, "probe launch: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

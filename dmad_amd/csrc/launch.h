@@ -184,6 +184,9 @@ struct PrologueParams {
 hipError_t launch_rmsnorm_rope(const PrologueParams& p, int dtype, hipStream_t s);
 
 hipError_t launch_transpose_pad(const TransposeParams& p, int BH, hipStream_t s);
+// MFMA ceiling probe (probe.hip): `blocks` workgroups of 4 waves, each wave 256 * rounds
+// back-to-back 32x32x16 MFMAs (bf16, or fp16 when f16).
+hipError_t launch_mfma_probe(bool f16, int blocks, int rounds, float* sink, hipStream_t s);
 hipError_t launch_bwd_prep(const PrepParams& p, int dtype, hipStream_t s);
 
 // ---------------------------------------------------------------- kernel choice per shape

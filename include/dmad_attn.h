@@ -248,6 +248,18 @@ int dmad_attn_bwd_plan(int dtype, int full, int tangent_grads, int64_t B, int64_
  */
 int dmad_set_kernel_events(void* const* events, int count);
 
+/*
+ * MFMA ceiling probe (no counterpart in the reference; a measurement aid for
+ * benchmarks). Launches `blocks` workgroups of four waves on `stream`; every
+ * wave issues `mfmas_per_wave` (a multiple of 256) back-to-back 32x32x16 MFMAs
+ * of the dtype (DMAD_BF16 or DMAD_F16, 32768 flops each) on four independent
+ * accumulators, with new operand bits every 32 MFMAs, and writes one float per
+ * thread to `sink` (blocks * 256 floats). With one workgroup per CU it runs the
+ * matrix units flat out under the board's power limit: the MFMA rate the
+ * attention kernels can be measured against on the same board.
+ */
+int dmad_probe_mfma(int dtype, int64_t blocks, int64_t mfmas_per_wave, float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -328,3 +328,11 @@ def test_bwd_noalloc_rejects_bad_arguments(nat, over, code, needle):
 
 def test_bwd_noalloc_empty_problem_is_a_no_op(nat):
     assert _bwd_noalloc(nat, B=0) == 0
+
+
+@pytest.mark.parametrize("args,code,needle", [((7, 1, 256), 2, "bf16 or fp16"), ((0, 0, 256), 1, "blocks"),
+                                              ((0, 1, 100), 1, "multiple of 256"), ((1, 1, 0), 1, "multiple")])
+def test_mfma_probe_rejects_bad_arguments(nat, args, code, needle):
+    assert nat.lib().dmad_probe_mfma(*args, ctypes.c_void_p(256), ctypes.c_void_p(0)) == code
+    assert needle in nat.lib().dmad_last_error().decode()
+    assert nat.lib().dmad_probe_mfma(0, 1, 256, ctypes.c_void_p(0), ctypes.c_void_p(0)) == 1

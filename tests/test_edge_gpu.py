@@ -181,3 +181,15 @@ def test_repeat_runs_are_bitwise_equal(gpu, D):
     r1, r2 = attention(*g, None, mask), attention(*g, None, mask)
     torch.cuda.synchronize()
     assert torch.equal(r1[0], r2[0]) and torch.equal(r1[1], r2[1])
+
+
+@pytest.mark.parametrize("dtype_code", [0, 1])
+def test_mfma_probe_runs(gpu, dtype_code):
+    """The ceiling probe the benchmark times (dmad_probe_mfma): a short launch on two
+    workgroups finishes and writes one finite float per thread."""
+    from dmad_amd import _native as nat
+
+    sink = torch.full((2 * 256,), float("nan"), device=gpu)
+    nat.check(nat.lib().dmad_probe_mfma(dtype_code, 2, 512, nat.ptr(sink), nat.stream_ptr(gpu)))
+    torch.cuda.synchronize()
+    assert torch.isfinite(sink).all()
