@@ -49,10 +49,21 @@ def _check_backward_mode(mode: str) -> None:
         raise ValueError(f"backward mode must be one of {_BACKWARD_MODES}, got {mode!r}")
 
 
+@torch._dynamo.assume_constant_result
+def _scoped_mode_at_trace() -> Optional[str]:
+    return _SCOPED_BACKWARD_MODE.get()
+
+
 def current_backward_mode() -> str:
     """The mode a forward called here would record: the innermost ``backward_mode``
-    scope of this thread or task, else the process default."""
-    m = _SCOPED_BACKWARD_MODE.get()
+    scope of this thread or task, else the process default.
+
+    Under ``torch.compile`` the scope is read once, when the graph is traced
+    (TorchDynamo cannot trace a context variable); the process default is a
+    module global, which the compiled graph guards on, so ``set_backward_mode``
+    retraces it.
+    """
+    m = _scoped_mode_at_trace() if torch.compiler.is_compiling() else _SCOPED_BACKWARD_MODE.get()
     return _DEFAULT_BACKWARD_MODE if m is None else m
 
 

@@ -125,3 +125,30 @@ def test_mode_is_recorded_by_the_forward():
         with backward_mode("full"):
             o, _ = _attention.apply(*xs)
         assert o.grad_fn.full is True
+
+
+def test_mode_read_traces_under_torch_compile():
+    """TorchDynamo cannot trace a context variable: under torch.compile the scope is
+    read once at trace time, and the process default is a guarded global, so
+    set_backward_mode makes the compiled function retrace (fullgraph: no break)."""
+    import torch._dynamo
+
+    from dmad_amd import backward_mode
+    from dmad_amd.jvp_attention import current_backward_mode
+
+    torch._dynamo.reset()
+
+    def f(x):
+        return x + (1.0 if current_backward_mode() == "full" else 2.0)
+
+    cf = torch.compile(f, backend="eager", fullgraph=True)
+    x = torch.zeros(2)
+    assert cf(x).tolist() == [2.0, 2.0]
+    set_backward_mode("full")
+    assert cf(x).tolist() == [1.0, 1.0]
+    set_backward_mode("auto")
+    assert cf(x).tolist() == [2.0, 2.0]
+    torch._dynamo.reset()
+    with backward_mode("full"):
+        assert cf(x).tolist() == [1.0, 1.0]
+    torch._dynamo.reset()
