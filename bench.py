@@ -271,7 +271,9 @@ def _do_bench(fn, flush, rep_ms=100.0, warmup_ms=25.0):
     warm-up calls and 100 ms of timed calls, at least 3 and at most 1000."""
     import torch
 
-    fn()
+    for _ in range(3):  # first calls (lazy code-object loads, allocator growth) stay out of the estimate
+        flush.zero_()
+        fn()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
