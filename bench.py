@@ -206,15 +206,17 @@ def plain_timing(q, k, v, do, dev):
     import torch
 
     from dmad_amd import _native
-    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+    from dmad_amd.jvp_attention import backward_plan, jvp_attention_backward, jvp_attention_forward
 
     s = q.shape[-1] ** -0.5
     o, _, lse, _ = jvp_attention_forward(q, k, v, None, None, None, s)
     jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
     torch.cuda.synchronize()
+    B, H, L, D = q.shape
+    bplan = backward_plan(q.dtype, B, H, L, L, D)
     best_f = best_b = float("inf")
     for _ in range(3):
-        tf, tb = _native.KernelTimer(1), _native.KernelTimer(2)
+        tf, tb = _native.KernelTimer(1), _native.KernelTimer(2 * bplan["pairs"])
         with tf:
             o, _, lse, _ = jvp_attention_forward(q, k, v, None, None, None, s)
         with tb:
@@ -222,10 +224,9 @@ def plain_timing(q, k, v, do, dev):
         torch.cuda.synchronize()
         best_f = min(best_f, tf.elapsed()[0])
         best_b = min(best_b, sum(tb.elapsed()))
-    B, H, L, D = q.shape
     unit = B * H * L * L * D
     tfs = 14.0 * unit / ((best_f + best_b) * 1e-3) / 1e12
-    return {"kernels": "attn_fwd32_kernel<bf16,plain> + attn_bwd_kv_tr_kernel + attn_bwd_dq_tr_kernel",
+    return {"kernels": f"attn_fwd32_kernel<bf16,plain> + {bplan['kernel']} + {bplan['kernel2']}",
             "ms_fwd": round(best_f, 3), "ms_bwd": round(best_b, 3),
             "fwd_pct_peak": round(100 * 4.0 * unit / (best_f * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
             "TFLOPs_fwd_bwd": round(tfs, 1), "pct_peak_fwd_bwd": round(100 * tfs / PEAK_BF16_TFLOPS, 2)}
@@ -244,8 +245,12 @@ def full_bwd_timing(q, k, v, tq, tk, tv, do, dto):
     o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
     B, H, L, D = q.shape
     unit = B * H * L * L * D
-    res = {"kernels": "bwd_prep_kernel + attn_bwd_kv_full_kernel + attn_bwd_dq_full_kernel "
-                      "[+ attn_bwd_kv_tr_kernel for the tangents' dK, dV]"}
+    from dmad_amd.jvp_attention import backward_plan
+
+    bplan = backward_plan(q.dtype, B, H, L, L, D, full=True, tangent_grads=True)
+    res = {"kernels": f"bwd_prep_kernel + {bplan['kernel']} + {bplan['kernel2']} "
+                      f"[+ {bplan['kernel3']} for the tangents' dK, dV]",
+           "score_slices_per_pair": bplan["score_slices"]}
     for tg, units, name in ((False, 24.0, "dq_dk_dv"), (True, 30.0, "all_six")):
         jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, do, dto, s, tg)
         torch.cuda.synchronize()
@@ -447,7 +452,7 @@ def main():
 
     sys.path.insert(0, ROOT)
     from dmad_amd import _native
-    from dmad_amd.jvp_attention import jvp_attention_backward, jvp_attention_forward
+    from dmad_amd.jvp_attention import backward_plan, jvp_attention_backward, jvp_attention_forward
     from dmad_amd.workload import make_inputs
 
     dev = torch.device("cuda:0")
@@ -467,11 +472,14 @@ def main():
     f_cross = 8.0 * H * L * LKX * D
     f_step = f_fwd + f_bwd + f_cross
 
+    # the dO-only backward's passes: with stored score gradients the key and query
+    # passes run once per group of (b, h) slices ("pairs"), timed pair by pair
+    bplan = backward_plan(torch.bfloat16, 1, H, L, L, D)
     timers = []
 
     def step(record):
         if record:
-            tf, tb, tc = _native.KernelTimer(1), _native.KernelTimer(2), _native.KernelTimer(1)
+            tf, tb, tc = _native.KernelTimer(1), _native.KernelTimer(2 * bplan["pairs"]), _native.KernelTimer(1)
             timers.append((tf, tb, tc))
             with tf:
                 o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
@@ -502,16 +510,20 @@ def main():
     for tf, tb, tc in timers:
         k_ms["fwd"] += tf.elapsed()[0] / len(timers)
         b = tb.elapsed()
-        k_ms["bwd_dkdv"] += b[0] / len(timers)
-        k_ms["bwd_dq"] += b[1] / len(timers)
+        k_ms["bwd_dkdv"] += sum(b[0::2]) / len(timers)
+        k_ms["bwd_dq"] += sum(b[1::2]) / len(timers)
         k_ms["cross"] += tc.elapsed()[0] / len(timers)
     value = f_step / (ms_step * 1e-3) / 1e12
 
-    # algorithmic flops of each main kernel (GEMM flops it must do, counting the
-    # S and dP recomputation of the dQ pass)
-    k_flops = {"fwd": f_fwd, "bwd_dkdv": 8.0 * H * L * L * D, "bwd_dq": 6.0 * H * L * L * D, "cross": f_cross}
-    k_names = {"fwd": "attn_fwd32_kernel<bf16,jvp>", "bwd_dkdv": "attn_bwd_kv_tr_kernel<bf16,128>",
-               "bwd_dq": "attn_bwd_dq_tr_kernel<bf16,128>", "cross": "attn_fwd32_x2_kernel<bf16>"}
+    # algorithmic flops of each main kernel (GEMM flops it must do: the recomputing dQ
+    # pass counts its S and dP recomputation, the stored-score one only dQ = s dS K)
+    sc = bplan["score_slices"] > 0
+    k_flops = {"fwd": f_fwd, "bwd_dkdv": 8.0 * H * L * L * D, "bwd_dq": (2.0 if sc else 6.0) * H * L * L * D,
+               "cross": f_cross}
+    k_names = {"fwd": "attn_fwd32_kernel<bf16,jvp>",
+               "bwd_dkdv": "attn_bwd_kv_tr_kernel<bf16,128,store>" if sc else "attn_bwd_kv_tr_kernel<bf16,128>",
+               "bwd_dq": "attn_bwd_dq_sc_kernel<bf16,1>" if sc else "attn_bwd_dq_tr_kernel<bf16,128>",
+               "cross": "attn_fwd32_x2_kernel<bf16>"}
     dom = max(k_ms, key=k_ms.get)
     dom_flops, dom_name = k_flops[dom], k_names[dom]
     achieved = dom_flops / (k_ms[dom] * 1e-3) / 1e12
@@ -540,6 +552,8 @@ def main():
         "ms_self_bwd_dkdv_kernel": round(k_ms["bwd_dkdv"], 3),
         "ms_self_bwd_dq_kernel": round(k_ms["bwd_dq"], 3),
         "ms_cross_fwd_jvp_kernel": round(k_ms["cross"], 4),
+        "bwd_kernels": {"dkdv": k_names["bwd_dkdv"], "dq": k_names["bwd_dq"], "pairs": bplan["pairs"],
+                        "score_slices_per_pair": bplan["score_slices"]},
         "kernel_pct_peak": {n: round(100 * k_flops[n] / (k_ms[n] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
                             for n in k_ms},
         "roofline": {
@@ -553,6 +567,12 @@ def main():
         },
         "wall_s_timed": round(wall, 3),
     }
+    if sc:
+        # the stored-score query pass streams the dS tiles from HBM once: its bound is HBM
+        sc_bytes = H * _native.bwd_score_bytes(_native.DMAD_BF16, False, L, L, D)
+        tbs = sc_bytes / (k_ms["bwd_dq"] * 1e-3) / 1e12
+        out["bwd_dq_hbm"] = {"bytes_read": sc_bytes, "achieved_TBps": round(tbs, 3), "peak_TBps": 8.0,
+                             "frac": round(tbs / 8.0, 4)}
     if sampler is not None and not args.power:
         # mean GFX clock and board power over the timed steps: the board runs at its power
         # limit, so the clock (not only the kernels) sets the step time. amd-smi gives about

@@ -14,8 +14,8 @@ and the attention helpers of train/wan/rcm/utils/jvp_helper.py):
 * ``apply_rope_with_tangent``       -- interleaved RoPE of a BSHD pair, differentiable
 """
 from .jvp_attention import (  # noqa: F401
-    _attention, attention, backward_mode, current_backward_mode, plain_attention, set_backward_mode,
-    set_reference_backward,
+    _attention, attention, backward_mode, backward_score_budget, current_backward_mode, plain_attention,
+    set_backward_mode, set_backward_score_budget, set_reference_backward,
 )
 from .jvp_helper import (  # noqa: F401
     FlexOrSdpaLocalAttentionWithT,

@@ -47,6 +47,7 @@ class Plan(ctypes.Structure):
         ("chunks", ctypes.c_int32),
         ("transposed_copies", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_int64),
+        ("score_slices", ctypes.c_int64),
     ]
 
     def as_dict(self) -> dict:
@@ -86,6 +87,8 @@ SIGNATURES = {
     "dmad_attn_bwd_workspace_bytes": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64, _SZP]),
     "dmad_attn_fwd_plan": (_INT, [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.POINTER(Plan)]),
     "dmad_attn_bwd_plan": (_INT, [_INT, _INT, _INT, _I64, _I64, _I64, _I64, _I64, ctypes.POINTER(Plan)]),
+    "dmad_attn_bwd_plan_ws": (_INT, [_INT, _INT, _INT, _I64, _I64, _I64, _I64, _I64, _SZ, ctypes.POINTER(Plan)]),
+    "dmad_attn_bwd_score_bytes": (_INT, [_INT, _INT, _I64, _I64, _I64, _SZP]),
     "dmad_attn_jvp_bwd": (_INT, [_INT, _I64, _I64, _I64, _I64, _I64,
                                  _P, _P, _P, _P, _P, _P, _I64P, _I64P, _I64P,
                                  _P, _P, _I64P, _P, _P, _P, _P, _I64P,
@@ -197,12 +200,26 @@ def fwd_plan(dtype: int, mode: int, B: int, H: int, Lq: int, Lk: int, Dqk: int, 
 
 
 def bwd_plan(dtype: int, B: int, H: int, Lq: int, Lk: int, D: int, full: bool = False,
-             tangent_grads: bool = False) -> dict:
+             tangent_grads: bool = False, workspace_bytes: int | None = None) -> dict:
     """The launch plan of a backward call (no GPU needed): the key and query passes (and the
-    tangent passes), their grids and block order, transposed copies, workspace."""
+    tangent passes), their grids and block order, transposed copies, workspace. With
+    ``workspace_bytes`` the plan of a call given that much workspace (``score_slices`` > 0:
+    the stored-score passes)."""
     pl = Plan()
-    check(lib().dmad_attn_bwd_plan(dtype, int(full), int(tangent_grads), B, H, Lq, Lk, D, ctypes.byref(pl)))
+    if workspace_bytes is None:
+        check(lib().dmad_attn_bwd_plan(dtype, int(full), int(tangent_grads), B, H, Lq, Lk, D, ctypes.byref(pl)))
+    else:
+        check(lib().dmad_attn_bwd_plan_ws(dtype, int(full), int(tangent_grads), B, H, Lq, Lk, D,
+                                          int(workspace_bytes), ctypes.byref(pl)))
     return pl.as_dict()
+
+
+@functools.lru_cache(maxsize=1024)
+def bwd_score_bytes(dtype: int, full: bool, Lq: int, Lk: int, D: int) -> int:
+    """Bytes of stored score gradients per (b, h) slice (0 where the path does not exist)."""
+    n = ctypes.c_size_t(0)
+    check(lib().dmad_attn_bwd_score_bytes(dtype, int(full), Lq, Lk, D, ctypes.byref(n)))
+    return int(n.value)
 
 
 @functools.lru_cache(maxsize=1024)

@@ -63,7 +63,44 @@ struct BwdParams {
   int B, H, Lq, Lk, LQP;
   float scale, scale_log2;
   int xcd_order;  // work items contiguous per XCD (common.h)
+  // Stored score gradients (key passes instantiated with STORE, 128-wide heads):
+  // the launch covers (b, h) slices bh0 .. bh0 + grid / key tiles - 1, and slice
+  // bh - bh0 of `sc` (sc_slice bytes apart) receives its dS [, dSd] in the layout
+  // of ScLayout below.
+  void* sc;
+  int64_t sc_slice;
+  int bh0;
 };
+
+// Layout of the score gradients a key pass stores for the query pass to read
+// back (the dQ pass then multiplies them by K instead of recomputing S and dP).
+// One (b, h) slice holds NT tensors (dS; or dS, dSd) in pieces of 32 queries x
+// 32 keys (2 KiB, bf16/fp16):
+//   [query block of 128][key block of 32][tensor][query tile of 32 (4)]
+//     [16-query chunk u (2)][row (32)][query half (2)][8 queries]
+// with row = (key % 32) ^ 4u. The key pass's wave owns one key block and holds,
+// per lane (key, half), the 8 consecutive queries 16u + 8 half + 0..7 of its
+// tile packed in 16 bytes, so each chunk leaves as one contiguous 1 KiB store.
+// The query pass copies a (query block, key block) piece of NT x 8 KiB into LDS
+// as it lies and reads dS^T straight from it as MFMA B operands with
+// ds_read_b64_tr_b16 (lane = query, 8 consecutive keys); the row XOR puts the
+// two chunks a 32-lane half reads at once in different 128-byte bank windows.
+struct ScLayout {
+  static constexpr int BQ = 128;          // queries per query block
+  static constexpr int BK = 32;           // keys per key block
+  static constexpr int PIECE = 8192;      // one tensor's (query block, key block) piece
+  static constexpr int TILE = 2048;       // one 32-query tile of a piece
+  static constexpr int CHUNK = 1024;      // one 16-query chunk of a tile
+  // byte offset of lane (key col, half)'s 16 bytes within chunk u
+  __device__ __forceinline__ static uint32_t lane_off(int col, int half, int u) {
+    return (uint32_t)((((col ^ (4 * u)) * 2) + half) * 16);
+  }
+};
+// Bytes of one (b, h) slice: NT tensors over Lq rounded up to 128 queries and
+// `nkb` key blocks (the key pass covers nkt * 128 keys: nkb = 4 nkt).
+__host__ __device__ inline int64_t sc_slice_bytes(int64_t lq, int64_t nkb, int nt) {
+  return (lq + ScLayout::BQ - 1) / ScLayout::BQ * nkb * nt * ScLayout::PIECE;
+}
 
 template <int D, int MODE>
 struct BwdCfg {
@@ -736,11 +773,18 @@ constexpr int kKvTrBmq = 32;
 // Compiled with MFMAs in VGPR form (bwd_kv_inst.hip): the S, dP MFMAs write
 // VGPRs that the VALU reads directly, and the dK, dV accumulators stay in
 // AGPRs through inline MFMAs (mfma32_acc).
-template <typename T, int D>
+// STORE (128-wide heads): also writes each tile's dS (the bf16/fp16 operand of
+// the dK update, keys at or beyond Lk as zeros) to p.sc in the ScLayout for
+// attn_bwd_dq_sc_kernel. Both chunks of tile j leave at the end of step j,
+// after the step's ring requests: the next barrier's vmcnt then counts them
+// among the most recent operations it lets stay in flight, whatever order the
+// stores and the ring loads complete in.
+template <typename T, int D, bool STORE = false>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(BwdParams p) {
   using C = KvTrCfg<D, kKvTrBmq>;
   constexpr int BMQ = C::BMQ, NQB = C::NQB, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
   static_assert(C::FITS, "configuration does not fit");
+  static_assert(!STORE || D == 128, "score stores are laid out for 128-wide heads");
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
@@ -752,11 +796,24 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
   const int work = work_item(p.xcd_order);  // block order (common.h)
-  const int bh = work / nkt, kt = work - bh * nkt;
+  const int slice = work / nkt, kt = work - slice * nkt;
+  const int bh = (STORE ? p.bh0 : 0) + slice;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
 
   const int key = kt * C::BK + wave * 32 + col;
+
+  // ---- score-gradient stores (STORE): this wave's key block of the slice's strips
+  const int64_t sc_strip = (int64_t)nkt * 4 * ScLayout::PIECE;  // one query block, one tensor
+  char* const sc_base = STORE ? (char*)p.sc + (int64_t)slice * p.sc_slice : nullptr;
+  const uint32_t sc_kb = (uint32_t)(kt * 4 + wave) * ScLayout::PIECE;
+  const uint32_t sc_lo0 = ScLayout::lane_off(col, half, 0), sc_lo1 = ScLayout::lane_off(col, half, 1);
+  const bool sc_tail = (kt + 1) * C::BK > p.Lk;  // keys at or beyond Lk in this workgroup
+  auto store_chunk = [&](int qt, int u, i32x4_t v) {
+    if (sc_tail && key >= p.Lk) v = i32x4_t{0, 0, 0, 0};
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)sc_strip);
+    buf_store16(rs, v, u ? sc_lo1 : sc_lo0, sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE + (uint32_t)u * ScLayout::CHUNK);
+  };
 
   // ---- stationary K, V rows: B operands of S = Q K^T and dP = dO V^T
   const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
@@ -992,6 +1049,10 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (STORE) {
+      store_chunk(j, 0, dsb[0]);
+      store_chunk(j, 1, dsb[1]);
+    }
   };
   static_assert(A1 + 2 + AS * 3 < NMA + 2 * DB, "chunk 1 is packed before its first update MFMA");
   static_assert(B1 + 2 + BS * 3 < NS, "chunk 0 of the next tile is packed within the step");
@@ -1004,6 +1065,10 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
     pb[0] = pb0;
     dsb[0] = ds0;
     chunk_now(s_cur, 1, sc[0], dpc[0], pb[1], dsb[1]);
+    if constexpr (STORE) {
+      store_chunk(nqt - 1, 0, dsb[0]);
+      store_chunk(nqt - 1, 1, dsb[1]);
+    }
     f32x16_t un_s[NQB], un_p[NQB];
 #pragma unroll
     for (int m = NMA; m < NS; ++m) mfma_slot(m, load_op(s_cur, s_cur, m), un_s, un_p, pb, dsb);

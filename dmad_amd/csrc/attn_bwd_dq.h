@@ -45,6 +45,13 @@ struct DqParams {
   int stat_tile;  // query tile of the statistics layout
   float scale, scale_log2;
   int xcd_order;  // work items contiguous per XCD (common.h)
+  // attn_bwd_dq_sc_kernel: the score gradients a STORE key pass wrote (ScLayout
+  // in attn_bwd.h) for (b, h) slices bh0 .. bh0 + grid / query blocks - 1, slice
+  // bh - bh0 at sc + (bh - bh0) sc_slice, with sc_nkb key blocks of 32
+  const void* sc;
+  int64_t sc_slice;
+  int sc_nkb;
+  int bh0;
 };
 
 template <int D, int MODE>

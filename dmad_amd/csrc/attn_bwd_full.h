@@ -77,7 +77,12 @@ __device__ __forceinline__ FullVals full_values(float s, float sd_raw, float dpd
   return r;
 }
 
-template <typename T, int D>
+// STORE: also writes each tile's dS and dSd (the operands of the dK updates,
+// keys at or beyond Lk as zeros) to p.sc in the ScLayout (tensor 0 = dS,
+// 1 = dSd) for attn_bwd_dq_sc_kernel. Tile j's four chunks leave at the end of
+// step j, after the step's ring requests, so the next barrier's vmcnt counts
+// them among the operations it lets stay in flight.
+template <typename T, int D, bool STORE = false>
 __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
   using C = KvFullCfg<D>;
   constexpr int BMQ = C::BMQ, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
@@ -93,10 +98,31 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
 
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
   const int work = work_item(p.xcd_order);  // block order (common.h)
-  const int bh = work / nkt, kt = work - bh * nkt;
+  const int slice = work / nkt, kt = work - slice * nkt;
+  const int bh = (STORE ? p.bh0 : 0) + slice;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
   const int key = kt * C::BK + wave * 32 + col;
+
+  // ---- score-gradient stores (STORE): this wave's key block of the slice's strips
+  const int64_t sc_strip = (int64_t)nkt * 4 * 2 * ScLayout::PIECE;  // one query block, both tensors
+  char* const sc_base = STORE ? (char*)p.sc + (int64_t)slice * p.sc_slice : nullptr;
+  const uint32_t sc_kb = (uint32_t)(kt * 4 + wave) * 2 * ScLayout::PIECE;
+  const uint32_t sc_lo0 = ScLayout::lane_off(col, half, 0), sc_lo1 = ScLayout::lane_off(col, half, 1);
+  const bool sc_tail = (kt + 1) * C::BK > p.Lk;  // keys at or beyond Lk in this workgroup
+  auto store_tile = [&](int qt, const i32x4_t (&ds)[2], const i32x4_t (&dsd)[2]) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)sc_strip);
+    const uint32_t so = sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        i32x4_t v = t ? dsd[u] : ds[u];
+        if (sc_tail && key >= p.Lk) v = i32x4_t{0, 0, 0, 0};
+        buf_store16(rs, v, u ? sc_lo1 : sc_lo0, so + (uint32_t)t * ScLayout::PIECE + (uint32_t)u * ScLayout::CHUNK);
+      }
+    }
+  };
 
   // ---- stationary K, Kd, V, Vd rows (B operands of the score MFMAs), kept in AGPRs
   const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
@@ -322,6 +348,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (STORE) store_tile(j, pk.ds, pk.dsd);
   };
   static_assert(NOPA == 32 && 4 * 7 + 1 < NOPA, "eight value pairs ride in the 32 phase-A slots");
   // last tile: its values, then its update MFMAs
@@ -337,6 +364,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
     }
     asm volatile("" : "+v"(pk.p[0]), "+v"(pk.p[1]), "+v"(pk.pd[0]), "+v"(pk.pd[1]));
     asm volatile("" : "+v"(pk.ds[0]), "+v"(pk.ds[1]), "+v"(pk.dsd[0]), "+v"(pk.dsd[1]));
+    if constexpr (STORE) store_tile(nqt - 1, pk.ds, pk.dsd);
     Scores un;
 #pragma unroll
     for (int o = NOPA; o < NOP; ++o) mfma_op(o, load_op(s_cur, s_cur, o), un, pk);

@@ -31,4 +31,25 @@ BwdLaunchFn kv_tr_select<Elt, 128>() {
   return &kv_tr_launch<Elt, 128>;
 }
 
+// dO-only half of the stored-score backward: the key pass writing dS and the
+// query pass reading it back (the full-derivative half is in bwd_full_inst.hip)
+template <typename T>
+static hipError_t kv_sc_launch(const BwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, 128, true>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+template <typename T>
+static hipError_t dq_sc1_launch(const DqParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_dq_sc_kernel<T, 1>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+template <>
+BwdLaunchFn kv_sc_dout_only<Elt>() {
+  return &kv_sc_launch<Elt>;
+}
+template <>
+DqLaunchFn dq_sc_dout_only<Elt>() {
+  return &dq_sc1_launch<Elt>;
+}
+
 }  // namespace dmad

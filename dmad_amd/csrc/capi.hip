@@ -56,7 +56,7 @@ template <> FwdLaunchFn fwd_magi_select<_Float16, 256>(int, int);
 namespace {
 
 thread_local std::string g_last_error;
-constexpr int kMaxEvents = 8;
+constexpr int kMaxEvents = 256;
 thread_local hipEvent_t g_events[kMaxEvents];
 thread_local int g_nevents = 0;
 
@@ -303,6 +303,18 @@ dmad::DqLaunchFn pick_dq_full(int dtype, bool tangent_grads) {
   return nullptr;
 }
 
+dmad::BwdLaunchFn pick_kv_sc(int dtype, bool full) {
+  if (dtype == DMAD_BF16) return dmad::kv_sc_select<__bf16>(full);
+  if (dtype == DMAD_F16) return dmad::kv_sc_select<_Float16>(full);
+  return nullptr;
+}
+
+dmad::DqLaunchFn pick_dq_sc(int dtype, bool full) {
+  if (dtype == DMAD_BF16) return dmad::dq_sc_select<__bf16>(full);
+  if (dtype == DMAD_F16) return dmad::dq_sc_select<_Float16>(full);
+  return nullptr;
+}
+
 dmad::DqLaunchFn pick_dq(int dtype, int64_t d, int mode) {
   using namespace dmad;
   if (dtype == DMAD_BF16) {
@@ -369,14 +381,35 @@ BwdWs bwd_ws_of(int dtype, int full, int64_t B, int64_t H, int64_t Lq, int64_t L
   return w;
 }
 
+// Stored score gradients (attn_bwd_dq_sc.h): bf16/fp16 operands of 128-wide
+// heads. Bytes per (b, h) slice: dS (and dSd for the full derivative) over Lq
+// rounded up to 128 queries and the key pass's 128-key tiles, bf16/fp16.
+bool score_store_ok(int dtype, int64_t D) { return (dtype == DMAD_BF16 || dtype == DMAD_F16) && D == 128; }
+int64_t score_slice_bytes(bool full, int64_t Lq, int64_t Lk) {
+  const int64_t nkt = (Lk + 127) / 128;
+  return round_up(dmad::sc_slice_bytes(Lq, 4 * nkt, full ? 2 : 1), 256);
+}
+// (b, h) slices per launch pair that `workspace_bytes` holds beyond the minimum
+// workspace `base` (0: the recomputing query pass runs)
+int64_t score_slices(int dtype, bool full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, int64_t base,
+                     int64_t workspace_bytes) {
+  if (!score_store_ok(dtype, D) || B * H == 0 || Lq == 0 || Lk == 0 || workspace_bytes <= base) return 0;
+  const int64_t one = score_slice_bytes(full, Lq, Lk);
+  const int64_t n = (workspace_bytes - base) / one;
+  return n < B * H ? n : B * H;
+}
+
 // Backward plan: the key-stationary pass (dK, dV), the query-stationary pass
 // (dQ [, dQd]), and with tangent gradients the dO-only passes run on (dOd, rho)
-// (the query one only where the full query pass does not give dQd).
+// (the query one only where the full query pass does not give dQd). With
+// score slices (sc > 0) the key pass also stores the score gradients and the
+// query pass reads them back, sc (b, h) slices per launch pair.
 struct BwdPlan {
   const char *kv, *dq, *kv_t, *dq_t;
   int64_t grid_kv, grid_dq;
   int xcd_kv, xcd_dq, copies;
   int64_t ws;
+  int64_t sc;
 };
 
 BwdPlan plan_bwd(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D) {
@@ -405,6 +438,23 @@ BwdPlan plan_bwd(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int64_t
   const BwdWs w = bwd_ws(full ? (tgrad ? 2 : 1) : 0, B, H, Lq, Lk, D);
   pl.copies = w.nq + w.nk;
   pl.ws = w.total;
+  return pl;
+}
+
+// The plan of a call given its workspace: the stored-score passes where the
+// workspace holds at least one (b, h) slice of score gradients beyond the minimum.
+BwdPlan plan_bwd_ws(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
+                    int64_t workspace_bytes) {
+  BwdPlan pl = plan_bwd(dtype, full, tgrad, B, H, Lq, Lk, D);
+  pl.sc = score_slices(dtype, full, B, H, Lq, Lk, D, pl.ws, workspace_bytes);
+  if (pl.sc > 0) {
+    pl.kv = full ? "attn_bwd_kv_full_kernel<store>" : "attn_bwd_kv_tr_kernel<store>";
+    pl.dq = "attn_bwd_dq_sc_kernel";
+    pl.grid_kv = (Lk + 127) / 128 * pl.sc;
+    pl.grid_dq = (Lq + 127) / 128 * pl.sc;
+    pl.xcd_dq = (Lq + 127) / 128 < dmad::kHeadMajorMinTiles;
+    pl.ws += pl.sc * score_slice_bytes(full, Lq, Lk);
+  }
   return pl;
 }
 
@@ -637,6 +687,8 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   }
   if (workspace == nullptr || (int64_t)workspace_bytes < w.total)
     return fail(DMAD_ERR_WORKSPACE, "workspace needs %lld bytes, got %lld", (long long)w.total, (long long)workspace_bytes);
+  // workspace beyond the minimum holds stored score gradients (128-wide bf16/fp16 heads)
+  const int64_t sc = use_scratch ? 0 : score_slices(dtype, full, B, H, Lq, Lk, D, w.total, (int64_t)workspace_bytes);
   if (((uintptr_t)workspace & 255) != 0) return fail(DMAD_ERR_INVALID, "workspace must be 256-byte aligned");
   const int64_t dp = D < 32 ? 32 : D, lqp = round_up(Lq, 64), lkp = round_up(Lk, kLkAlign), BH = B * H;
   if (dp * lqp * 2 >= kMaxHeadBytes || dp * lkp * 2 >= kMaxHeadBytes) return fail(DMAD_ERR_UNSUPPORTED, "sequence too long");
@@ -814,6 +866,50 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     return fail(DMAD_ERR_UNSUPPORTED, "grid too large");
   p.xcd_order = plan.xcd_kv;  // block order (common.h)
   pq.xcd_order = plan.xcd_dq;
+  if (sc > 0) {
+    // stored score gradients: per launch pair, the key pass over sc (b, h)
+    // slices writes their dS [, dSd] after the minimum workspace and the query
+    // pass reads them back; main kernels in launch order (key, query) per pair,
+    // then the tangent key pass
+    const dmad::BwdLaunchFn fs = pick_kv_sc(dtype, full);
+    const dmad::DqLaunchFn fqs = pick_dq_sc(dtype, full);
+    if (fs == nullptr || fqs == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no stored-score backward kernel");
+    const int64_t nkt = (Lk + 127) / 128, nqb = (Lq + 127) / 128;
+    p.sc = ws + w.total;
+    p.sc_slice = score_slice_bytes(full, Lq, Lk);
+    pq.sc = p.sc;
+    pq.sc_slice = p.sc_slice;
+    pq.sc_nkb = (int)(4 * nkt);
+    pq.xcd_order = nqb < dmad::kHeadMajorMinTiles;
+    int ev = 0;
+    for (int64_t bh0 = 0; bh0 < BH; bh0 += sc) {
+      const int64_t n = BH - bh0 < sc ? BH - bh0 : sc;
+      p.bh0 = pq.bh0 = (int)bh0;
+      mark(ev, false, s);
+      if ((e = fs(p, (int)(n * nkt), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+      mark(ev++, true, s);
+      mark(ev, false, s);
+      if ((e = fqs(pq, (int)(n * nqb), s)) != hipSuccess)
+        return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
+      mark(ev++, true, s);
+    }
+    if (tgrad) {
+      // 128-wide heads: dQd came from the query pass; dKd, dVd from the dO-only
+      // key pass with (dO, D) := (dOd, rho)
+      dmad::BwdParams pt = p;
+      pt.dout = dto;
+      pt.doT = trdto;
+      pt.stats = stats_bt;
+      pt.dk = dtk;
+      pt.dv = dtv;
+      pt.bh0 = 0;
+      mark(ev, false, s);
+      if ((e = fn_a(pt, (int)plan.grid_kv, s)) != hipSuccess)
+        return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+      mark(ev, true, s);
+    }
+    return ok();
+  }
   mark(0, false, s);
   if ((e = fn(p, (int)plan.grid_kv, s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   mark(0, true, s);
@@ -854,7 +950,7 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
 
 extern "C" {
 
-int dmad_abi_version(void) { return 1; }
+int dmad_abi_version(void) { return 2; }
 
 const char* dmad_last_error(void) { return g_last_error.c_str(); }
 
@@ -956,6 +1052,29 @@ int dmad_attn_bwd_plan(int dtype, int full, int tangent_grads, int64_t B, int64_
   out->chunks = 1;
   out->transposed_copies = pl.copies;
   out->workspace_bytes = pl.ws;
+  return ok();
+}
+int dmad_attn_bwd_plan_ws(int dtype, int full, int tangent_grads, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                          int64_t D, size_t workspace_bytes, dmad_plan* out) {
+  const int rc = dmad_attn_bwd_plan(dtype, full, tangent_grads, B, H, Lq, Lk, D, out);
+  if (rc != DMAD_OK) return rc;
+  const BwdPlan pl = plan_bwd_ws(dtype, full != 0, tangent_grads != 0, B, H, Lq, Lk, D, (int64_t)workspace_bytes);
+  if (pl.sc > 0) {
+    out->kernel = pl.kv;
+    out->kernel2 = pl.dq;
+    out->grid = pl.grid_kv;
+    out->grid2 = pl.grid_dq;
+    out->xcd_order2 = pl.xcd_dq;
+    out->workspace_bytes = pl.ws;
+    out->score_slices = pl.sc;
+  }
+  return ok();
+}
+int dmad_attn_bwd_score_bytes(int dtype, int full, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes) {
+  if (bytes == nullptr) return fail(DMAD_ERR_INVALID, "bytes: null pointer");
+  if (full != 0 && full != 1) return fail(DMAD_ERR_INVALID, "full must be 0 or 1");
+  if (Lq < 0 || Lk < 0 || !head_dim_ok(D)) return fail(DMAD_ERR_INVALID, "bad sizes");
+  *bytes = score_store_ok(dtype, D) && Lq > 0 && Lk > 0 ? (size_t)score_slice_bytes(full != 0, Lq, Lk) : 0;
   return ok();
 }
 int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes) {

@@ -50,6 +50,10 @@ __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* l
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds_base, 16, (int)voff, (int)soff, 0, 0);
 }
 
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, i32x4_t v, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, (int)soff, 0);
+}
+
 __device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, u32x2_t v, uint32_t voff) {
   i32x2_t w = {(int)v[0], (int)v[1]};
   __builtin_amdgcn_raw_buffer_store_b64(w, r, (int)voff, 0, 0);

@@ -9,6 +9,7 @@
 #include "attn_bwd.h"
 #include "attn_bwd_dq.h"
 #include "attn_bwd_full.h"
+#include "attn_bwd_dq_sc.h"
 #include "attn_f32.h"
 
 namespace dmad {
@@ -97,6 +98,27 @@ template <> DqLaunchFn dq_full_select<__bf16>(bool);
 template <> DqLaunchFn dq_full_select<_Float16>(bool);
 // Head dims whose full derivative runs on those passes.
 inline bool full_reads_rows(int d) { return d == 128; }
+
+// Stored-score backward of 128-wide heads: the key pass that also writes dS
+// (dO only: attn_bwd_kv_tr_kernel<T, 128, true>, bwd_kv_inst.hip) or dS, dSd
+// (full derivative: attn_bwd_kv_full_kernel<T, 128, true>, bwd_full_inst.hip),
+// and the query pass over them (attn_bwd_dq_sc_kernel<T, 1 | 2>).
+template <typename T>
+BwdLaunchFn kv_sc_dout_only();
+template <> BwdLaunchFn kv_sc_dout_only<__bf16>();
+template <> BwdLaunchFn kv_sc_dout_only<_Float16>();
+template <typename T>
+DqLaunchFn dq_sc_dout_only();
+template <> DqLaunchFn dq_sc_dout_only<__bf16>();
+template <> DqLaunchFn dq_sc_dout_only<_Float16>();
+template <typename T>
+BwdLaunchFn kv_sc_select(bool full);
+template <> BwdLaunchFn kv_sc_select<__bf16>(bool);
+template <> BwdLaunchFn kv_sc_select<_Float16>(bool);
+template <typename T>
+DqLaunchFn dq_sc_select(bool full);
+template <> DqLaunchFn dq_sc_select<__bf16>(bool);
+template <> DqLaunchFn dq_sc_select<_Float16>(bool);
 
 // Query tile of the dK/dV kernel, which fixes the layout of the backward
 // statistics (the full-derivative kernel always uses 32-query tiles).

@@ -31,6 +31,7 @@ from __future__ import annotations
 
 import contextlib
 import contextvars
+import os
 from typing import Iterator, Optional, Tuple
 
 import torch
@@ -97,6 +98,57 @@ def set_backward_mode(mode: str) -> None:
     global _DEFAULT_BACKWARD_MODE
     _check_backward_mode(mode)
     _DEFAULT_BACKWARD_MODE = mode
+
+
+# Device memory (bytes) the backward of 128-wide bf16/fp16 heads may take, per
+# call and on top of its minimum workspace, for stored score gradients: its key
+# pass then writes dS (and dSd) and the query pass reads them back instead of
+# recomputing the scores, as many (b, h) slices per launch pair as fit. 0 turns
+# the path off. Environment default: DMAD_BWD_SCORE_BUDGET_MB.
+_SCORE_BUDGET = int(os.environ.get("DMAD_BWD_SCORE_BUDGET_MB", "16384")) << 20
+
+
+def set_backward_score_budget(nbytes: int) -> None:
+    """Set how much device memory (bytes) each backward may use for stored score gradients
+    (0: the query pass recomputes the scores; the memory is workspace, freed with the call)."""
+    global _SCORE_BUDGET
+    if int(nbytes) < 0:
+        raise ValueError("the budget must be >= 0")
+    _SCORE_BUDGET = int(nbytes)
+
+
+def backward_score_budget() -> int:
+    return _SCORE_BUDGET
+
+
+# The dO-only backward stores its scores from this many queries and keys on: below it
+# the recomputing query pass measured as fast or faster (the stores cost the key pass
+# about a fifth of its time; the full derivative's query pass saves more than that).
+_SCORE_MIN_LEN_DOUT_ONLY = 4096
+
+
+def _score_bytes(code: int, full: bool, B: int, H: int, Lq: int, Lk: int, D: int) -> int:
+    """Workspace bytes for stored score gradients within the budget (whole (b, h) slices)."""
+    if not full and min(Lq, Lk) < _SCORE_MIN_LEN_DOUT_ONLY:
+        return 0
+    one = nat.bwd_score_bytes(code, full, Lq, Lk, D) if _SCORE_BUDGET > 0 else 0
+    if one == 0 or _SCORE_BUDGET < one:
+        return 0
+    return min(B * H, _SCORE_BUDGET // one) * one
+
+
+def backward_plan(dtype: torch.dtype, B: int, H: int, Lq: int, Lk: int, D: int, full: bool = False,
+                  tangent_grads: bool = False) -> dict:
+    """The launch plan of the backward this op runs for these sizes under the current score
+    budget (no GPU needed): kernels, grids, workspace and ``score_slices``; with score slices
+    the key and query passes run ``pairs`` times, one pair per group of slices."""
+    code = nat.dtype_code(dtype)
+    mode = (2 if tangent_grads else 1) if full else 0
+    ws = nat.bwd_workspace_bytes_of(code, mode, B, H, Lq, Lk, D) + _score_bytes(code, full, B, H, Lq, Lk, D)
+    pl = nat.bwd_plan(code, B, H, Lq, Lk, D, full=full, tangent_grads=full and tangent_grads, workspace_bytes=ws)
+    n = pl["score_slices"]
+    pl["pairs"] = -(-(B * H) // n) if n else 1
+    return pl
 
 
 def set_reference_backward(flag: bool) -> None:
@@ -349,7 +401,8 @@ def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_sc
     dtv = torch.empty_like(dv) if tgrads else None
     lib = nat.lib()
     ws_mode = (2 if tgrads else 1) if full else 0
-    ws_ptr, ws_size, ws = nat.workspace(nat.bwd_workspace_bytes_of(code, ws_mode, B, H, Lq, Lk, D), q.device)
+    ws_bytes = nat.bwd_workspace_bytes_of(code, ws_mode, B, H, Lq, Lk, D) + _score_bytes(code, full, B, H, Lq, Lk, D)
+    ws_ptr, ws_size, ws = nat.workspace(ws_bytes, q.device)
     nat.check(
         lib.dmad_attn_jvp_bwd(
             code, B, H, Lq, Lk, D,

@@ -139,7 +139,10 @@ int dmad_attn_bwd_workspace_bytes(int full, int64_t B, int64_t H, int64_t Lq, in
  * strides given in dq_strides (shared by dq, dtq), dk_strides (dk, dtk) and
  * dv_strides (dv, dtv); do/dto share do_strides. B, H or Lq = Lk = 0 is a
  * no-op; Lq = 0 with Lk > 0 (where dk, dv are zero) is DMAD_ERR_INVALID: the
- * caller fills the zeros.
+ * caller fills the zeros. A workspace larger than dmad_attn_bwd_workspace_bytes
+ * by whole slices of dmad_attn_bwd_score_bytes selects the stored-score passes
+ * (128-wide bf16/fp16 heads; the gradients agree with the recomputing passes
+ * to rounding).
  */
 int dmad_attn_jvp_bwd(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, const void* q,
                       const void* k, const void* v, const void* tq, const void* tk, const void* tv,
@@ -224,6 +227,9 @@ typedef struct dmad_plan {
                                 modes (two per task) */
   int32_t transposed_copies; /* operands copied transposed into the workspace before the kernels */
   int64_t workspace_bytes;   /* workspace the call needs */
+  int64_t score_slices;      /* backward (dmad_attn_bwd_plan_ws): (b, h) slices per launch pair of the stored-score
+                                passes (`kernel` stores dS [, dSd], `kernel2` reads them back; grids are per pair);
+                                0: the query pass recomputes the scores */
 } dmad_plan;
 
 /* Plan of dmad_attn_jvp_fwd / dmad_attn_fwd (magi_tasks < 0) or of
@@ -231,9 +237,28 @@ typedef struct dmad_plan {
 int dmad_attn_fwd_plan(int dtype, int mode, int64_t magi_tasks, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
                        int64_t Dqk, int64_t Dv, dmad_plan* plan);
 
-/* Plan of dmad_attn_jvp_bwd; full and tangent_grads: 0 or 1 (dto and dtq/dtk/dtv given). */
+/* Plan of dmad_attn_jvp_bwd with the minimum workspace; full and tangent_grads: 0 or 1 (dto and dtq/dtk/dtv
+ * given). */
 int dmad_attn_bwd_plan(int dtype, int full, int tangent_grads, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
                        dmad_plan* plan);
+
+/* Plan of dmad_attn_jvp_bwd called with `workspace_bytes` of workspace (see dmad_attn_bwd_score_bytes). */
+int dmad_attn_bwd_plan_ws(int dtype, int full, int tangent_grads, int64_t B, int64_t H, int64_t Lq, int64_t Lk,
+                          int64_t D, size_t workspace_bytes, dmad_plan* plan);
+
+/*
+ * Bytes of stored score gradients per (b, h) slice (no counterpart in the
+ * reference; the reference's backward is flash-attn's, which recomputes).
+ * For bf16/fp16 operands of 128-wide heads the backward's key pass can write
+ * the dS (full = 1: and dSd) tiles it computes, in bf16/fp16, so that the
+ * query pass becomes a streaming GEMM over them instead of recomputing S and
+ * dP. dmad_attn_jvp_bwd takes that path when its workspace exceeds
+ * dmad_attn_bwd_workspace_bytes by at least these bytes, processing as many
+ * (b, h) slices per launch pair as the excess holds (e.g. Wan2.1-14B,
+ * L = 32760: 2.15 GB per slice dO-only, 4.3 GB with dOd). 0 for other head dims
+ * and for fp32 (the path does not exist there).
+ */
+int dmad_attn_bwd_score_bytes(int dtype, int full, int64_t Lq, int64_t Lk, int64_t D, size_t* bytes);
 
 /*
  * Timing hook (no counterpart in the reference; for benchmarks and profilers
@@ -243,8 +268,10 @@ int dmad_attn_bwd_plan(int dtype, int full, int tangent_grads, int64_t B, int64_
  * before and after its i-th main kernel, excluding the layout and statistics
  * passes. Main kernels in order: forward -> {attention}; backward -> {dK/dV
  * pass, dQ pass[, tangent dK/dV pass[, tangent dQ pass]]} (for 128-wide heads
- * the full derivative's dQ pass also gives dQd: no tangent dQ pass). Kernels
- * without a pair of events are not timed. count = 0 (events may be NULL) stops.
+ * the full derivative's dQ pass also gives dQd: no tangent dQ pass); a
+ * backward on stored score gradients -> {dK/dV pass, dQ pass} once per launch
+ * pair, then [tangent dK/dV pass]. Kernels without a pair of events are not
+ * timed. count <= 256; count = 0 (events may be NULL) stops.
  */
 int dmad_set_kernel_events(void* const* events, int count);
 

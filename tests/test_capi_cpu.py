@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(nat):
     lib = nat.lib()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.dmad_abi_version() == 1
+    assert lib.dmad_abi_version() == 2
 
 
 def _strides(*v):
@@ -113,8 +113,9 @@ def test_kernel_event_hook_validates(nat):
     assert lib.dmad_set_kernel_events(None, 2) == 1
     arr = (ctypes.c_void_p * 3)(None, None, None)
     assert lib.dmad_set_kernel_events(arr, 3) == 1
-    arr = (ctypes.c_void_p * 10)()
-    assert lib.dmad_set_kernel_events(arr, 10) == 1
+    arr = (ctypes.c_void_p * 258)()
+    assert lib.dmad_set_kernel_events(arr, 258) == 1  # at most 256 events
+    assert lib.dmad_set_kernel_events(arr, 256) == 0
     assert lib.dmad_set_kernel_events(None, 0) == 0
 
 

@@ -190,3 +190,75 @@ def test_argument_checks():
         nat.bwd_plan(F32, 1, 2, 64, 64, 64, full=True)
     with pytest.raises(ValueError):
         nat.bwd_plan(BF16, 1, 2, 64, 64, 64, tangent_grads=True)
+
+
+def test_stored_score_sizes():
+    """Bytes per (b, h) slice of stored score gradients: dS (and dSd) in bf16/fp16 over Lq
+    rounded up to 128 queries and the key pass's 128-key tiles; none for other head dims and fp32."""
+    gib = 1 << 30
+    for dt in (BF16, F16):
+        assert nat.bwd_score_bytes(dt, False, 32760, 32760, 128) == 2 * gib  # 256 x 256 pieces of 32 KiB
+        assert nat.bwd_score_bytes(dt, True, 32760, 32760, 128) == 4 * gib
+        assert nat.bwd_score_bytes(dt, False, 1, 1, 128) == 128 * 128 * 2
+        assert nat.bwd_score_bytes(dt, True, 300, 700, 128) == 384 * 768 * 2 * 2
+    assert nat.bwd_score_bytes(F32, False, 4096, 4096, 128) == 0
+    for D in (16, 32, 64, 256):
+        assert nat.bwd_score_bytes(BF16, False, 4096, 4096, D) == 0
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_stored_score_plan_follows_the_workspace(full):
+    """dmad_attn_bwd_plan_ws: whole score slices beyond the minimum workspace select the
+    stored-score passes, as many (b, h) slices per launch pair as fit (at most B*H)."""
+    B, H, L = 1, 40, 32760
+    base = nat.bwd_plan(BF16, B, H, L, L, 128, full=full, tangent_grads=full)
+    one = nat.bwd_score_bytes(BF16, full, L, L, 128)
+    p = nat.bwd_plan(BF16, B, H, L, L, 128, full=full, tangent_grads=full,
+                     workspace_bytes=base["workspace_bytes"] + 3 * one + one // 2)
+    assert p["score_slices"] == 3
+    assert p["kernel"] == ("attn_bwd_kv_full_kernel<store>" if full else "attn_bwd_kv_tr_kernel<store>")
+    assert p["kernel2"] == "attn_bwd_dq_sc_kernel"
+    assert (p["grid"], p["grid2"]) == (3 * 256, 3 * 256)
+    assert p["workspace_bytes"] == base["workspace_bytes"] + 3 * one
+    assert p["kernel3"] == base["kernel3"]  # the tangent key pass is unchanged
+    # the minimum workspace, or less than one slice beyond it, keeps the recomputing passes
+    for extra in (0, one - 256):
+        q = nat.bwd_plan(BF16, B, H, L, L, 128, full=full, tangent_grads=full,
+                         workspace_bytes=base["workspace_bytes"] + extra)
+        assert q["score_slices"] == 0 and q["kernel2"] == base["kernel2"]
+    # more room than B*H slices: all of them in one pair
+    p = nat.bwd_plan(BF16, B, H, L, L, 128, full=full, tangent_grads=full,
+                     workspace_bytes=base["workspace_bytes"] + 100 * one)
+    assert p["score_slices"] == 40
+    # no stored-score path for fp32 or other head dims
+    for dt, D in ((F32, 128), (BF16, 64)):
+        if dt == F32 and full:
+            continue
+        q = nat.bwd_plan(dt, B, H, L, L, D, full=full, tangent_grads=full, workspace_bytes=1 << 50)
+        assert q["score_slices"] == 0
+
+
+def test_python_score_budget():
+    """The op's workspace: whole slices within the process budget (0 turns the path off)."""
+    from dmad_amd import jvp_attention as ja
+
+    one = nat.bwd_score_bytes(BF16, False, 32760, 32760, 128)
+    old = ja.backward_score_budget()
+    try:
+        ja.set_backward_score_budget(16 << 30)
+        assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128) == 8 * one
+        ja.set_backward_score_budget(0)
+        assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128) == 0
+        ja.set_backward_score_budget(one - 1)
+        assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128) == 0
+        ja.set_backward_score_budget(1 << 50)
+        assert ja._score_bytes(BF16, True, 2, 3, 300, 300, 128) == 6 * nat.bwd_score_bytes(BF16, True, 300, 300, 128)
+        # the dO-only backward keeps the recomputing passes below 4096 queries or keys
+        assert ja._score_bytes(BF16, False, 2, 3, 300, 300, 128) == 0
+        assert ja._score_bytes(BF16, False, 1, 2, 4096, 4095, 128) == 0
+        assert ja._score_bytes(BF16, False, 1, 2, 4096, 4096, 128) == 2 * nat.bwd_score_bytes(BF16, False, 4096, 4096, 128)
+        assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 64) == 0
+        with pytest.raises(ValueError):
+            ja.set_backward_score_budget(-1)
+    finally:
+        ja.set_backward_score_budget(old)
