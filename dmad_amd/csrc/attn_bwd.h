@@ -775,10 +775,11 @@ constexpr int kKvTrBmq = 32;
 // AGPRs through inline MFMAs (mfma32_acc).
 // STORE (128-wide heads): also writes each tile's dS (the bf16/fp16 operand of
 // the dK update, keys at or beyond Lk as zeros) to p.sc in the ScLayout for
-// attn_bwd_dq_sc_kernel. Both chunks of tile j leave at the end of step j,
-// after the step's ring requests: the next barrier's vmcnt then counts them
-// among the most recent operations it lets stay in flight, whatever order the
-// stores and the ring loads complete in.
+// attn_bwd_dq_sc_kernel, chunk 0 of tile j in slot 14 of step j and chunk 1
+// (packed by slot 13) in slot 28, between the step's ring requests. The next
+// barrier's vmcnt(LOADS) stays exact whatever order stores and loads complete
+// in: a request of tile j + 2 still in flight means all LOADS requests of tile
+// j + 3 are too.
 template <typename T, int D, bool STORE = false>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(BwdParams p) {
   using C = KvTrCfg<D, kKvTrBmq>;
@@ -812,7 +813,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   auto store_chunk = [&](int qt, int u, i32x4_t v) {
     if (sc_tail && key >= p.Lk) v = i32x4_t{0, 0, 0, 0};
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)sc_strip);
-    buf_store16(rs, v, u ? sc_lo1 : sc_lo0, sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE + (uint32_t)u * ScLayout::CHUNK);
+    buf_store16_stream(rs, v, u ? sc_lo1 : sc_lo0,
+                       sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE + (uint32_t)u * ScLayout::CHUNK);
   };
 
   // ---- stationary K, V rows: B operands of S = Q K^T and dP = dO V^T
@@ -1013,6 +1015,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   constexpr int A1 = NS == 32 ? 2 : 0, AS = NS == 32 ? 3 : 1;
   constexpr int B1 = NMA + 1, BS = NS == 32 ? 4 : 1;
   constexpr int STAT_SLOT = NS == 32 ? 12 : 6;  // statistics of tile j + 1 requested here
+  constexpr int SC_SLOT0 = 14, SC_SLOT1 = 28;   // score stores of tile j (STORE, 32 slots per step)
   auto step = [&](auto kk, int j, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], f32x16_t (&sn)[NQB],
                   f32x16_t (&dpn)[NQB], const i32x4_t& pb0, const i32x4_t& ds0, i32x4_t& pb0n, i32x4_t& ds0n) {
     constexpr int k = decltype(kk)::value;
@@ -1043,20 +1046,21 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
         if (m == B1 + 2 + BS * i) pair_second(i, hn[i], pb0n, ds0n);
       }
       if (m == STAT_SLOT) load_stats(s_next, 0, svn);
+      if constexpr (STORE) {
+        if (m == SC_SLOT0) store_chunk(j, 0, ds0);
+        if (m == SC_SLOT1) store_chunk(j, 1, dsb[1]);
+      }
 #pragma unroll
       for (int li = 0; li < C::LOADS; ++li) {
         if (li * NS / C::LOADS == m) issue_load(s_req, j + 3, li);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (STORE) {
-      store_chunk(j, 0, dsb[0]);
-      store_chunk(j, 1, dsb[1]);
-    }
   };
   static_assert(A1 + 2 + AS * 3 < NMA + 2 * DB, "chunk 1 is packed before its first update MFMA");
   static_assert(B1 + 2 + BS * 3 < NS, "chunk 0 of the next tile is packed within the step");
   static_assert(STAT_SLOT < B1, "statistics of the next tile are requested before their first use");
+  static_assert(!STORE || (NS == 32 && A1 + 2 + AS * 3 < SC_SLOT1), "chunk 1 is packed before its store");
   // final tile: chunk 1 values then the update MFMAs
   auto last_step = [&](auto kk, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], const i32x4_t& pb0,
                        const i32x4_t& ds0) {

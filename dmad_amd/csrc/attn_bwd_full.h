@@ -79,9 +79,11 @@ __device__ __forceinline__ FullVals full_values(float s, float sd_raw, float dpd
 
 // STORE: also writes each tile's dS and dSd (the operands of the dK updates,
 // keys at or beyond Lk as zeros) to p.sc in the ScLayout (tensor 0 = dS,
-// 1 = dSd) for attn_bwd_dq_sc_kernel. Tile j's four chunks leave at the end of
-// step j, after the step's ring requests, so the next barrier's vmcnt counts
-// them among the operations it lets stay in flight.
+// 1 = dSd) for attn_bwd_dq_sc_kernel: tile j's four chunks leave in phase B of
+// step j, one every eight update MFMAs, between the ring requests. The next
+// barrier's vmcnt(LOADS) stays exact whatever order stores and loads complete
+// in: a request of tile j + 2 still in flight means all LOADS requests of tile
+// j + 3 are too.
 template <typename T, int D, bool STORE = false>
 __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
   using C = KvFullCfg<D>;
@@ -110,18 +112,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
   const uint32_t sc_kb = (uint32_t)(kt * 4 + wave) * 2 * ScLayout::PIECE;
   const uint32_t sc_lo0 = ScLayout::lane_off(col, half, 0), sc_lo1 = ScLayout::lane_off(col, half, 1);
   const bool sc_tail = (kt + 1) * C::BK > p.Lk;  // keys at or beyond Lk in this workgroup
-  auto store_tile = [&](int qt, const i32x4_t (&ds)[2], const i32x4_t (&dsd)[2]) {
+  // chunk u of tensor t (0: dS, 1: dSd) of tile qt
+  auto store_chunk = [&](int qt, int t, int u, i32x4_t v) {
+    if (sc_tail && key >= p.Lk) v = i32x4_t{0, 0, 0, 0};
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)sc_strip);
-    const uint32_t so = sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        i32x4_t v = t ? dsd[u] : ds[u];
-        if (sc_tail && key >= p.Lk) v = i32x4_t{0, 0, 0, 0};
-        buf_store16(rs, v, u ? sc_lo1 : sc_lo0, so + (uint32_t)t * ScLayout::PIECE + (uint32_t)u * ScLayout::CHUNK);
-      }
-    }
+    buf_store16_stream(rs, v, u ? sc_lo1 : sc_lo0,
+                       sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE + (uint32_t)t * ScLayout::PIECE +
+                           (uint32_t)u * ScLayout::CHUNK);
   };
 
   // ---- stationary K, Kd, V, Vd rows (B operands of the score MFMAs), kept in AGPRs
@@ -346,9 +343,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
       for (int li = 0; li < C::LOADS; ++li) {
         if (NOPA + li * NOPB / C::LOADS == o) issue_load(s_req, j + 3, li);
       }
+      if constexpr (STORE) {
+        // phase-B slots 4, 12, 20, 28: dS chunks 0, 1, then dSd chunks 0, 1
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (o == NOPA + 4 + 8 * c) store_chunk(j, c >> 1, c & 1, (c >> 1) ? pk.dsd[c & 1] : pk.ds[c & 1]);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (STORE) store_tile(j, pk.ds, pk.dsd);
   };
   static_assert(NOPA == 32 && 4 * 7 + 1 < NOPA, "eight value pairs ride in the 32 phase-A slots");
   // last tile: its values, then its update MFMAs
@@ -364,7 +367,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
     }
     asm volatile("" : "+v"(pk.p[0]), "+v"(pk.p[1]), "+v"(pk.pd[0]), "+v"(pk.pd[1]));
     asm volatile("" : "+v"(pk.ds[0]), "+v"(pk.ds[1]), "+v"(pk.dsd[0]), "+v"(pk.dsd[1]));
-    if constexpr (STORE) store_tile(nqt - 1, pk.ds, pk.dsd);
+    if constexpr (STORE) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) store_chunk(nqt - 1, c >> 1, c & 1, (c >> 1) ? pk.dsd[c & 1] : pk.ds[c & 1]);
+    }
     Scores un;
 #pragma unroll
     for (int o = NOPA; o < NOP; ++o) mfma_op(o, load_op(s_cur, s_cur, o), un, pk);

@@ -40,7 +40,7 @@ static hipError_t kv_sc_launch(const BwdParams& p, int grid, hipStream_t s) {
 }
 template <typename T>
 static hipError_t dq_sc1_launch(const DqParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_bwd_dq_sc_kernel<T, 1>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_bwd_dq_sc_kernel<T, 1>), dim3(grid), dim3(DqScCfg<1>::NW * 64), 0, s, p);
   return hipGetLastError();
 }
 template <>

@@ -450,9 +450,10 @@ BwdPlan plan_bwd_ws(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int6
   if (pl.sc > 0) {
     pl.kv = full ? "attn_bwd_kv_full_kernel<store>" : "attn_bwd_kv_tr_kernel<store>";
     pl.dq = "attn_bwd_dq_sc_kernel";
+    const int64_t npair = ((Lq + 127) / 128 + 1) / 2;  // two 128-query blocks per query-pass workgroup
     pl.grid_kv = (Lk + 127) / 128 * pl.sc;
-    pl.grid_dq = (Lq + 127) / 128 * pl.sc;
-    pl.xcd_dq = (Lq + 127) / 128 < dmad::kHeadMajorMinTiles;
+    pl.grid_dq = npair * pl.sc;
+    pl.xcd_dq = npair < dmad::kHeadMajorMinTiles;
     pl.ws += pl.sc * score_slice_bytes(full, Lq, Lk);
   }
   return pl;
@@ -874,13 +875,13 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
     const dmad::BwdLaunchFn fs = pick_kv_sc(dtype, full);
     const dmad::DqLaunchFn fqs = pick_dq_sc(dtype, full);
     if (fs == nullptr || fqs == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no stored-score backward kernel");
-    const int64_t nkt = (Lk + 127) / 128, nqb = (Lq + 127) / 128;
+    const int64_t nkt = (Lk + 127) / 128, nqw = ((Lq + 127) / 128 + 1) / 2;  // query-pass workgroups per slice
     p.sc = ws + w.total;
     p.sc_slice = score_slice_bytes(full, Lq, Lk);
     pq.sc = p.sc;
     pq.sc_slice = p.sc_slice;
     pq.sc_nkb = (int)(4 * nkt);
-    pq.xcd_order = nqb < dmad::kHeadMajorMinTiles;
+    pq.xcd_order = nqw < dmad::kHeadMajorMinTiles;
     int ev = 0;
     for (int64_t bh0 = 0; bh0 < BH; bh0 += sc) {
       const int64_t n = BH - bh0 < sc ? BH - bh0 : sc;
@@ -889,7 +890,7 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
       if ((e = fs(p, (int)(n * nkt), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
       mark(ev++, true, s);
       mark(ev, false, s);
-      if ((e = fqs(pq, (int)(n * nqb), s)) != hipSuccess)
+      if ((e = fqs(pq, (int)(n * nqw), s)) != hipSuccess)
         return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
       mark(ev++, true, s);
     }

@@ -218,7 +218,7 @@ def test_stored_score_plan_follows_the_workspace(full):
     assert p["score_slices"] == 3
     assert p["kernel"] == ("attn_bwd_kv_full_kernel<store>" if full else "attn_bwd_kv_tr_kernel<store>")
     assert p["kernel2"] == "attn_bwd_dq_sc_kernel"
-    assert (p["grid"], p["grid2"]) == (3 * 256, 3 * 256)
+    assert (p["grid"], p["grid2"]) == (3 * 256, 3 * 128)  # two 128-query blocks per query-pass workgroup
     assert p["workspace_bytes"] == base["workspace_bytes"] + 3 * one
     assert p["kernel3"] == base["kernel3"]  # the tangent key pass is unchanged
     # the minimum workspace, or less than one slice beyond it, keeps the recomputing passes
