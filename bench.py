@@ -556,6 +556,8 @@ def main():
                         "score_slices_per_pair": bplan["score_slices"]},
         "kernel_pct_peak": {n: round(100 * k_flops[n] / (k_ms[n] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)
                             for n in k_ms},
+        # the whole dO-only backward (both passes, every launch pair) on the reference's 10 units
+        "bwd_pct_peak": round(100 * f_bwd / ((k_ms["bwd_dkdv"] + k_ms["bwd_dq"]) * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
         "roofline": {
             "kernel": dom_name,
             "bound": "mfma",

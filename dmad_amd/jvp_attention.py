@@ -127,6 +127,13 @@ def backward_score_budget() -> int:
 _SCORE_MIN_LEN_DOUT_ONLY = 4096
 
 
+# A launch pair covering fewer slices than B*H should give its key pass at least
+# this many workgroups (four per CU): with fewer, the last partly filled round of
+# every pair idles a large share of the CUs (720p, one 11.4 GB slice per pair:
+# 591 workgroups, 2.3 rounds), and the recomputing passes are kept instead.
+_SCORE_MIN_KEY_WORKGROUPS = 4 * 256
+
+
 def _score_bytes(code: int, full: bool, B: int, H: int, Lq: int, Lk: int, D: int) -> int:
     """Workspace bytes for stored score gradients within the budget (whole (b, h) slices)."""
     if not full and min(Lq, Lk) < _SCORE_MIN_LEN_DOUT_ONLY:
@@ -134,7 +141,10 @@ def _score_bytes(code: int, full: bool, B: int, H: int, Lq: int, Lk: int, D: int
     one = nat.bwd_score_bytes(code, full, Lq, Lk, D) if _SCORE_BUDGET > 0 else 0
     if one == 0 or _SCORE_BUDGET < one:
         return 0
-    return min(B * H, _SCORE_BUDGET // one) * one
+    n = min(B * H, _SCORE_BUDGET // one)
+    if n < B * H and n * ((Lk + 127) // 128) < _SCORE_MIN_KEY_WORKGROUPS:
+        return 0
+    return n * one
 
 
 def backward_plan(dtype: torch.dtype, B: int, H: int, Lq: int, Lk: int, D: int, full: bool = False,

@@ -258,6 +258,14 @@ def test_python_score_budget():
         assert ja._score_bytes(BF16, False, 1, 2, 4096, 4095, 128) == 0
         assert ja._score_bytes(BF16, False, 1, 2, 4096, 4096, 128) == 2 * nat.bwd_score_bytes(BF16, False, 4096, 4096, 128)
         assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 64) == 0
+        # a pair of fewer than B*H slices keeps at least four key-pass workgroups per CU
+        one720 = nat.bwd_score_bytes(BF16, False, 75600, 75600, 128)
+        ja.set_backward_score_budget(16 << 30)  # one 11.4 GB slice: 591 workgroups per pair
+        assert ja._score_bytes(BF16, False, 1, 40, 75600, 75600, 128) == 0
+        ja.set_backward_score_budget(2 * one720)  # 1182 workgroups per pair
+        assert ja._score_bytes(BF16, False, 1, 40, 75600, 75600, 128) == 2 * one720
+        ja.set_backward_score_budget(one720)  # one slice, but it is all of them
+        assert ja._score_bytes(BF16, False, 1, 1, 75600, 75600, 128) == one720
         with pytest.raises(ValueError):
             ja.set_backward_score_budget(-1)
     finally:
