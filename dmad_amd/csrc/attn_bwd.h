@@ -91,6 +91,11 @@ struct ScLayout {
   static constexpr int PIECE = 8192;      // one tensor's (query block, key block) piece
   static constexpr int TILE = 2048;       // one 32-query tile of a piece
   static constexpr int CHUNK = 1024;      // one 16-query chunk of a tile
+  // Query blocks' strips start STRIP_PAD bytes apart beyond their size: the
+  // query pass streams all strips of a slice at once, and strips an exact
+  // power of two apart read 2-4% slower (5.80 against 6.05 TB/s at the 14B shape).
+  static constexpr int STRIP_PAD = 20480;
+  __host__ __device__ static int64_t strip_stride(int64_t nkb, int nt) { return nkb * nt * PIECE + STRIP_PAD; }
   // byte offset of lane (key col, half)'s 16 bytes within chunk u
   __device__ __forceinline__ static uint32_t lane_off(int col, int half, int u) {
     return (uint32_t)((((col ^ (4 * u)) * 2) + half) * 16);
@@ -99,7 +104,7 @@ struct ScLayout {
 // Bytes of one (b, h) slice: NT tensors over Lq rounded up to 128 queries and
 // `nkb` key blocks (the key pass covers nkt * 128 keys: nkb = 4 nkt).
 __host__ __device__ inline int64_t sc_slice_bytes(int64_t lq, int64_t nkb, int nt) {
-  return (lq + ScLayout::BQ - 1) / ScLayout::BQ * nkb * nt * ScLayout::PIECE;
+  return (lq + ScLayout::BQ - 1) / ScLayout::BQ * ScLayout::strip_stride(nkb, nt);
 }
 
 template <int D, int MODE>
@@ -805,14 +810,15 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   const int key = kt * C::BK + wave * 32 + col;
 
   // ---- score-gradient stores (STORE): this wave's key block of the slice's strips
-  const int64_t sc_strip = (int64_t)nkt * 4 * ScLayout::PIECE;  // one query block, one tensor
+  const int64_t sc_strip = ScLayout::strip_stride(4 * nkt, 1);  // one query block, one tensor
   char* const sc_base = STORE ? (char*)p.sc + (int64_t)slice * p.sc_slice : nullptr;
   const uint32_t sc_kb = (uint32_t)(kt * 4 + wave) * ScLayout::PIECE;
   const uint32_t sc_lo0 = ScLayout::lane_off(col, half, 0), sc_lo1 = ScLayout::lane_off(col, half, 1);
   const bool sc_tail = (kt + 1) * C::BK > p.Lk;  // keys at or beyond Lk in this workgroup
   auto store_chunk = [&](int qt, int u, i32x4_t v) {
     if (sc_tail && key >= p.Lk) v = i32x4_t{0, 0, 0, 0};
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)sc_strip);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)(sc_strip - ScLayout::STRIP_PAD));
     buf_store16_stream(rs, v, u ? sc_lo1 : sc_lo0,
                        sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE + (uint32_t)u * ScLayout::CHUNK);
   };

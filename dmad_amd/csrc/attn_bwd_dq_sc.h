@@ -85,10 +85,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_sc_kernel(DqParams p) {
   const __amdgpu_buffer_rsrc_t rtk = make_rsrc((const char*)(NT == 2 ? p.tk : p.k) + khead * 2, k_bytes);
   const uint32_t k_step = (uint32_t)((int64_t)BN * p.k_sl * 2);
   const uint32_t strip = (uint32_t)p.sc_nkb * NT * ScLayout::PIECE;
+  const int64_t stride = ScLayout::strip_stride(p.sc_nkb, NT);
   const char* sc_slice = (const char*)p.sc + (int64_t)slice * p.sc_slice;
   const int qb0 = 2 * qbp, qb1 = 2 * qbp + 1 < nqb ? 2 * qbp + 1 : nqb - 1;
-  const __amdgpu_buffer_rsrc_t rsc0 = make_rsrc(sc_slice + (int64_t)qb0 * strip, strip);
-  const __amdgpu_buffer_rsrc_t rsc1 = make_rsrc(sc_slice + (int64_t)qb1 * strip, strip);
+  const __amdgpu_buffer_rsrc_t rsc0 = make_rsrc(sc_slice + (int64_t)qb0 * stride, strip);
+  const __amdgpu_buffer_rsrc_t rsc1 = make_rsrc(sc_slice + (int64_t)qb1 * stride, strip);
 
   // request i (0 <= i < NREQ; wave w issues i = w, w + NW, ...) of step jj into
   // stage st: rows of K [and Kd] (1 KiB each), then the pieces of block 0 and

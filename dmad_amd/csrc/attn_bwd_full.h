@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
   const int key = kt * C::BK + wave * 32 + col;
 
   // ---- score-gradient stores (STORE): this wave's key block of the slice's strips
-  const int64_t sc_strip = (int64_t)nkt * 4 * 2 * ScLayout::PIECE;  // one query block, both tensors
+  const int64_t sc_strip = ScLayout::strip_stride(4 * nkt, 2);  // one query block, both tensors
   char* const sc_base = STORE ? (char*)p.sc + (int64_t)slice * p.sc_slice : nullptr;
   const uint32_t sc_kb = (uint32_t)(kt * 4 + wave) * 2 * ScLayout::PIECE;
   const uint32_t sc_lo0 = ScLayout::lane_off(col, half, 0), sc_lo1 = ScLayout::lane_off(col, half, 1);
@@ -115,7 +115,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kv_full_kernel(BwdParams p) {
   // chunk u of tensor t (0: dS, 1: dSd) of tile qt
   auto store_chunk = [&](int qt, int t, int u, i32x4_t v) {
     if (sc_tail && key >= p.Lk) v = i32x4_t{0, 0, 0, 0};
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)sc_strip);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(sc_base + (int64_t)(qt >> 2) * sc_strip, (uint32_t)(sc_strip - ScLayout::STRIP_PAD));
     buf_store16_stream(rs, v, u ? sc_lo1 : sc_lo0,
                        sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE + (uint32_t)t * ScLayout::PIECE +
                            (uint32_t)u * ScLayout::CHUNK);

@@ -103,9 +103,10 @@ def set_backward_mode(mode: str) -> None:
 # Device memory (bytes) the backward of 128-wide bf16/fp16 heads may take, per
 # call and on top of its minimum workspace, for stored score gradients: its key
 # pass then writes dS (and dSd) and the query pass reads them back instead of
-# recomputing the scores, as many (b, h) slices per launch pair as fit. 0 turns
-# the path off. Environment default: DMAD_BWD_SCORE_BUDGET_MB.
-_SCORE_BUDGET = int(os.environ.get("DMAD_BWD_SCORE_BUDGET_MB", "16384")) << 20
+# recomputing the scores, up to as many (b, h) slices per launch pair as fit. 0
+# turns the path off. Environment default: DMAD_BWD_SCORE_BUDGET_MB (18 GiB: eight
+# dO-only or four full-derivative slices of a Wan2.1-14B layer, 2.15 / 4.3 GB each).
+_SCORE_BUDGET = int(os.environ.get("DMAD_BWD_SCORE_BUDGET_MB", "18432")) << 20
 
 
 def set_backward_score_budget(nbytes: int) -> None:
@@ -141,10 +142,31 @@ def _score_bytes(code: int, full: bool, B: int, H: int, Lq: int, Lk: int, D: int
     one = nat.bwd_score_bytes(code, full, Lq, Lk, D) if _SCORE_BUDGET > 0 else 0
     if one == 0 or _SCORE_BUDGET < one:
         return 0
-    n = min(B * H, _SCORE_BUDGET // one)
+    n = _score_slices(B * H, min(B * H, _SCORE_BUDGET // one), Lq, Lk)
     if n < B * H and n * ((Lk + 127) // 128) < _SCORE_MIN_KEY_WORKGROUPS:
         return 0
     return n * one
+
+
+def _score_slices(bh: int, n_max: int, Lq: int, Lk: int) -> int:
+    """(b, h) slices per launch pair, at most n_max: the count whose pairs fill the 256 CUs
+    best. A pair of n slices runs n * key tiles key-pass workgroups and n * query-block
+    pairs query-pass workgroups, one per CU at a time; every partly filled last round
+    costs a whole round. Rounds are weighted by their measured lengths (a key-pass round
+    ~1.4 query-pass rounds at equal Lq = Lk); ties go to more slices."""
+    nkt = (Lk + 127) // 128
+    nqw = ((Lq + 127) // 128 + 1) // 2
+
+    def rounds(m):
+        return 1.4 * (-(-m * nkt // 256)) + (-(-m * nqw // 256))
+
+    best, best_cost = n_max, None
+    for n in range(n_max, max(1, n_max // 2) - 1, -1):
+        full, rest = divmod(bh, n)
+        cost = full * rounds(n) + (rounds(rest) if rest else 0.0)
+        if best_cost is None or cost < best_cost - 1e-9:
+            best, best_cost = n, cost
+    return best
 
 
 def backward_plan(dtype: torch.dtype, B: int, H: int, Lq: int, Lk: int, D: int, full: bool = False,

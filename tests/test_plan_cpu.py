@@ -194,13 +194,18 @@ def test_argument_checks():
 
 def test_stored_score_sizes():
     """Bytes per (b, h) slice of stored score gradients: dS (and dSd) in bf16/fp16 over Lq
-    rounded up to 128 queries and the key pass's 128-key tiles; none for other head dims and fp32."""
+    rounded up to 128 queries and the key pass's 128-key tiles, one strip per 128-query block
+    padded by 20 KiB; none for other head dims and fp32."""
+    def size(lq, lk, nt):
+        strip = (lk + 127) // 128 * 128 * 128 * 2 * nt + 20480
+        return -(-((lq + 127) // 128 * strip) // 256) * 256
+
     gib = 1 << 30
     for dt in (BF16, F16):
-        assert nat.bwd_score_bytes(dt, False, 32760, 32760, 128) == 2 * gib  # 256 x 256 pieces of 32 KiB
-        assert nat.bwd_score_bytes(dt, True, 32760, 32760, 128) == 4 * gib
-        assert nat.bwd_score_bytes(dt, False, 1, 1, 128) == 128 * 128 * 2
-        assert nat.bwd_score_bytes(dt, True, 300, 700, 128) == 384 * 768 * 2 * 2
+        assert nat.bwd_score_bytes(dt, False, 32760, 32760, 128) == size(32760, 32760, 1) == 2 * gib + 256 * 20480
+        assert nat.bwd_score_bytes(dt, True, 32760, 32760, 128) == size(32760, 32760, 2) == 4 * gib + 256 * 20480
+        assert nat.bwd_score_bytes(dt, False, 1, 1, 128) == 128 * 128 * 2 + 20480
+        assert nat.bwd_score_bytes(dt, True, 300, 700, 128) == size(300, 700, 2) == 384 * 768 * 2 * 2 + 3 * 20480
     assert nat.bwd_score_bytes(F32, False, 4096, 4096, 128) == 0
     for D in (16, 32, 64, 256):
         assert nat.bwd_score_bytes(BF16, False, 4096, 4096, D) == 0
@@ -245,8 +250,15 @@ def test_python_score_budget():
     one = nat.bwd_score_bytes(BF16, False, 32760, 32760, 128)
     old = ja.backward_score_budget()
     try:
-        ja.set_backward_score_budget(16 << 30)
+        ja.set_backward_score_budget(18 << 30)
         assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128) == 8 * one
+        assert ja._score_bytes(BF16, True, 1, 40, 32760, 32760, 128) == \
+            4 * nat.bwd_score_bytes(BF16, True, 32760, 32760, 128)
+        # 7 slices fit in 16 GiB, but pairs of 7 leave the query pass's last round half
+        # empty (896 workgroups); pairs of 6 fill it (768, and a last pair of 4: 512)
+        ja.set_backward_score_budget(16 << 30)
+        assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128) == 6 * one
+        assert ja._score_slices(40, 8, 32760, 32760) == 8
         ja.set_backward_score_budget(0)
         assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128) == 0
         ja.set_backward_score_budget(one - 1)
@@ -260,7 +272,7 @@ def test_python_score_budget():
         assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 64) == 0
         # a pair of fewer than B*H slices keeps at least four key-pass workgroups per CU
         one720 = nat.bwd_score_bytes(BF16, False, 75600, 75600, 128)
-        ja.set_backward_score_budget(16 << 30)  # one 11.4 GB slice: 591 workgroups per pair
+        ja.set_backward_score_budget(18 << 30)  # one 11.4 GB slice: 591 workgroups per pair
         assert ja._score_bytes(BF16, False, 1, 40, 75600, 75600, 128) == 0
         ja.set_backward_score_budget(2 * one720)  # 1182 workgroups per pair
         assert ja._score_bytes(BF16, False, 1, 40, 75600, 75600, 128) == 2 * one720

@@ -24,12 +24,14 @@ DTYPES = [torch.bfloat16, torch.float16]
 
 @pytest.fixture
 def budget(monkeypatch):
-    """Sets the stored-score budget for one test (the dO-only backward's length threshold
-    lifted, so that short sequences take the path too) and restores the process default."""
+    """Sets the stored-score budget for one test (the dO-only backward's length threshold and
+    the minimum workgroups per launch pair lifted, so that short sequences and one-slice pairs
+    take the path too) and restores the process default."""
     import dmad_amd
     from dmad_amd import jvp_attention as ja
 
     monkeypatch.setattr(ja, "_SCORE_MIN_LEN_DOUT_ONLY", 0)
+    monkeypatch.setattr(ja, "_SCORE_MIN_KEY_WORKGROUPS", 0)
     old = dmad_amd.backward_score_budget()
     yield dmad_amd.set_backward_score_budget
     dmad_amd.set_backward_score_budget(old)
