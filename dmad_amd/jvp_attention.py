@@ -122,10 +122,11 @@ def backward_score_budget() -> int:
     return _SCORE_BUDGET
 
 
-# The dO-only backward stores its scores from this many queries and keys on: below it
-# the recomputing query pass measured as fast or faster (the stores cost the key pass
-# about a fifth of its time; the full derivative's query pass saves more than that).
-_SCORE_MIN_LEN_DOUT_ONLY = 4096
+# The dO-only backward stores its scores from this many queries and keys on: at 1024
+# the recomputing query pass measured as fast (B=4, H=32, fp16: within 1% either way;
+# 2048: the stored scores 4-7% faster). The stores cost the key pass about 15% of its
+# time; the full derivative's query pass saves more than that at every length.
+_SCORE_MIN_LEN_DOUT_ONLY = 2048
 
 
 # A launch pair covering fewer slices than B*H should give its key pass at least

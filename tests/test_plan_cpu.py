@@ -265,10 +265,10 @@ def test_python_score_budget():
         assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128) == 0
         ja.set_backward_score_budget(1 << 50)
         assert ja._score_bytes(BF16, True, 2, 3, 300, 300, 128) == 6 * nat.bwd_score_bytes(BF16, True, 300, 300, 128)
-        # the dO-only backward keeps the recomputing passes below 4096 queries or keys
+        # the dO-only backward keeps the recomputing passes below 2048 queries or keys
         assert ja._score_bytes(BF16, False, 2, 3, 300, 300, 128) == 0
-        assert ja._score_bytes(BF16, False, 1, 2, 4096, 4095, 128) == 0
-        assert ja._score_bytes(BF16, False, 1, 2, 4096, 4096, 128) == 2 * nat.bwd_score_bytes(BF16, False, 4096, 4096, 128)
+        assert ja._score_bytes(BF16, False, 1, 2, 4096, 2047, 128) == 0
+        assert ja._score_bytes(BF16, False, 1, 2, 2048, 2048, 128) == 2 * nat.bwd_score_bytes(BF16, False, 2048, 2048, 128)
         assert ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 64) == 0
         # a pair of fewer than B*H slices keeps at least four key-pass workgroups per CU
         one720 = nat.bwd_score_bytes(BF16, False, 75600, 75600, 128)
