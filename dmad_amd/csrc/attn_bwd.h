@@ -775,26 +775,44 @@ struct KvTrCfg {
 // Query tile of attn_bwd_kv_tr_kernel.
 constexpr int kKvTrBmq = 32;
 
+// What attn_bwd_kv_tr_kernel does with stored score gradients (ScLayout).
+enum KvScMode : int {
+  kScNone = 0,   // nothing stored or read
+  kScStore = 1,  // writes each tile's dS (dO-only backward: the query pass reads it back)
+  kScLoad = 2    // reads dS (tensor 1 of a full-derivative layout: dSd) instead of computing dP, dS
+};
+
 // Compiled with MFMAs in VGPR form (bwd_kv_inst.hip): the S, dP MFMAs write
 // VGPRs that the VALU reads directly, and the dK, dV accumulators stay in
 // AGPRs through inline MFMAs (mfma32_acc).
-// STORE (128-wide heads): also writes each tile's dS (the bf16/fp16 operand of
-// the dK update, keys at or beyond Lk as zeros) to p.sc in the ScLayout for
-// attn_bwd_dq_sc_kernel, chunk 0 of tile j in slot 14 of step j and chunk 1
-// (packed by slot 13) in slot 28, between the step's ring requests. The next
-// barrier's vmcnt(LOADS) stays exact whatever order stores and loads complete
-// in: a request of tile j + 2 still in flight means all LOADS requests of tile
-// j + 3 are too.
-template <typename T, int D, bool STORE = false>
+// SCM == kScStore (128-wide heads): also writes each tile's dS (the bf16/fp16
+// operand of the dK update, keys at or beyond Lk as zeros) to p.sc in the
+// ScLayout for attn_bwd_dq_sc_kernel, chunk 0 of tile j in slot 14 of step j
+// and chunk 1 (packed by slot 13) in slot 28, between the step's ring requests.
+// The next barrier's vmcnt(LOADS) stays exact whatever order stores and loads
+// complete in: a request of tile j + 2 still in flight means all LOADS requests
+// of tile j + 3 are too.
+// SCM == kScLoad (128-wide heads; the full derivative's tangent key pass, run on
+// (dO, D) := (dOd, rho)): dS = P (dP - D) is the dSd the full key pass stored
+// (tensor 1 of its layout), so the pass reads it instead of computing dP: each
+// wave's two 1 KiB chunks of a tile ride in the ring stage with the Q and dO
+// rows (a lane's 16 bytes land where it reads them), V is not read, and a step
+// runs 8 S MFMAs and 16 update MFMAs instead of 32.
+template <typename T, int D, int SCM = kScNone>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(BwdParams p) {
   using C = KvTrCfg<D, kKvTrBmq>;
   constexpr int BMQ = C::BMQ, NQB = C::NQB, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
+  constexpr bool STORE = SCM == kScStore, LOAD = SCM == kScLoad;
   static_assert(C::FITS, "configuration does not fit");
-  static_assert(!STORE || D == 128, "score stores are laid out for 128-wide heads");
-  __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) char stg3[C::STAGE];
+  static_assert(SCM == kScNone || D == 128, "stored score gradients are laid out for 128-wide heads");
+  // the loaded dS chunks follow the stage's rows and statistics: 2 KiB per wave
+  constexpr int OFF_DS = C::STAGE, STAGE = C::STAGE + (LOAD ? C::NW * 2 * ScLayout::CHUNK : 0);
+  constexpr int LOADS = C::LOADS + (LOAD ? 2 : 0);  // requests per wave per tile
+  static_assert(4 * STAGE <= 160 * 1024, "the ring fits the LDS");
+  __shared__ __attribute__((aligned(1024))) char stg0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg1[STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg2[STAGE];
+  __shared__ __attribute__((aligned(1024))) char stg3[STAGE];
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -803,16 +821,18 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   const int nkt = (p.Lk + C::BK - 1) / C::BK;
   const int work = work_item(p.xcd_order);  // block order (common.h)
   const int slice = work / nkt, kt = work - slice * nkt;
-  const int bh = (STORE ? p.bh0 : 0) + slice;
+  const int bh = (SCM != kScNone ? p.bh0 : 0) + slice;
   const int b = bh / p.H, h = bh - b * p.H;
   const int nqt = p.LQP / BMQ;
 
   const int key = kt * C::BK + wave * 32 + col;
 
-  // ---- score-gradient stores (STORE): this wave's key block of the slice's strips
-  const int64_t sc_strip = ScLayout::strip_stride(4 * nkt, 1);  // one query block, one tensor
-  char* const sc_base = STORE ? (char*)p.sc + (int64_t)slice * p.sc_slice : nullptr;
-  const uint32_t sc_kb = (uint32_t)(kt * 4 + wave) * ScLayout::PIECE;
+  // ---- stored score gradients (STORE: dS written; LOAD: tensor 1 of a full
+  // layout read): this wave's key block of the slice's strips
+  constexpr int SC_NT = LOAD ? 2 : 1;
+  const int64_t sc_strip = ScLayout::strip_stride(4 * nkt, SC_NT);  // one query block
+  char* const sc_base = SCM != kScNone ? (char*)p.sc + (int64_t)slice * p.sc_slice : nullptr;
+  const uint32_t sc_kb = (uint32_t)(kt * 4 + wave) * SC_NT * ScLayout::PIECE + (LOAD ? ScLayout::PIECE : 0);
   const uint32_t sc_lo0 = ScLayout::lane_off(col, half, 0), sc_lo1 = ScLayout::lane_off(col, half, 1);
   const bool sc_tail = (kt + 1) * C::BK > p.Lk;  // keys at or beyond Lk in this workgroup
   auto store_chunk = [&](int qt, int u, i32x4_t v) {
@@ -823,7 +843,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
                        sc_kb + (uint32_t)(qt & 3) * ScLayout::TILE + (uint32_t)u * ScLayout::CHUNK);
   };
 
-  // ---- stationary K, V rows: B operands of S = Q K^T and dP = dO V^T
+  // ---- stationary K, V rows: B operands of S = Q K^T and dP = dO V^T (LOAD: K only)
   const uint32_t k_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.k_sl + D) * 2);
   const uint32_t v_bytes = (uint32_t)(((int64_t)(p.Lk - 1) * p.v_sl + D) * 2);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc((const char*)p.k + (b * p.k_sb + h * p.k_sh) * 2, k_bytes);
@@ -835,7 +855,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       kreg[s] = buf_load16(rk, ko + s * 32);
-      vreg[s] = buf_load16(rv, vo + s * 32);
+      if constexpr (!LOAD) vreg[s] = buf_load16(rv, vo + s * 32);
     }
   }
 
@@ -868,15 +888,23 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
     else if constexpr (k == 2) return (lds_char_t*)stg2;
     else return (lds_char_t*)stg3;
   };
-  // request li (0 <= li < C::LOADS) of tile qt into stage st; tiles at or beyond
-  // the end read zeros or in-range rows into a stage nobody reads again
+  // request li (0 <= li < LOADS) of tile qt into stage st; tiles at or beyond
+  // the end read zeros or in-range rows into a stage nobody reads again (the
+  // loaded dS chunks of such tiles are the last tile's again: a strip beyond the
+  // slice does not exist)
   auto issue_load = [&](lds_char_t* st, int qt, int li) {
     if (li < 2 * RPW) {
       const int jj = li >> 1, i = wave + jj * C::NW;
       if (li & 1) buf_load16_lds(rdo, st + C::OFF_DO + i * 1024, roff_do[jj], (uint32_t)qt * do_step);
       else buf_load16_lds(rq, st + C::OFF_Q + i * 1024, roff_q[jj], (uint32_t)qt * q_step);
-    } else {
+    } else if (li == 2 * RPW) {
       if (st_lane) buf_load16_lds(rst, st + C::OFF_ST, lane * 16, (uint32_t)qt * C::STAT_BYTES);
+    } else if constexpr (LOAD) {
+      const int u = li - 2 * RPW - 1, qc = qt < nqt ? qt : nqt - 1;
+      const __amdgpu_buffer_rsrc_t rs =
+          make_rsrc(sc_base + (int64_t)(qc >> 2) * sc_strip, (uint32_t)(sc_strip - ScLayout::STRIP_PAD));
+      buf_load16_lds(rs, st + OFF_DS + wave * 2 * ScLayout::CHUNK + u * ScLayout::CHUNK, u ? sc_lo1 : sc_lo0,
+                     sc_kb + (uint32_t)(qc & 3) * ScLayout::TILE + (uint32_t)u * ScLayout::CHUNK);
     }
   };
 
@@ -925,7 +953,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   // so the compiler can fit two waves per SIMD in 256 registers)
   constexpr bool kAccAgpr = D == 128;
   constexpr int PF = 4;
-  constexpr int NMA = 2 * KS * NQB;   // S, dP MFMAs
+  constexpr int NMA = (LOAD ? 1 : 2) * KS * NQB;   // S, dP MFMAs (LOAD: S)
   constexpr int NMB = 4 * NQB * DB;   // dV^T, dK^T MFMAs
   constexpr int NS = NMA + NMB;
   constexpr int NVAL = 16 * NQB;      // P, dS values per lane per tile
@@ -933,6 +961,9 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   // operand m: m < NMA reads Q / dO rows of the next tile (s = m / (2 NQB)),
   // otherwise dO^T / Q^T of this tile (u = 16-query chunk, db = 32-row d block)
   auto load_op = [&](const lds_char_t* s_next, const lds_char_t* s_cur, int m) -> i32x4_t {
+    if constexpr (LOAD) {
+      if (m < NMA) return *(lds_i32x4_t*)(s_next + C::OFF_Q + (m % NQB) * 32 * ROWB + sx[m / NQB]);
+    }
     if (m < NMA) {
       const int s = m / (2 * NQB), r = m % (2 * NQB), qb = r >> 1;
       return *(lds_i32x4_t*)(s_next + ((r & 1) ? C::OFF_DO : C::OFF_Q) + qb * 32 * ROWB + sx[s]);
@@ -970,17 +1001,33 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
       const float l2 = sv.l[e >> 2][e & 3], dl = sv.d[e >> 2][e & 3];
       // re-define the inputs here (an empty asm) so the compiler cannot hoist the
       // arithmetic out of its MFMA slot and bunch the VALU work together
-      float s_in = sc[v], d_in = dpc[v];
-      asm volatile("" : "+v"(s_in), "+v"(d_in));
-      hv.p[w] = fast_exp2(fmaf(s_in, p.scale_log2, -l2));
-      hv.dd[w] = d_in - dl;
+      if constexpr (LOAD) {
+        float s_in = sc[v];
+        asm volatile("" : "+v"(s_in));
+        hv.p[w] = fast_exp2(fmaf(s_in, p.scale_log2, -l2));
+      } else {
+        float s_in = sc[v], d_in = dpc[v];
+        asm volatile("" : "+v"(s_in), "+v"(d_in));
+        hv.p[w] = fast_exp2(fmaf(s_in, p.scale_log2, -l2));
+        hv.dd[w] = d_in - dl;
+      }
     }
   };
   auto pair_second = [&](int i, Half& hv, i32x4_t& pbu, i32x4_t& dsbu) {
-    asm volatile("" : "+v"(hv.p[0]), "+v"(hv.p[1]), "+v"(hv.dd[0]), "+v"(hv.dd[1]));
-    pbu[i] = (int)Elem<T>::pack2(hv.p[0], hv.p[1]);
-    dsbu[i] = (int)Elem<T>::pack2(hv.p[0] * hv.dd[0], hv.p[1] * hv.dd[1]);
-    asm volatile("" : "+v"(pbu[i]), "+v"(dsbu[i]));
+    if constexpr (LOAD) {  // P~ only: dS~ is loaded
+      asm volatile("" : "+v"(hv.p[0]), "+v"(hv.p[1]));
+      pbu[i] = (int)Elem<T>::pack2(hv.p[0], hv.p[1]);
+      asm volatile("" : "+v"(pbu[i]));
+    } else {
+      asm volatile("" : "+v"(hv.p[0]), "+v"(hv.p[1]), "+v"(hv.dd[0]), "+v"(hv.dd[1]));
+      pbu[i] = (int)Elem<T>::pack2(hv.p[0], hv.p[1]);
+      dsbu[i] = (int)Elem<T>::pack2(hv.p[0] * hv.dd[0], hv.p[1] * hv.dd[1]);
+      asm volatile("" : "+v"(pbu[i]), "+v"(dsbu[i]));
+    }
+  };
+  // the loaded dS~ chunk u of the tile in stage st (LOAD)
+  auto load_ds = [&](const lds_char_t* st, int u) -> i32x4_t {
+    return *(lds_i32x4_t*)(st + OFF_DS + wave * 2 * ScLayout::CHUNK + u * ScLayout::CHUNK + lane * 16);
   };
   // all 16 values of a tile at once (prologue and last step)
   auto chunk_now = [&](const lds_char_t* st, int u, const f32x16_t& sc, const f32x16_t& dpc, i32x4_t& pbu,
@@ -996,7 +1043,10 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
   };
   auto mfma_slot = [&](int m, i32x4_t op, f32x16_t (&sn)[NQB], f32x16_t (&dpn)[NQB], const i32x4_t (&pb)[2 * NQB],
                        const i32x4_t (&dsb)[2 * NQB]) {
-    if (m < NMA) {
+    if (LOAD && m < NMA) {
+      const int s = m / NQB, qb = m % NQB;
+      sn[qb] = mfma32(op, kreg[s], s == 0 ? zero16 : sn[qb], T());
+    } else if (m < NMA) {
       const int s = m / (2 * NQB), r = m % (2 * NQB), qb = r >> 1;
       if (r & 1) dpn[qb] = mfma32(op, vreg[s], s == 0 ? zero16 : dpn[qb], T());
       else sn[qb] = mfma32(op, kreg[s], s == 0 ? zero16 : sn[qb], T());
@@ -1011,21 +1061,25 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
       }
     }
   };
-  static_assert(NQB == 1 && (NS == 32 || NS == 16), "slot plan below assumes one 32-query block per step");
+  static_assert(NQB == 1 && (NS == 32 || NS == 16 || (LOAD && NS == 24)),
+                "slot plan below assumes one 32-query block per step");
   // Slot plan of step j (P~, dS~ of chunk 0 of tile j arrive computed by the previous step), D = 128:
   //   slots  0..15  S, dP MFMAs of tile j + 1; chunk 1 of tile j: pair i halves at 2 + 3i, 4 + 3i
   //   slots 16..23  dV, dK MFMAs of chunk 0; 24..31 of chunk 1
   //   slots 17..31  chunk 0 of tile j + 1 (S, dP of tile j + 1 complete after slot 15): halves at 17 + 4i, 19 + 4i
   // D = 64 (half the MFMAs, the same values): S, dP in slots 0..7, updates of chunk 0 in 8..11 and of chunk 1
   // in 12..15; chunk 1 of tile j: halves at i, 2 + i; chunk 0 of tile j + 1: halves at 9 + i, 11 + i.
-  constexpr int A1 = NS == 32 ? 2 : 0, AS = NS == 32 ? 3 : 1;
-  constexpr int B1 = NMA + 1, BS = NS == 32 ? 4 : 1;
-  constexpr int STAT_SLOT = NS == 32 ? 12 : 6;  // statistics of tile j + 1 requested here
+  // LOAD (D = 128, P~ only): S in slots 0..7, updates of chunk 0 in 8..15 and of chunk 1 in 16..23; chunk 1 of
+  // tile j: halves at 1 + 2i, 3 + 2i; chunk 0 of tile j + 1: halves at 9 + 3i, 11 + 3i; the loaded dS~ of tile j
+  // read in slot 0.
+  constexpr int A1 = NS == 32 ? 2 : LOAD ? 1 : 0, AS = NS == 32 ? 3 : LOAD ? 2 : 1;
+  constexpr int B1 = NMA + 1, BS = NS == 32 ? 4 : LOAD ? 3 : 1;
+  constexpr int STAT_SLOT = NS == 16 ? 6 : LOAD ? 6 : 12;  // statistics of tile j + 1 requested here
   constexpr int SC_SLOT0 = 14, SC_SLOT1 = 28;   // score stores of tile j (STORE, 32 slots per step)
   auto step = [&](auto kk, int j, const f32x16_t (&sc)[NQB], const f32x16_t (&dpc)[NQB], f32x16_t (&sn)[NQB],
                   f32x16_t (&dpn)[NQB], const i32x4_t& pb0, const i32x4_t& ds0, i32x4_t& pb0n, i32x4_t& ds0n) {
     constexpr int k = decltype(kk)::value;
-    ring_sync<C::LOADS>();  // tile j + 1 has landed (tile j + 2 may be in flight)
+    ring_sync<LOADS>();  // tile j + 1 has landed (tile j + 2 may be in flight)
     pin_offsets();
     const lds_char_t* s_next = stage(IC<k + 1>{});
     const lds_char_t* s_cur = stage(IC<k>{});
@@ -1037,7 +1091,12 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
     for (int m = 0; m < PF; ++m) opr[m] = load_op(s_next, s_cur, m);
     i32x4_t pb[2], dsb[2];
     pb[0] = pb0;
-    dsb[0] = ds0;
+    if constexpr (LOAD) {
+      dsb[0] = load_ds(s_cur, 0);
+      dsb[1] = load_ds(s_cur, 1);
+    } else {
+      dsb[0] = ds0;
+    }
     Half h1[4], hn[4];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1057,8 +1116,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
         if (m == SC_SLOT1) store_chunk(j, 1, dsb[1]);
       }
 #pragma unroll
-      for (int li = 0; li < C::LOADS; ++li) {
-        if (li * NS / C::LOADS == m) issue_load(s_req, j + 3, li);
+      for (int li = 0; li < LOADS; ++li) {
+        if (li * NS / LOADS == m) issue_load(s_req, j + 3, li);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1075,6 +1134,10 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
     pb[0] = pb0;
     dsb[0] = ds0;
     chunk_now(s_cur, 1, sc[0], dpc[0], pb[1], dsb[1]);
+    if constexpr (LOAD) {
+      dsb[0] = load_ds(s_cur, 0);
+      dsb[1] = load_ds(s_cur, 1);
+    }
     if constexpr (STORE) {
       store_chunk(nqt - 1, 0, dsb[0]);
       store_chunk(nqt - 1, 1, dsb[1]);
@@ -1086,12 +1149,12 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_kv_tr_kernel(Bw
 
   if (nqt > 0) {
 #pragma unroll
-    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
+    for (int li = 0; li < LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
 #pragma unroll
-    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
+    for (int li = 0; li < LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
 #pragma unroll
-    for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
-    ring_sync<2 * C::LOADS>();  // K, V rows and tile 0
+    for (int li = 0; li < LOADS; ++li) issue_load(stage(IC<2>{}), 2, li);
+    ring_sync<2 * LOADS>();  // K, V rows and tile 0
     f32x16_t sa[NQB], pa[NQB], sb[NQB], pbb[NQB];
     i32x4_t ca_p, ca_d, cb_p, cb_d;  // chunk-0 packs carried between steps (alternating)
     {

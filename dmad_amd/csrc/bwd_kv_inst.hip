@@ -35,7 +35,13 @@ BwdLaunchFn kv_tr_select<Elt, 128>() {
 // query pass reading it back (the full-derivative half is in bwd_full_inst.hip)
 template <typename T>
 static hipError_t kv_sc_launch(const BwdParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, 128, true>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, 128, kScStore>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+// the full derivative's tangent key pass on the dSd its key pass stored
+template <typename T>
+static hipError_t kv_ld_launch(const BwdParams& p, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_kv_tr_kernel<T, 128, kScLoad>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 template <typename T>
@@ -50,6 +56,10 @@ BwdLaunchFn kv_sc_dout_only<Elt>() {
 template <>
 DqLaunchFn dq_sc_dout_only<Elt>() {
   return &dq_sc1_launch<Elt>;
+}
+template <>
+BwdLaunchFn kv_sc_tangent<Elt>() {
+  return &kv_ld_launch<Elt>;
 }
 
 }  // namespace dmad

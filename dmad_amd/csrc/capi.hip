@@ -309,6 +309,12 @@ dmad::BwdLaunchFn pick_kv_sc(int dtype, bool full) {
   return nullptr;
 }
 
+dmad::BwdLaunchFn pick_kv_sc_tangent(int dtype) {
+  if (dtype == DMAD_BF16) return dmad::kv_sc_tangent<__bf16>();
+  if (dtype == DMAD_F16) return dmad::kv_sc_tangent<_Float16>();
+  return nullptr;
+}
+
 dmad::DqLaunchFn pick_dq_sc(int dtype, bool full) {
   if (dtype == DMAD_BF16) return dmad::dq_sc_select<__bf16>(full);
   if (dtype == DMAD_F16) return dmad::dq_sc_select<_Float16>(full);
@@ -450,6 +456,7 @@ BwdPlan plan_bwd_ws(int dtype, bool full, bool tgrad, int64_t B, int64_t H, int6
   if (pl.sc > 0) {
     pl.kv = full ? "attn_bwd_kv_full_kernel<store>" : "attn_bwd_kv_tr_kernel<store>";
     pl.dq = "attn_bwd_dq_sc_kernel";
+    if (tgrad) pl.kv_t = "attn_bwd_kv_tr_kernel<load>";  // per launch pair, on the stored dSd
     const int64_t npair = ((Lq + 127) / 128 + 1) / 2;  // two 128-query blocks per query-pass workgroup
     pl.grid_kv = (Lk + 127) / 128 * pl.sc;
     pl.grid_dq = npair * pl.sc;
@@ -869,23 +876,32 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
   pq.xcd_order = plan.xcd_dq;
   if (sc > 0) {
     // stored score gradients: per launch pair, the key pass over sc (b, h)
-    // slices writes their dS [, dSd] after the minimum workspace and the query
-    // pass reads them back; main kernels in launch order (key, query) per pair,
-    // then the tangent key pass
+    // slices writes their dS [, dSd] after the minimum workspace, the query
+    // pass reads them back, and with tangent gradients the dO-only key pass on
+    // (dOd, rho) reads the stored dSd for dKd, dVd; main kernels in launch order
     const dmad::BwdLaunchFn fs = pick_kv_sc(dtype, full);
     const dmad::DqLaunchFn fqs = pick_dq_sc(dtype, full);
-    if (fs == nullptr || fqs == nullptr) return fail(DMAD_ERR_UNSUPPORTED, "no stored-score backward kernel");
+    const dmad::BwdLaunchFn fts = tgrad ? pick_kv_sc_tangent(dtype) : nullptr;
+    if (fs == nullptr || fqs == nullptr || (tgrad && fts == nullptr))
+      return fail(DMAD_ERR_UNSUPPORTED, "no stored-score backward kernel");
     const int64_t nkt = (Lk + 127) / 128, nqw = ((Lq + 127) / 128 + 1) / 2;  // query-pass workgroups per slice
     p.sc = ws + w.total;
     p.sc_slice = score_slice_bytes(full, Lq, Lk);
     pq.sc = p.sc;
     pq.sc_slice = p.sc_slice;
+    // tangent key pass: dKd, dVd from (dOd, rho) and the stored dSd (a copy of p
+    // made after the score fields are set: it reads the same slices)
+    dmad::BwdParams pt = p;
+    pt.dout = dto;
+    pt.stats = stats_bt;
+    pt.dk = dtk;
+    pt.dv = dtv;
     pq.sc_nkb = (int)(4 * nkt);
     pq.xcd_order = nqw < dmad::kHeadMajorMinTiles;
     int ev = 0;
     for (int64_t bh0 = 0; bh0 < BH; bh0 += sc) {
       const int64_t n = BH - bh0 < sc ? BH - bh0 : sc;
-      p.bh0 = pq.bh0 = (int)bh0;
+      p.bh0 = pq.bh0 = pt.bh0 = (int)bh0;
       mark(ev, false, s);
       if ((e = fs(p, (int)(n * nkt), s)) != hipSuccess) return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
       mark(ev++, true, s);
@@ -893,21 +909,12 @@ int bwd_impl(int dtype, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D,
       if ((e = fqs(pq, (int)(n * nqw), s)) != hipSuccess)
         return fail(DMAD_ERR_HIP, "backward dq launch: %s", hipGetErrorString(e));
       mark(ev++, true, s);
-    }
-    if (tgrad) {
-      // 128-wide heads: dQd came from the query pass; dKd, dVd from the dO-only
-      // key pass with (dO, D) := (dOd, rho)
-      dmad::BwdParams pt = p;
-      pt.dout = dto;
-      pt.doT = trdto;
-      pt.stats = stats_bt;
-      pt.dk = dtk;
-      pt.dv = dtv;
-      pt.bh0 = 0;
-      mark(ev, false, s);
-      if ((e = fn_a(pt, (int)plan.grid_kv, s)) != hipSuccess)
-        return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
-      mark(ev, true, s);
+      if (tgrad) {
+        mark(ev, false, s);
+        if ((e = fts(pt, (int)(n * nkt), s)) != hipSuccess)
+          return fail(DMAD_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+        mark(ev++, true, s);
+      }
     }
     return ok();
   }
@@ -1063,6 +1070,7 @@ int dmad_attn_bwd_plan_ws(int dtype, int full, int tangent_grads, int64_t B, int
   if (pl.sc > 0) {
     out->kernel = pl.kv;
     out->kernel2 = pl.dq;
+    out->kernel3 = pl.kv_t;
     out->grid = pl.grid_kv;
     out->grid2 = pl.grid_dq;
     out->xcd_order2 = pl.xcd_dq;

@@ -112,6 +112,10 @@ DqLaunchFn dq_sc_dout_only();
 template <> DqLaunchFn dq_sc_dout_only<__bf16>();
 template <> DqLaunchFn dq_sc_dout_only<_Float16>();
 template <typename T>
+BwdLaunchFn kv_sc_tangent();  // attn_bwd_kv_tr_kernel<T, 128, kScLoad>
+template <> BwdLaunchFn kv_sc_tangent<__bf16>();
+template <> BwdLaunchFn kv_sc_tangent<_Float16>();
+template <typename T>
 BwdLaunchFn kv_sc_select(bool full);
 template <> BwdLaunchFn kv_sc_select<__bf16>(bool);
 template <> BwdLaunchFn kv_sc_select<_Float16>(bool);

@@ -228,8 +228,9 @@ typedef struct dmad_plan {
   int32_t transposed_copies; /* operands copied transposed into the workspace before the kernels */
   int64_t workspace_bytes;   /* workspace the call needs */
   int64_t score_slices;      /* backward (dmad_attn_bwd_plan_ws): (b, h) slices per launch pair of the stored-score
-                                passes (`kernel` stores dS [, dSd], `kernel2` reads them back; grids are per pair);
-                                0: the query pass recomputes the scores */
+                                passes (`kernel` stores dS [, dSd], `kernel2` reads them back, `kernel3` with tangent
+                                gradients reads the stored dSd; grids are per pair); 0: the query pass recomputes
+                                the scores */
 } dmad_plan;
 
 /* Plan of dmad_attn_jvp_fwd / dmad_attn_fwd (magi_tasks < 0) or of
@@ -269,8 +270,8 @@ int dmad_attn_bwd_score_bytes(int dtype, int full, int64_t Lq, int64_t Lk, int64
  * passes. Main kernels in order: forward -> {attention}; backward -> {dK/dV
  * pass, dQ pass[, tangent dK/dV pass[, tangent dQ pass]]} (for 128-wide heads
  * the full derivative's dQ pass also gives dQd: no tangent dQ pass); a
- * backward on stored score gradients -> {dK/dV pass, dQ pass} once per launch
- * pair, then [tangent dK/dV pass]. Kernels without a pair of events are not
+ * backward on stored score gradients -> {dK/dV pass, dQ pass[, tangent dK/dV
+ * pass]} once per launch pair. Kernels without a pair of events are not
  * timed. count <= 256; count = 0 (events may be NULL) stops.
  */
 int dmad_set_kernel_events(void* const* events, int count);
