@@ -158,14 +158,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   }
 
   // everything in VGPRs (no AGPRs: 256 per lane at two waves per SIMD); the
-  // accumulators take 128 of them
+  // accumulators take 128 of them. Step 0 starts them (its first 16-key
+  // chunk's MFMAs take a zero C operand), so they need no clearing.
   f32x16_t oacc[DB], cacc[DB];
   const f32x16_t zero16 = {};
-#pragma unroll
-  for (int d = 0; d < DB; ++d) {
-    oacc[d] = zero16;
-    cacc[d] = zero16;
-  }
   float m_i = -__builtin_inff(), l_i = 0.f, r_i = 0.f;
 
   // Online softmax of one tile (log2 domain; lanes l and l^32 share a query):
@@ -177,7 +173,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   // the compiler would otherwise sink them to the end of the step and keep all
   // 32 values live.
   float neg_m = 0.f;
-  auto soft_head = [&](const f32x16_t& sc) -> float {
+  auto soft_head = [&](const f32x16_t& sc, auto first) -> float {
     float a = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     float b2 = fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]));
     float c2 = fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11]));
@@ -189,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
     const float alpha = fast_exp2(m_i - m_new);
     m_i = m_new;
     neg_m = -m_new;
-    if (moved) {  // rare with the slack
+    if (!decltype(first)::value && moved) {  // rare with the slack; nothing to rescale at step 0
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -219,8 +215,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   constexpr int PFA = 2;  // phase-A operand pairs (K slice, Qd slice) read ahead
   constexpr int NB = 2 * DB;
   constexpr int PFB = 4;  // phase-B operands read ahead (the first ones during the softmax)
-  // step i: tile i sits in stage kk % 3
-  auto step = [&](auto kk, int i) {
+  // step i: tile i sits in stage kk % 3 (first: step 0, which starts the accumulators)
+  auto step = [&](auto kk, int i, auto first) {
+    constexpr bool FIRST = decltype(first)::value;
     ring_sync<C::LOADS>();  // tile i has landed (tile i+1 may be in flight); all waves are past step i-1
     asm volatile("" : "+v"(kx0), "+v"(qx0), "+v"(tx0[0]), "+v"(tx0[1]));
     const lds_char_t* s_cur = stage(kk);
@@ -277,7 +274,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
     // softmax of the first 16-key chunk (two pairs per scheduling group)
     i32x4_t pk[2], hk[2];
     float ls = 0.f, rs = 0.f;
-    const float alpha = soft_head(sc);
+    const float alpha = soft_head(sc, first);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int v = 0; v < 8; v += 2) {
@@ -292,8 +289,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
       const int t = j / DB, db = j % DB;
       const i32x4_t a = vb[j % PFB];
       if (j + PFB < NB) vb[j % PFB] = load_vt(j + PFB);
-      oacc[db] = mfma32(a, pk[t], oacc[db], T());
-      cacc[db] = mfma32(a, hk[t], cacc[db], T());
+      oacc[db] = mfma32(a, pk[t], (FIRST && t == 0) ? zero16 : oacc[db], T());
+      cacc[db] = mfma32(a, hk[t], (FIRST && t == 0) ? zero16 : cacc[db], T());
       if (j < DB) soft_pair(8 + 2 * j, sc, tc, pk, hk, ls, rs);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -308,14 +305,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<0>{}), 0, li);
 #pragma unroll
   for (int li = 0; li < C::LOADS; ++li) issue_load(stage(IC<1>{}), 1, li);
-  int i = 0;
+  step(IC<0>{}, 0, IC<1>{});  // ntiles >= 1
+  int i = 1;
   for (; i + 3 <= ntiles; i += 3) {
-    step(IC<0>{}, i);
-    step(IC<1>{}, i + 1);
-    step(IC<2>{}, i + 2);
+    step(IC<1>{}, i, IC<0>{});
+    step(IC<2>{}, i + 1, IC<0>{});
+    step(IC<3>{}, i + 2, IC<0>{});
   }
-  if (i < ntiles) step(IC<0>{}, i);
-  if (i + 1 < ntiles) step(IC<1>{}, i + 1);
+  if (i < ntiles) step(IC<1>{}, i, IC<0>{});
+  if (i + 1 < ntiles) step(IC<2>{}, i + 1, IC<0>{});
   wait_vmem();  // no request beyond the last tile stays in flight
 
   // ---- epilogue: lane (query col, half) holds d = 32 db + 8 jj + 4 half + (0..3)
