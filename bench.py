@@ -1,10 +1,11 @@
 #!/usr/bin/env python3
 """Benchmark of the flash-attention JVP path on one MI355X.
 
-One step = one Wan2.1-14B DiT layer's attention work on the JVP path:
+One step = one Wan2.1-14B DiT layer's attention work on the JVP path, in the layer's order
+(self-attention, then text cross-attention, forward; then the self-attention backward):
   * self-attention forward + JVP     B=1, H=40, L=32760, D=128, bf16   (12 L^2 D H flop)
-  * self-attention backward, dO only (what the reference computes)       (10 L^2 D H flop)
   * text cross-attention forward + JVP, Lq=32760 over 512 keys, Kd=Vd=0  (8 Lq Lk D H flop)
+  * self-attention backward, dO only (what the reference computes)       (10 L^2 D H flop)
 Inputs are resident in HBM before timing starts (synthetic, seeded: Q, K RMS-normalised
 over H*D and rotated by 3D RoPE on the 21x30x52 latent grid, V ~ N(0,1), tangents
 ~ N(0, 0.1^2), dO ~ N(0,1)).
@@ -483,14 +484,14 @@ def main():
             timers.append((tf, tb, tc))
             with tf:
                 o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
-            with tb:
-                jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
             with tc:
                 jvp_attention_forward(q, kc, vc, tq, None, None, s)
+            with tb:
+                jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
         else:
             o, to, lse, mu = jvp_attention_forward(q, k, v, tq, tk, tv, s)
-            jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
             jvp_attention_forward(q, kc, vc, tq, None, None, s)
+            jvp_attention_backward(q, k, v, None, None, None, o, None, lse, None, do, None, s, False)
 
     for _ in range(args.warmup):
         step(False)
