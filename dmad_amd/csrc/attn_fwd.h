@@ -156,13 +156,27 @@ __device__ void magi_store_empty(const FwdParams& p, int bh, const MagiTask& t, 
   }
 }
 
-// Rescale threshold (log2 units): the running max used for exp2 only moves when
-// a row's tile max exceeds it by more than this, so the accumulators are
-// rescaled only on those (rare) steps and P~ <= 2^8. bf16 shares fp32's
-// exponent range; fp16 keeps the exact running max (P~ <= 1, H~ bounded as in
-// the reference) so nothing new can overflow.
-template <typename T> struct RescaleSlack { static constexpr float value = 8.0f; };
-template <> struct RescaleSlack<_Float16> { static constexpr float value = 0.0f; };
+// Lazy rescale (log2 units): the running max m only moves when a row's tile
+// max exceeds it by more than `value`, so the accumulators are rescaled only
+// on those steps, and P~ = exp2(x - m - offset). bf16 shares fp32's exponent
+// range: offset 0, P~ <= 2^8. fp16 subtracts offset = value, so P~ <= 1 and
+// H~ = P~ s Sd stay within the reference's bounds (its P~ <= 1 with the exact
+// max) and nothing new can overflow; l, r and the accumulators all carry the
+// same factor, which cancels in O, Od and mu, and LSE adds the offset back.
+template <typename T> struct RescaleSlack {
+  static constexpr float value = 8.0f;
+  static constexpr float offset = 0.0f;
+};
+template <> struct RescaleSlack<_Float16> {
+  static constexpr float value = 4.0f;
+  static constexpr float offset = 4.0f;
+};
+// m + offset (m itself when the offset is 0, bit for bit)
+template <typename T>
+__device__ __forceinline__ float exp_base(float m) {
+  if constexpr (RescaleSlack<T>::offset != 0.0f) return m + RescaleSlack<T>::offset;
+  else return m;
+}
 
 template <int DQK, int DV, int MODE>
 struct FwdCfg {
@@ -375,7 +389,7 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
     const float m_new = moved ? fmaxf(m_i, mx) : m_i;
     const float alpha = fast_exp2(m_i - m_new);
     m_i = m_new;
-    const float neg_m = -m_new;
+    const float neg_m = -exp_base<T>(m_new);
     float pv[8], hv[8], ls = 0.f, rs = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -505,7 +519,7 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(FwdParams p) {
   }
   if (grp == 0 && qrow < p.Lq) {
     const int64_t si = (int64_t)bh * p.Lq + qrow;
-    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    p.lse[si] = (exp_base<T>(m_i) + __builtin_log2f(l)) * 0.6931471805599453f;
     if constexpr (C::JVP) p.mu[si] = mu;
   }
 }
@@ -708,7 +722,7 @@ __global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
       const float m_new = sm.moved ? fmaxf(m_i, sm.mx) : m_i;
       sm.alpha = fast_exp2(m_i - m_new);
       m_i = m_new;
-      sm.neg_m = -m_new;
+      sm.neg_m = -exp_base<T>(m_new);
     } else if (u < 11) {
       const int e = u - 3, sb = e >> 2, v = e & 3;
       sm.pv[e & 1] = fast_exp2(fmaf(sc[sb][v], p.scale_log2, sm.neg_m));
@@ -861,7 +875,7 @@ __global__ __launch_bounds__(512) void attn_fwd_stream_kernel(FwdParams p) {
   }
   if (grp == 0 && qrow < p.Lq) {
     const int64_t si = (int64_t)bh * p.Lq + qrow;
-    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    p.lse[si] = (exp_base<T>(m_i) + __builtin_log2f(l)) * 0.6931471805599453f;
     if constexpr (C::JVP) p.mu[si] = mu;
   }
 }

@@ -428,7 +428,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
       const float m_new = sm.moved ? fmaxf(m_i, sm.mx) : m_i;
       sm.alpha = fast_exp2(m_i - m_new);
       m_i = m_new;
-      sm.neg_m = -m_new;
+      sm.neg_m = -exp_base<T>(m_new);
     } else {
       const int v = u - 2;
       const float pe = fast_exp2(fmaf(sc[v], p.scale_log2, sm.neg_m));
@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // every chunk's workgroup holds the same statistics; chunk 0 stores them
   if (half == 0 && query < p.Lq && keep && chunk == 0) {
     const int64_t si = (int64_t)bh * p.Lq + query;
-    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    p.lse[si] = (exp_base<T>(m_i) + __builtin_log2f(l)) * 0.6931471805599453f;
     if constexpr (C::JVP) p.mu[si] = mu;
   }
 }

@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
     const float m_new = moved ? fmaxf(m_i, mx) : m_i;
     const float alpha = fast_exp2(m_i - m_new);
     m_i = m_new;
-    neg_m = -m_new;
+    neg_m = -exp_base<T>(m_new);
     if (!decltype(first)::value && moved) {  // rare with the slack; nothing to rescale at step 0
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   }
   if (half == 0 && query < p.Lq) {
     const int64_t si = (int64_t)bh * p.Lq + query;
-    p.lse[si] = (m_i + __builtin_log2f(l)) * 0.6931471805599453f;
+    p.lse[si] = (exp_base<T>(m_i) + __builtin_log2f(l)) * 0.6931471805599453f;
     p.mu[si] = mu;
   }
 }

@@ -102,8 +102,8 @@ def _growing_logits(g, B, H, Lq, Lk, D, dtype, rise):
                                             (900, 128, "jvp", 10.0), (640, 64, "jvp", 10.0)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_rescale_at_every_step(gpu, Lk, D, mode, rise, dtype):
-    """Logits rising along the keys: every tile moves the running max beyond the slack (bf16 2^8,
-    fp16 exact), exercising the accumulator rescale on each kernel (two-workgroups-per-CU for
+    """Logits rising along the keys: every tile moves the running max beyond the slack (2^8 for
+    bf16, 2^4 for fp16), exercising the accumulator rescale on each kernel (two-workgroups-per-CU for
     Kd = Vd = 0 up to 2048 keys, the row kernels otherwise)."""
     from dmad_amd.jvp_attention import jvp_attention_forward
 
