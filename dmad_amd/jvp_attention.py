@@ -104,9 +104,11 @@ def set_backward_mode(mode: str) -> None:
 # call and on top of its minimum workspace, for stored score gradients: its key
 # pass then writes dS (and dSd) and the query pass reads them back instead of
 # recomputing the scores, up to as many (b, h) slices per launch pair as fit. 0
-# turns the path off. Environment default: DMAD_BWD_SCORE_BUDGET_MB (18 GiB: eight
-# dO-only or four full-derivative slices of a Wan2.1-14B layer, 2.15 / 4.3 GB each).
-_SCORE_BUDGET = int(os.environ.get("DMAD_BWD_SCORE_BUDGET_MB", "18432")) << 20
+# turns the path off. Environment default: DMAD_BWD_SCORE_BUDGET_MB (36 GiB, an eighth
+# of an MI355X's HBM: sixteen dO-only or eight full-derivative slices of a Wan2.1-14B
+# layer at 480p, 2.15 / 4.3 GB each, or three dO-only slices at 720p, 11.5 GB each;
+# 18 GiB held only one 720p slice, too few key-pass workgroups for a launch pair).
+_SCORE_BUDGET = int(os.environ.get("DMAD_BWD_SCORE_BUDGET_MB", "36864")) << 20
 
 
 def set_backward_score_budget(nbytes: int) -> None:
