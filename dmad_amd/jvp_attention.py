@@ -151,6 +151,21 @@ def _score_bytes(code: int, full: bool, B: int, H: int, Lq: int, Lk: int, D: int
     return n * one
 
 
+def _backward_workspace(code: int, ws_mode: int, B: int, H: int, Lq: int, Lk: int, D: int, device):
+    """(pointer, size, owner) of a backward's workspace: the minimum plus the stored score
+    gradients the budget allows. The stored scores only save time, so when the device cannot
+    hold them the call takes the minimum and the query pass recomputes the scores (the same
+    dQ bit for bit); an allocation failure of the minimum itself propagates."""
+    base = nat.bwd_workspace_bytes_of(code, ws_mode, B, H, Lq, Lk, D)
+    extra = _score_bytes(code, ws_mode > 0, B, H, Lq, Lk, D)
+    if extra > 0:
+        try:
+            return nat.workspace(base + extra, device)
+        except torch.cuda.OutOfMemoryError:
+            pass
+    return nat.workspace(base, device)
+
+
 def _score_slices(bh: int, n_max: int, Lq: int, Lk: int) -> int:
     """(b, h) slices per launch pair, at most n_max: the count whose pairs fill the 256 CUs
     best. A pair of n slices runs n * key tiles key-pass workgroups and n * query-block
@@ -436,8 +451,7 @@ def jvp_attention_backward(q, k, v, tq, tk, tv, o, to, lse, mu, dout, dto, sm_sc
     dtv = torch.empty_like(dv) if tgrads else None
     lib = nat.lib()
     ws_mode = (2 if tgrads else 1) if full else 0
-    ws_bytes = nat.bwd_workspace_bytes_of(code, ws_mode, B, H, Lq, Lk, D) + _score_bytes(code, full, B, H, Lq, Lk, D)
-    ws_ptr, ws_size, ws = nat.workspace(ws_bytes, q.device)
+    ws_ptr, ws_size, ws = _backward_workspace(code, ws_mode, B, H, Lq, Lk, D, q.device)
     nat.check(
         lib.dmad_attn_jvp_bwd(
             code, B, H, Lq, Lk, D,

@@ -9,6 +9,7 @@ dim, fp32, the block-sparse forward, the backward passes, the workspace sizes (e
 workspace queries) and the argument checks.
 """
 import pytest
+import torch
 
 from dmad_amd import _native as nat
 
@@ -283,3 +284,34 @@ def test_python_score_budget():
             ja.set_backward_score_budget(-1)
     finally:
         ja.set_backward_score_budget(old)
+
+
+def test_backward_workspace_falls_back_to_the_minimum(monkeypatch):
+    """The stored score gradients are a speed-up: when the device cannot hold them the
+    backward takes its minimum workspace (the recomputing query pass); a failure to
+    allocate the minimum itself is not hidden."""
+    from dmad_amd import jvp_attention as ja
+
+    base = nat.bwd_workspace_bytes_of(BF16, 0, 1, 40, 32760, 32760, 128)
+    extra = ja._score_bytes(BF16, False, 1, 40, 32760, 32760, 128)
+    assert extra > 0
+    asked = []
+
+    def fake_workspace(nbytes, device, limit=base):
+        asked.append(nbytes)
+        if nbytes > limit:
+            raise torch.cuda.OutOfMemoryError("no room")
+        return 1 << 20, nbytes, object()
+
+    monkeypatch.setattr(ja.nat, "workspace", fake_workspace)
+    ptr, size, owner = ja._backward_workspace(BF16, 0, 1, 40, 32760, 32760, 128, "cpu")
+    assert asked == [base + extra, base] and size == base
+    # with room for both, one allocation of the whole
+    asked.clear()
+    monkeypatch.setattr(ja.nat, "workspace", lambda n, d: fake_workspace(n, d, limit=1 << 50))
+    assert ja._backward_workspace(BF16, 0, 1, 40, 32760, 32760, 128, "cpu")[1] == base + extra
+    assert asked == [base + extra]
+    # the minimum itself failing propagates
+    monkeypatch.setattr(ja.nat, "workspace", lambda n, d: fake_workspace(n, d, limit=0))
+    with pytest.raises(torch.cuda.OutOfMemoryError):
+        ja._backward_workspace(BF16, 0, 1, 40, 32760, 32760, 128, "cpu")
