@@ -140,6 +140,12 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   constexpr int DVC = C::DVC, CRV = C::CRV, ROWBV = C::ROWBV, NSTAGE = C::NSTAGE;
   constexpr int NOPA = C::NOPA, NOPB = C::NOPB, NOP = NOPA + NOPB, PF = 4;
   constexpr float kSlack = RescaleSlack<T>::value;
+  // Without Kd, Vd (C~ = V^T H~ alone) and in bf16 (fp32's range), H~ = P~ Sd
+  // is formed without the softmax scale, which the epilogue applies to C~ and
+  // to r once per row: one multiply per score value fewer. fp16, whose range
+  // the unscaled H~ could leave, and the full JVP (C~ also sums Vd^T P~) keep
+  // the reference's H~ = P~ (s Sd).
+  constexpr bool kHScaled = C::KVT || !std::is_same<T, __bf16>::value;
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
@@ -435,7 +441,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
       sm.ls += pe;
       float he = 0.f;
       if constexpr (C::JVP) {
-        he = pe * (tc[v] * p.scale);
+        he = kHScaled ? pe * (tc[v] * p.scale) : pe * tc[v];
         sm.rs += he;
       }
       if (v & 1) {
@@ -635,8 +641,9 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
   // ---- epilogue: lane (query col, half) holds d = 32 db + 8 jj + 4 half + (0..3)
   const float l = l_i + other_half(l_i);
   const float inv_l = 1.0f / l;
+  const float inv_lh = kHScaled ? inv_l : inv_l * p.scale;  // 1 / l, with the scale H~ left out
   float mu = 0.f;
-  if constexpr (C::JVP) mu = (r_i + other_half(r_i)) * inv_l;
+  if constexpr (C::JVP) mu = (r_i + other_half(r_i)) * inv_lh;
   // O (Od) resources start at this workgroup's column chunk
   const int64_t obase = b * p.o_sb + h * p.o_sh + chunk * DVC;
   const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + DVC) * 2);
@@ -664,7 +671,7 @@ __global__ __launch_bounds__(256, DH == 64 ? (MODE == kFwdPlain && !MAGI ? 4 : 2
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         ov[e] = oacc[d][4 * jj + e] * inv_l;
-        if constexpr (C::JVP) tv[e] = cacc[d][4 * jj + e] * inv_l - mu * ov[e];
+        if constexpr (C::JVP) tv[e] = cacc[d][4 * jj + e] * inv_lh - mu * ov[e];
       }
       stage_put<DVC>(region, col, half, d, jj, u32x2_t{Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])});
       if constexpr (C::JVP)

@@ -66,6 +66,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   using C = Fwd32X2Cfg;
   constexpr int D = C::D, BN = C::BN, KS = C::KS, DB = C::DB, CR = C::CR, ROWB = C::ROWB;
   constexpr float kSlack = RescaleSlack<T>::value;
+  // bf16 forms H~ = P~ Sd without the softmax scale and applies it to C~ and r
+  // in the epilogue, as attn_fwd32_kernel does in this mode (the same bits)
+  constexpr bool kHScaled = !std::is_same<T, __bf16>::value;
   __shared__ __attribute__((aligned(1024))) char stg0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char stg2[C::STAGE];
@@ -202,10 +205,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
     const float p0 = fast_exp2(fmaf(sc[v], p.scale_log2, neg_m));
     const float p1 = fast_exp2(fmaf(sc[v + 1], p.scale_log2, neg_m));
     ls += p0;
-    const float h0 = p0 * (tc[v] * p.scale);
+    const float h0 = kHScaled ? p0 * (tc[v] * p.scale) : p0 * tc[v];
     rs += h0;
     ls += p1;
-    const float h1 = p1 * (tc[v + 1] * p.scale);
+    const float h1 = kHScaled ? p1 * (tc[v + 1] * p.scale) : p1 * tc[v + 1];
     rs += h1;
     pk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(p0, p1);
     hk[v >> 3][(v & 7) >> 1] = (int)Elem<T>::pack2(h0, h1);
@@ -319,7 +322,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
   // ---- epilogue: lane (query col, half) holds d = 32 db + 8 jj + 4 half + (0..3)
   const float l = l_i + other_half(l_i);
   const float inv_l = 1.0f / l;
-  const float mu = (r_i + other_half(r_i)) * inv_l;
+  const float inv_lh = kHScaled ? inv_l : inv_l * p.scale;  // 1 / l, with the scale H~ left out
+  const float mu = (r_i + other_half(r_i)) * inv_lh;
   const int64_t obase = b * p.o_sb + h * p.o_sh;
   const uint32_t o_bytes = (uint32_t)(((int64_t)(p.Lq - 1) * p.o_sl + D) * 2);
   const __amdgpu_buffer_rsrc_t ro = make_rsrc((char*)p.o + obase * 2, o_bytes);
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd32_x2_kernel(FwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         ov[e] = oacc[d][4 * jj + e] * inv_l;
-        tv[e] = cacc[d][4 * jj + e] * inv_l - mu * ov[e];
+        tv[e] = cacc[d][4 * jj + e] * inv_lh - mu * ov[e];
       }
       stage_put<D>(ostage, col, half, d, jj, u32x2_t{Elem<T>::pack2(ov[0], ov[1]), Elem<T>::pack2(ov[2], ov[3])});
       stage_put<D>(tstage, col, half, d, jj, u32x2_t{Elem<T>::pack2(tv[0], tv[1]), Elem<T>::pack2(tv[2], tv[3])});
