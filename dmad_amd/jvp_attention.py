@@ -14,7 +14,10 @@ torch's current stream. There is no CPU or PyTorch fallback.
 
 Differences from the reference, all additive:
   * ``tk``/``tv`` may be ``None`` (tangents of K and V known to be zero, as in
-    Wan cross-attention): the forward then skips the two GEMMs they feed.
+    Wan cross-attention): the forward then skips the two GEMMs they feed. O is
+    the same bit for bit as with zero tangents; in bf16 ``to`` differs from the
+    zero-tangent result by the rounding of P~ * Sd (formed without the softmax
+    scale, which is applied once per row), as close to the exact value.
   * backward (``backward_mode`` for a scope, ``set_backward_mode`` for the
     process default): by default the reference's dO-only
     gradients, with the reference's saved tensors (q, k, v, o, LSE; the
